@@ -1,0 +1,114 @@
+// Device layer: Buffer identity, kernel arguments, compiled programs and the
+// device interface that backends implement (src/device.rs:96-354).
+//
+// The reference trait compiles a source string with no launch geometry
+// (device.rs:309-314) and hard-codes the clang renderer at the call site
+// (tensor.rs:850). Here each device owns its lowering: `optimize` runs the
+// device's kernel passes on a rangeified kernel, `render` produces source plus
+// launch geometry, and `compile`/`execute` mirror the reference trait.
+#pragma once
+
+#include <functional>
+#include <memory>
+#include <string>
+#include <vector>
+
+#include "ir.hpp"
+
+namespace fg {
+
+class Device;
+
+struct BufferInner {
+  size_t id = 0;
+  DeviceId device = DeviceId::Hip;
+  DType dtype;
+  size_t numel = 0;
+  void* storage = nullptr;  // device pointer for HIP, host pointer for CPU
+  bool realized = false;
+  // Holds the zeros `allocate` produced and nothing has written it since
+  // (allocation contract: device.rs:282, cpu.rs:277-280).
+  bool known_zero = false;
+  size_t nbytes() const { return dtype.size_bytes() * numel; }
+  bool is_realized() const { return realized; }
+  void ensure_allocated();  // device.rs:191-213
+  ~BufferInner();
+};
+
+size_t next_buffer_id();
+
+// device.rs:242-251
+struct KernelArg {
+  enum class Kind : uint8_t { Buffer, I32, F32, Bool } kind = Kind::I32;
+  Buffer buffer;
+  int32_t i = 0;
+  float f = 0.f;
+  bool b = false;
+  static KernelArg buf(const Buffer& x) { KernelArg a; a.kind = Kind::Buffer; a.buffer = x; return a; }
+  static KernelArg i32(int32_t x) { KernelArg a; a.kind = Kind::I32; a.i = x; return a; }
+  static KernelArg f32(float x) { KernelArg a; a.kind = Kind::F32; a.f = x; return a; }
+  static KernelArg boolean(bool x) { KernelArg a; a.kind = Kind::Bool; a.b = x; return a; }
+};
+
+// What a renderer hands to `Device::compile`: the source and everything the
+// launch needs that the reference's `compile(source, name, num_args)` lacks.
+struct RenderedKernel {
+  std::string source;
+  std::string name;
+  unsigned grid[3] = {1, 1, 1};
+  unsigned block[3] = {1, 1, 1};
+  unsigned lds_bytes = 0;
+  std::string kind;  // lowering class, for debug output and tests
+  std::vector<std::pair<int, DType>> params;  // (slot, dtype) in launch order
+};
+
+struct Program {
+  virtual ~Program() = default;
+  size_t num_args = 0;
+  RenderedKernel meta;
+};
+
+class Device {
+ public:
+  virtual ~Device() = default;
+  virtual DeviceId id() const = 0;
+
+  // device.rs:280 — identity only, no storage.
+  Buffer reserve_buffer(DType dtype, size_t numel);
+  // device.rs:283 — zero-initialised storage.
+  virtual Buffer allocate(DType dtype, size_t numel) = 0;
+  // Give a reserved buffer storage. `zero` asks for zero-filled memory; kernel
+  // outputs that overwrite every element pass false.
+  virtual void realize_storage(BufferInner& b, bool zero) = 0;
+  virtual void release(BufferInner& b) = 0;
+  virtual void copy_from_host(const Buffer& b, const void* src, size_t nbytes) = 0;
+  virtual std::vector<uint8_t> copy_to_host(const Buffer& b) = 0;
+
+  // Kernel pipeline after rangeify.
+  virtual UOp optimize(const UOp& rangeified) = 0;
+  virtual RenderedKernel render(const UOp& optimized, const std::string& name) = 0;
+  virtual std::shared_ptr<Program> compile(const RenderedKernel& rk, size_t num_args) = 0;
+  virtual void execute(Program& p, std::vector<KernelArg>& args) = 0;
+  virtual void synchronize() {}
+  // Whether schedule-time value-preserving fusion (shared elementwise
+  // subexpressions inlined into one kernel, zero buffers folded) is enabled.
+  virtual bool fuse_elementwise() const { return false; }
+
+  // device.rs:323-327
+  std::shared_ptr<Program> cached_program(const UOp& sink);
+  void insert_program(const UOp& sink, std::shared_ptr<Program> p);
+  void clear_for_tests();
+  size_t cache_size() const { return programs_.size(); }
+
+ protected:
+  UOpMap<std::shared_ptr<Program>> programs_;
+};
+
+// Registry (device.rs:334-354). The HIP device is built in; the CPU device is
+// provided by the test oracle, which registers itself at load time.
+Device& get_device(DeviceId id);
+bool has_device(DeviceId id);
+void register_device(DeviceId id, Device* dev);
+Device* make_hip_device();
+
+}  // namespace fg

@@ -1,0 +1,1151 @@
+// gfx950 lowering and HIP codegen for rangeified kernels.
+//
+// The reference lowers every kernel to nested scalar C loops (upcast/unroll in
+// src/optimize/, expand.rs, devectorize.rs, linearize.rs, codegen/clang.rs).
+// Here a kernel is classified and rendered as one of:
+//   Gemm          Reduce(Add, Mul(Load A, Load B)) over one range with affine
+//                 operand indexes (the pattern nn::Linear and its gradients
+//                 produce): fp32 MFMA 32x32x2 tiles, LDS double buffering,
+//                 XCD-aware tile order, the rest of the kernel as epilogue.
+//   Elementwise   no reduction: one thread per 4 consecutive outputs,
+//                 16-byte loads/stores where the index is unit-stride.
+//   RowReduce     threads of a group split the innermost reduce range
+//                 (unit-stride loads), then a wave64 DPP/ds_swizzle tree and
+//                 an LDS step across waves.
+//   ColumnReduce  threads own outputs along the unit-stride output range and
+//                 split the reduce range; partials combine through LDS.
+//   Serial        one thread per output, reductions as serial loops in the
+//                 reference's exact order (REDUCE x UNROLL(4) left fold,
+//                 devectorize.rs:206-214, 274-347) — bit-identical to the CPU.
+#include "gpu_lower.hpp"
+
+#include <algorithm>
+#include <charconv>
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <functional>
+#include <map>
+#include <set>
+#include <sstream>
+
+namespace fg {
+
+// ── affine index analysis ───────────────────────────────────────────────────
+int64_t Affine::coef(const UOp& t) const {
+  for (auto& p : terms)
+    if (p.first == t) return p.second;
+  return 0;
+}
+
+bool Affine::has_scalar_terms() const {
+  for (auto& p : terms)
+    if (p.first.op() == Op::ParamScalar && p.second != 0) return true;
+  return false;
+}
+
+static void affine_rec(const UOp& e, int64_t mul, Affine& out) {
+  if (!out.ok) return;
+  switch (e.op()) {
+    case Op::Const:
+      if (e.arg().kind == Arg::Kind::Int) out.c0 += mul * e.arg().a;
+      else out.ok = false;
+      return;
+    case Op::Range:
+    case Op::ParamScalar: {
+      for (auto& p : out.terms)
+        if (p.first == e) {
+          p.second += mul;
+          return;
+        }
+      out.terms.emplace_back(e, mul);
+      return;
+    }
+    case Op::Add:
+      affine_rec(e.src(0), mul, out);
+      affine_rec(e.src(1), mul, out);
+      return;
+    case Op::Mul:
+      if (e.src(1).op() == Op::Const && e.src(1).arg().kind == Arg::Kind::Int) {
+        affine_rec(e.src(0), mul * e.src(1).arg().a, out);
+      } else if (e.src(0).op() == Op::Const && e.src(0).arg().kind == Arg::Kind::Int) {
+        affine_rec(e.src(1), mul * e.src(0).arg().a, out);
+      } else {
+        out.ok = false;
+      }
+      return;
+    default:
+      out.ok = false;
+  }
+}
+
+Affine affine_of(const UOp& e) {
+  Affine a;
+  affine_rec(e, 1, a);
+  return a;
+}
+
+int64_t range_extent(const UOp& r) {
+  FG_CHECK(r.op() == Op::Range && !r.srcs().empty() && r.src(0).arg().kind == Arg::Kind::Int,
+           "range bound must be a constant");
+  return r.src(0).arg().a;
+}
+
+const char* kernel_class_name(KernelClass k) {
+  switch (k) {
+    case KernelClass::Gemm: return "gemm_mfma_f32";
+    case KernelClass::Elementwise: return "elementwise";
+    case KernelClass::RowReduce: return "row_reduce";
+    case KernelClass::ColumnReduce: return "column_reduce";
+    case KernelClass::Serial: return "serial";
+  }
+  return "?";
+}
+
+KernelInfo analyze_kernel(const UOp& sink) {
+  FG_CHECK(sink.op() == Op::Sink && sink.srcs().size() == 1, "kernel must be Sink(one effect)");
+  KernelInfo ki;
+  UOp n = sink.src(0);
+  while (n.op() == Op::End) {
+    FG_CHECK(n.srcs().size() == 2, "output loop End must carry exactly one body");
+    ki.out_ranges.push_back(n.src(0));
+    ki.out_ext.push_back(range_extent(n.src(0)));
+    n = n.src(1);
+  }
+  FG_CHECK(n.op() == Op::Store, "kernel body must be a Store");
+  ki.store = n;
+  const UOp& idx = n.src(0);
+  FG_CHECK(idx.op() == Op::Index && idx.srcs().size() == 2, "store target must be Index(param, flat)");
+  ki.out_param = idx.src(0);
+  FG_CHECK(ki.out_param.op() == Op::ParamBuffer, "store target must be a kernel buffer parameter");
+  ki.out_index = idx.src(1);
+  ki.value = n.src(1);
+  for (auto& x : ki.value.toposort())
+    if (x.op() == Op::Reduce) ki.reduces.push_back(x);
+  std::map<int, UOp> ps;
+  for (auto& x : sink.toposort())
+    if (x.op() == Op::ParamBuffer || x.op() == Op::ParamScalar) ps[static_cast<int>(x.arg().a)] = x;
+  for (auto& p : ps) ki.params.emplace_back(p.first, p.second);
+  return ki;
+}
+
+// ── optimize: symbolic + size-1 reduce ranges ───────────────────────────────
+UOp gpu_optimize(const UOp& rangeified) {
+  UOp k = graph_rewrite(rangeified, symbolic_simple);
+  // A reduce range of extent 1 iterates once at index 0: substitute 0 and
+  // drop it from the Reduce (the accumulation itself is kept).
+  auto drop_unit = [](const UOp& n) -> UOp {
+    if (n.op() != Op::Reduce) return UOp();
+    std::vector<UOp> keep;
+    UOpMap<UOp> sub;
+    for (size_t i = 1; i < n.srcs().size(); i++) {
+      const UOp& r = n.src(i);
+      if (r.op() == Op::Range && range_extent(r) == 1) sub[r] = UOp::const_int(0, DType::I32(), r.device());
+      else keep.push_back(r);
+    }
+    if (sub.empty()) return UOp();
+    std::vector<UOp> srcs{substitute_with_map(n.src(0), sub)};
+    srcs.insert(srcs.end(), keep.begin(), keep.end());
+    return UOp::make_new(Op::Reduce, n.dtype(), srcs, n.arg());
+  };
+  k = graph_rewrite(k, drop_unit);
+  k = graph_rewrite(k, symbolic_simple);
+  // Output ranges map to the launch grid: retag LOOP as GLOBAL.
+  auto retag = [](const UOp& n) -> UOp {
+    if (n.op() != Op::Range || n.arg().range_kind() != AxisKind::Loop) return UOp();
+    return UOp::make_new(Op::Range, n.dtype(), n.srcs(), Arg::range(n.arg().a, AxisKind::Global));
+  };
+  return graph_rewrite(k, retag);
+}
+
+// ── rendering helpers ───────────────────────────────────────────────────────
+namespace {
+
+const char* ctype(DType d) {
+  switch (d.kind) {
+    case DTypeKind::F32: return "float";
+    case DTypeKind::I32: return "int";
+    case DTypeKind::Bool: return "bool";
+    default: return "void";
+  }
+}
+
+// Float literals use the text the reference emits (clang.rs:93-115): the
+// shortest round-trip decimal of the f64 value with an `f` suffix, so both
+// compilers round the same decimal to f32.
+std::string float_lit(double v) {
+  if (std::isinf(v)) return v > 0 ? "__builtin_inff()" : "(-__builtin_inff())";
+  if (std::isnan(v)) return "__builtin_nanf(\"\")";
+  char buf[64];
+  auto r = std::to_chars(buf, buf + sizeof(buf), v);
+  std::string s(buf, r.ptr);
+  if (s.find_first_of(".eE") == std::string::npos) s += ".0";
+  return s + "f";
+}
+
+std::string const_lit(const UOp& c) {
+  const Arg& a = c.arg();
+  switch (a.kind) {
+    case Arg::Kind::Float:
+      if (c.dtype().kind == DTypeKind::F32) return float_lit(a.f);
+      if (c.dtype().kind == DTypeKind::I32) return std::to_string(static_cast<int64_t>(a.f));
+      return a.f != 0.0 ? "true" : "false";
+    case Arg::Kind::Int:
+      if (c.dtype().kind == DTypeKind::F32) return float_lit(static_cast<double>(a.a));
+      if (c.dtype().kind == DTypeKind::Bool) return a.a ? "true" : "false";
+      return std::to_string(a.a);
+    case Arg::Kind::Bool:
+      if (c.dtype().kind == DTypeKind::F32) return a.a ? "1.0f" : "0.0f";
+      return a.a ? "true" : "false";
+    default:
+      fail("Const with unexpected arg");
+  }
+}
+
+std::string pname(const UOp& p) { return "data" + std::to_string(p.arg().a); }
+
+// Combine two values with a reduce op in the reference's operand order.
+std::string combine(Op rop, const std::string& a, const std::string& b) {
+  if (rop == Op::Add) return "(" + a + "+" + b + ")";
+  if (rop == Op::Max) return "((" + a + ">" + b + ")?" + a + ":" + b + ")";
+  fail("unsupported reduce op");
+}
+
+std::string init_lit(Op rop, DType dt) {  // devectorize.rs:219-225
+  if (dt.kind != DTypeKind::F32) return rop == Op::Add ? "0" : "(-2147483647-1)";
+  return rop == Op::Add ? "0.0f" : "(-__builtin_inff())";
+}
+
+// Scoped statement emitter for a value DAG. Each node is emitted once per
+// (scope, lane); nodes are placed in the innermost open scope that defines a
+// range they depend on, so loop-invariant loads hoist out of reduce loops.
+class Emitter {
+ public:
+  struct Scope {
+    std::string header, footer;
+    std::ostringstream body;
+    std::set<const UOpInner*> ranges;
+    std::vector<std::pair<const UOpInner*, int>> keys;
+    int indent = 1;
+  };
+
+  Emitter() { scopes_.emplace_back(new Scope()); }
+
+  void define_range(const UOp& r, const std::string& expr) {
+    range_expr_[r.get()] = expr;
+    scopes_.back()->ranges.insert(r.get());
+  }
+
+  // The range whose value differs per lane: lane u reads `base + u`.
+  void set_lane_range(const UOp& r, int lanes) {
+    lane_range_ = r.get();
+    lanes_ = lanes;
+  }
+  void clear_lane_range() {
+    lane_range_ = nullptr;
+    lanes_ = 1;
+  }
+
+  void open_scope(const std::string& header, const std::string& footer) {
+    auto* s = new Scope();
+    s->header = header;
+    s->footer = footer;
+    s->indent = scopes_.back()->indent + 1;
+    scopes_.emplace_back(s);
+  }
+
+  void close_scope() {
+    std::unique_ptr<Scope> s(scopes_.back().release());
+    scopes_.pop_back();
+    for (auto& k : s->keys) cache_.erase(k);
+    for (auto* r : s->ranges) range_expr_.erase(r);
+    Scope& p = *scopes_.back();
+    std::string ind(static_cast<size_t>(p.indent) * 2, ' ');
+    p.body << ind << s->header << "\n" << s->body.str() << ind << s->footer << "\n";
+  }
+
+  // Emit a raw line into the current (innermost) scope.
+  void line(const std::string& l) {
+    Scope& s = *scopes_.back();
+    s.body << std::string(static_cast<size_t>(s.indent) * 2, ' ') << l << "\n";
+  }
+
+  std::string fresh(const char* prefix) { return std::string(prefix) + std::to_string(counter_++); }
+
+  std::string code() { return scopes_.front()->body.str(); }
+
+  bool depends_on(const UOp& n, const UOpInner* r) {
+    if (!r) return false;
+    auto key = std::make_pair(n.get(), r);
+    auto it = dep_cache_.find(key);
+    if (it != dep_cache_.end()) return it->second;
+    bool d = n.get() == r;
+    if (!d)
+      for (auto& s : n.srcs())
+        if (depends_on(s, r)) {
+          d = true;
+          break;
+        }
+    dep_cache_[key] = d;
+    return d;
+  }
+
+  // Index of the innermost open scope that defines a range `n` depends on.
+  size_t scope_of(const UOp& n) {
+    size_t best = 0;
+    for (size_t i = scopes_.size(); i-- > 1;) {
+      for (auto* r : scopes_[i]->ranges) {
+        if (depends_on(n, r)) return i;
+      }
+    }
+    return best;
+  }
+
+  std::string idx(const UOp& e, int lane) {
+    switch (e.op()) {
+      case Op::Const: return const_lit(e);
+      case Op::ParamScalar: return pname(e);
+      case Op::Range: {
+        auto it = range_expr_.find(e.get());
+        FG_CHECK(it != range_expr_.end(), "range used outside its scope");
+        if (e.get() == lane_range_ && lane > 0) return "(" + it->second + "+" + std::to_string(lane) + ")";
+        return it->second;
+      }
+      case Op::Add: return "(" + idx(e.src(0), lane) + "+" + idx(e.src(1), lane) + ")";
+      case Op::Mul: return "(" + idx(e.src(0), lane) + "*" + idx(e.src(1), lane) + ")";
+      default: break;
+    }
+    // Non-index ops inside an int expression are values.
+    return val(e, lane);
+  }
+
+  // Vectorised load check: unit stride along the lane range, every other
+  // term a multiple of 4 (16-byte aligned for 4-byte elements).
+  bool vec4_load(const UOp& load) {
+    if (lanes_ != 4 || !lane_range_) return false;
+    DType dt = load.dtype();
+    if (dt.kind != DTypeKind::F32 && dt.kind != DTypeKind::I32) return false;
+    Affine a = affine_of(load.src(0).src(1));
+    if (!a.ok || a.has_scalar_terms() || a.c0 % 4 != 0) return false;
+    bool unit = false;
+    for (auto& t : a.terms) {
+      if (t.first.get() == lane_range_) unit = t.second == 1;
+      else if (t.second % 4 != 0) return false;
+    }
+    return unit && lane_base_aligned_;
+  }
+  void set_lane_base_aligned(bool b) { lane_base_aligned_ = b; }
+
+  std::string val(const UOp& n, int lane) {
+    bool lane_dep = lane_range_ && depends_on(n, lane_range_);
+    int key_lane = lane_dep ? lane : -1;
+    auto key = std::make_pair(n.get(), key_lane);
+    auto it = cache_.find(key);
+    if (it != cache_.end()) return it->second;
+    std::string out;
+    switch (n.op()) {
+      case Op::Const: return const_lit(n);
+      case Op::ParamScalar: return pname(n);
+      case Op::Range: case Op::Add: case Op::Mul:
+        if (n.dtype().kind == DTypeKind::I32 && (n.op() == Op::Range || is_index_expr(n))) return idx(n, lane);
+        break;
+      default: break;
+    }
+    size_t si = scope_of(n);
+    if (n.op() == Op::Load) {
+      const UOp& ix = n.src(0);
+      FG_CHECK(ix.op() == Op::Index, "Load must read through Index");
+      if (lane_dep && vec4_load(n)) {
+        std::string v = fresh("vec");
+        const char* vt = n.dtype().kind == DTypeKind::F32 ? "float4" : "int4";
+        emit_at(si, std::string("const ") + vt + " " + v + " = *(const " + vt + "*)(" + pname(ix.src(0)) + "+" +
+                        idx(ix.src(1), 0) + ");");
+        static const char* comp[4] = {".x", ".y", ".z", ".w"};
+        for (int u = 0; u < 4; u++) remember(si, std::make_pair(n.get(), u), v + comp[u]);
+        return v + comp[lane];
+      }
+      std::string v = fresh("val");
+      emit_at(si, std::string(ctype(n.dtype())) + " " + v + " = " + pname(ix.src(0)) + "[" + idx(ix.src(1), lane) + "];");
+      out = v;
+    } else if (n.op() == Op::Reduce) {
+      FG_CHECK(reduce_cb_, "Reduce reached a renderer without reduction support");
+      out = reduce_cb_(n, lane);
+      return out;  // the callback caches its own result
+    } else {
+      std::vector<std::string> s;
+      for (auto& x : n.srcs()) s.push_back(val(x, lane));
+      std::string e;
+      switch (n.op()) {
+        case Op::Neg: e = "(-" + s[0] + ")"; break;
+        case Op::Exp2: e = "(float)exp2((double)" + s[0] + ")"; break;   // clang.rs:218 (double exp2)
+        case Op::Log2: e = "(float)log2((double)" + s[0] + ")"; break;   // clang.rs:219 (double log2)
+        case Op::Sqrt: e = "__fsqrt_rn(" + s[0] + ")"; break;            // correctly rounded, as sqrtf
+        case Op::Reciprocal:
+          e = n.dtype().kind == DTypeKind::F32 ? "__fdiv_rn(1.0f," + s[0] + ")" : "(1/" + s[0] + ")";
+          break;
+        case Op::Add: e = "(" + s[0] + "+" + s[1] + ")"; break;
+        case Op::Mul: e = "(" + s[0] + "*" + s[1] + ")"; break;
+        case Op::Max: e = "((" + s[0] + ">" + s[1] + ")?" + s[0] + ":" + s[1] + ")"; break;
+        case Op::CmpLt: e = "(" + s[0] + "<" + s[1] + ")"; break;
+        case Op::Where: e = "(" + s[0] + "?" + s[1] + ":" + s[2] + ")"; break;
+        default: fail(std::string("HIP renderer cannot emit ") + op_name(n.op()));
+      }
+      std::string v = fresh("alu");
+      emit_at(si, std::string(ctype(n.dtype())) + " " + v + " = " + e + ";");
+      out = v;
+    }
+    remember(si, key, out);
+    return out;
+  }
+
+  void remember(size_t si, std::pair<const UOpInner*, int> key, const std::string& name) {
+    cache_[key] = name;
+    scopes_[si]->keys.push_back(key);
+  }
+  void remember_here(const UOp& n, int lane, const std::string& name) {
+    bool lane_dep = lane_range_ && depends_on(n, lane_range_);
+    remember(scopes_.size() - 1, std::make_pair(n.get(), lane_dep ? lane : -1), name);
+  }
+
+  void emit_at(size_t si, const std::string& l) {
+    Scope& s = *scopes_[si];
+    s.body << std::string(static_cast<size_t>(s.indent) * 2, ' ') << l << "\n";
+  }
+
+  size_t depth() const { return scopes_.size(); }
+
+  std::function<std::string(const UOp&, int)> reduce_cb_;
+
+ private:
+  static bool is_index_expr(const UOp& n) {
+    if (n.op() == Op::Range || n.op() == Op::Const || n.op() == Op::ParamScalar) return true;
+    if (n.op() == Op::Add || n.op() == Op::Mul) return is_index_expr(n.src(0)) && is_index_expr(n.src(1));
+    return false;
+  }
+
+  std::vector<std::unique_ptr<Scope>> scopes_;
+  std::map<std::pair<const UOpInner*, int>, std::string> cache_;
+  std::map<std::pair<const UOpInner*, const UOpInner*>, bool> dep_cache_;
+  std::unordered_map<const UOpInner*, std::string> range_expr_;
+  const UOpInner* lane_range_ = nullptr;
+  int lanes_ = 1;
+  bool lane_base_aligned_ = true;
+  int counter_ = 0;
+};
+
+std::string signature(const KernelInfo& ki, const std::string& name, int block) {
+  std::ostringstream os;
+  os << "extern \"C\" __global__ void __launch_bounds__(" << block << ") " << name << "(";
+  bool first = true;
+  // Find which buffers are written (the store target) to drop const.
+  for (auto& [slot, p] : ki.params) {
+    if (!first) os << ", ";
+    first = false;
+    if (p.op() == Op::ParamBuffer) {
+      bool written = p == ki.out_param;
+      os << (written ? "" : "const ") << ctype(p.dtype()) << "* __restrict__ data" << slot;
+    } else {
+      os << ctype(p.dtype()) << " data" << slot;
+    }
+  }
+  os << ")";
+  return os.str();
+}
+
+const char* kPrelude = R"(// generated by ferrograd_amd for gfx950
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+// Cross-lane moves on 32-bit values. DPP row-local patterns for distances
+// inside a row of 16 lanes, ds_swizzle for 16, ds_bpermute for 32.
+#define FG_DPP(v, ctrl) __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), ctrl, 0xF, 0xF, false))
+#define FG_DPPI(v, ctrl) (__builtin_amdgcn_update_dpp(0, (v), ctrl, 0xF, 0xF, false))
+__device__ __forceinline__ float fg_swz16_f(float v) { return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x401F)); }
+__device__ __forceinline__ int fg_swz16_i(int v) { return __builtin_amdgcn_ds_swizzle(v, 0x401F); }
+__device__ __forceinline__ float fg_x32_f(float v) { return __int_as_float(__builtin_amdgcn_ds_bpermute(((int)(threadIdx.x ^ 32u)) << 2, __float_as_int(v))); }
+__device__ __forceinline__ int fg_x32_i(int v) { return __builtin_amdgcn_ds_bpermute(((int)(threadIdx.x ^ 32u)) << 2, v); }
+)";
+
+// Group-of-T lane reduction (T a power of two <= 64, groups aligned to T).
+// quad_perm xor1 (0xB1), xor2 (0x4E); row_half_mirror (0x141) and row_mirror
+// (0x140) pair each half with the reflected half, so after each step every
+// lane of the group holds the group total.
+std::string wave_reduce(const std::string& var, int T, Op rop, DType dt) {
+  std::ostringstream os;
+  bool f = dt.kind == DTypeKind::F32;
+  auto step = [&](const std::string& other) {
+    os << "{ " << ctype(dt) << " o = " << other << "; " << var << " = " << combine(rop, var, "o") << "; }\n";
+  };
+  const char* dpp = f ? "FG_DPP" : "FG_DPPI";
+  if (T >= 2) step(std::string(dpp) + "(" + var + ", 0xB1)");
+  if (T >= 4) step(std::string(dpp) + "(" + var + ", 0x4E)");
+  if (T >= 8) step(std::string(dpp) + "(" + var + ", 0x141)");
+  if (T >= 16) step(std::string(dpp) + "(" + var + ", 0x140)");
+  if (T >= 32) step(std::string(f ? "fg_swz16_f(" : "fg_swz16_i(") + var + ")");
+  if (T >= 64) step(std::string(f ? "fg_x32_f(" : "fg_x32_i(") + var + ")");
+  return os.str();
+}
+
+int pow2_floor(int64_t x) {
+  int p = 1;
+  while (static_cast<int64_t>(p) * 2 <= x) p *= 2;
+  return p;
+}
+
+// Decode the flattened output index `lin` into range variables (innermost
+// range varies fastest). Emits `int idxN = ...;` lines, skipping `skip`.
+void decode_outputs(Emitter& em, const KernelInfo& ki, const std::string& lin, const UOp& skip) {
+  std::string rest = lin;
+  bool first = true;
+  for (size_t i = ki.out_ranges.size(); i-- > 0;) {
+    const UOp& r = ki.out_ranges[i];
+    if (r == skip) continue;
+    std::string name = "idx" + std::to_string(r.arg().a);
+    int64_t e = ki.out_ext[i];
+    // Is this the outermost remaining range? Then no modulo is needed.
+    bool outermost = true;
+    for (size_t j = 0; j < i; j++)
+      if (ki.out_ranges[j] != skip) outermost = false;
+    if (outermost) em.line("const int " + name + " = (int)(" + rest + ");");
+    else em.line("const int " + name + " = (int)((" + rest + ") % " + std::to_string(e) + ");");
+    em.define_range(r, name);
+    if (!outermost) {
+      std::string nr = "rest" + std::to_string(i);
+      em.line("const long " + nr + " = (" + rest + ") / " + std::to_string(e) + ";");
+      rest = nr;
+    }
+    first = false;
+  }
+  (void)first;
+}
+
+UOp pick_fast_output(const KernelInfo& ki) {
+  if (ki.out_ranges.empty()) return UOp();
+  Affine a = affine_of(ki.out_index);
+  for (auto& r : ki.out_ranges)
+    if (a.ok && a.coef(r) == 1) return r;
+  return ki.out_ranges.back();
+}
+
+int64_t total_outputs(const KernelInfo& ki) {
+  int64_t t = 1;
+  for (auto e : ki.out_ext) t *= e;
+  return t;
+}
+
+// Serial reduction in the reference's exact order: loops over the reduce
+// ranges in source order; the innermost splits into REDUCE x UNROLL(4) when its
+// extent is a multiple of 4 above 4 (unroll.rs:41-113), and each outer step
+// folds acc = acc (op) (((v0 op v1) op v2) op v3) (devectorize.rs:206-214, 306-319).
+std::string emit_serial_reduce(Emitter& em, const UOp& R, int lane_outer) {
+  (void)lane_outer;
+  Op rop = R.arg().rop;
+  std::vector<UOp> ranges(R.srcs().begin() + 1, R.srcs().end());
+  std::string acc = em.fresh("acc");
+  em.line(std::string(ctype(R.dtype())) + " " + acc + " = " + init_lit(rop, R.dtype()) + ";");
+  size_t opened = 0;
+  int unroll = 1;
+  for (size_t i = 0; i < ranges.size(); i++) {
+    const UOp& r = ranges[i];
+    int64_t ext = range_extent(r);
+    std::string v = "ridx" + std::to_string(r.arg().a) + "_" + std::to_string(em.depth());
+    bool last = i + 1 == ranges.size();
+    if (last && ext > 4 && ext % 4 == 0) {
+      unroll = 4;
+      em.open_scope("for (int " + v + " = 0; " + v + " < " + std::to_string(ext / 4) + "; " + v + "++) {", "}");
+      em.define_range(r, "(" + v + "*4)");
+      em.set_lane_range(r, 4);
+    } else {
+      em.open_scope("for (int " + v + " = 0; " + v + " < " + std::to_string(ext) + "; " + v + "++) {", "}");
+      em.define_range(r, v);
+    }
+    opened++;
+  }
+  const UOp& value = R.src(0);
+  std::string group;
+  if (unroll == 4) {
+    std::vector<std::string> lanes;
+    for (int u = 0; u < 4; u++) lanes.push_back(em.val(value, u));
+    group = lanes[0];
+    for (int u = 1; u < 4; u++) group = combine(rop, group, lanes[u]);
+  } else {
+    group = em.val(value, 0);
+  }
+  em.line(acc + " = " + combine(rop, acc, group) + ";");
+  if (unroll == 4) em.clear_lane_range();
+  for (size_t i = 0; i < opened; i++) em.close_scope();
+  return acc;
+}
+
+// ── Serial / fallback ───────────────────────────────────────────────────────
+RenderedKernel render_serial(const KernelInfo& ki, const std::string& name) {
+  Emitter em;
+  int64_t T = total_outputs(ki);
+  em.line("const long gid = (long)blockIdx.x * 256 + threadIdx.x;");
+  em.line("if (gid >= " + std::to_string(T) + "L) return;");
+  decode_outputs(em, ki, "gid", UOp());
+  em.reduce_cb_ = [&](const UOp& R, int lane) {
+    std::string acc = emit_serial_reduce(em, R, lane);
+    em.remember_here(R, lane, acc);
+    return acc;
+  };
+  std::string v = em.val(ki.value, 0);
+  em.line(pname(ki.out_param) + "[" + em.idx(ki.out_index, 0) + "] = " + v + ";");
+  RenderedKernel rk;
+  rk.name = name;
+  rk.kind = kernel_class_name(KernelClass::Serial);
+  rk.source = std::string(kPrelude) + signature(ki, name, 256) + " {\n" + em.code() + "}\n";
+  rk.block[0] = 256;
+  rk.grid[0] = static_cast<unsigned>((T + 255) / 256);
+  return rk;
+}
+
+// ── Elementwise ─────────────────────────────────────────────────────────────
+RenderedKernel render_elementwise(const KernelInfo& ki, const std::string& name) {
+  Emitter em;
+  UOp fast = pick_fast_output(ki);
+  int64_t T = total_outputs(ki);
+  int V = 1;
+  int64_t fext = 1;
+  if (fast) {
+    for (size_t i = 0; i < ki.out_ranges.size(); i++)
+      if (ki.out_ranges[i] == fast) fext = ki.out_ext[i];
+    if (fext % 4 == 0) V = 4;
+  }
+  int64_t threads = T / V;
+  em.line("const long gid = (long)blockIdx.x * 256 + threadIdx.x;");
+  em.line("if (gid >= " + std::to_string(threads) + "L) return;");
+  if (V == 4) {
+    int64_t per = fext / 4;
+    em.line("const int fbase = (int)(gid % " + std::to_string(per) + ") * 4;");
+    em.line("const long orest = gid / " + std::to_string(per) + ";");
+    em.define_range(fast, "fbase");
+    decode_outputs(em, ki, "orest", fast);
+    em.set_lane_range(fast, 4);
+  } else {
+    decode_outputs(em, ki, "gid", UOp());
+  }
+  std::vector<std::string> vals;
+  for (int u = 0; u < V; u++) vals.push_back(em.val(ki.value, u));
+  const std::string out = pname(ki.out_param);
+  bool vstore = false;
+  if (V == 4) {
+    Affine a = affine_of(ki.out_index);
+    DType dt = ki.out_param.dtype();
+    vstore = a.ok && !a.has_scalar_terms() && a.coef(fast) == 1 && a.c0 % 4 == 0 &&
+             (dt.kind == DTypeKind::F32 || dt.kind == DTypeKind::I32);
+    for (auto& t : a.terms)
+      if (t.first != fast && t.second % 4 != 0) vstore = false;
+    if (vstore) {
+      const char* vt = dt.kind == DTypeKind::F32 ? "float4" : "int4";
+      const char* mk = dt.kind == DTypeKind::F32 ? "make_float4" : "make_int4";
+      em.line(std::string("*(") + vt + "*)(" + out + "+" + em.idx(ki.out_index, 0) + ") = " + mk + "(" + vals[0] +
+              ", " + vals[1] + ", " + vals[2] + ", " + vals[3] + ");");
+    }
+  }
+  if (!vstore)
+    for (int u = 0; u < V; u++) em.line(out + "[" + em.idx(ki.out_index, u) + "] = " + vals[u] + ";");
+  RenderedKernel rk;
+  rk.name = name;
+  rk.kind = kernel_class_name(KernelClass::Elementwise);
+  rk.source = std::string(kPrelude) + signature(ki, name, 256) + " {\n" + em.code() + "}\n";
+  rk.block[0] = 256;
+  rk.grid[0] = static_cast<unsigned>((threads + 255) / 256);
+  return rk;
+}
+
+// Loads inside the reduced value.
+std::vector<UOp> loads_in(const UOp& v) {
+  std::vector<UOp> out;
+  for (auto& n : v.toposort())
+    if (n.op() == Op::Load) out.push_back(n);
+  return out;
+}
+
+// ── RowReduce ───────────────────────────────────────────────────────────────
+RenderedKernel render_row_reduce(const KernelInfo& ki, const std::string& name) {
+  const UOp& R = ki.reduces[0];
+  Op rop = R.arg().rop;
+  DType dt = R.dtype();
+  std::vector<UOp> ranges(R.srcs().begin() + 1, R.srcs().end());
+  const UOp r_in = ranges.back();
+  int64_t L = range_extent(r_in);
+  int T = std::min<int>(256, pow2_floor(std::max<int64_t>(1, L / 16)));
+  int OPW = 256 / T;  // outputs per workgroup
+  int64_t NOUT = total_outputs(ki);
+  // Vector width along r_in: all lane-dependent loads unit-stride and aligned.
+  int V = (L % 4 == 0) ? 4 : 1;
+  if (V == 4) {
+    for (auto& ld : loads_in(R.src(0))) {
+      Affine a = affine_of(ld.src(0).src(1));
+      int64_t c = a.ok ? a.coef(r_in) : -1;
+      if (c == 0) continue;
+      bool ok = a.ok && !a.has_scalar_terms() && c == 1 && a.c0 % 4 == 0 &&
+                (ld.dtype().kind == DTypeKind::F32 || ld.dtype().kind == DTypeKind::I32);
+      for (auto& t : a.terms)
+        if (t.first != r_in && t.second % 4 != 0) ok = false;
+      if (!ok) V = 1;
+    }
+  }
+  Emitter em;
+  em.line("const int tid = threadIdx.x;");
+  em.line("const int rlane = tid % " + std::to_string(T) + ";");
+  em.line("const long oid = (long)blockIdx.x * " + std::to_string(OPW) + " + tid / " + std::to_string(T) + ";");
+  em.line("const bool active = oid < " + std::to_string(NOUT) + "L;");
+  em.line("const long ocl = active ? oid : 0;");
+  decode_outputs(em, ki, "ocl", UOp());
+  std::string result;
+  em.reduce_cb_ = [&](const UOp& RR, int lane) -> std::string {
+    FG_CHECK(RR == R, "row reduce renders exactly one reduction");
+    std::string acc = "racc";
+    em.line(std::string(ctype(dt)) + " " + acc + " = " + init_lit(rop, dt) + ";");
+    size_t opened = 0;
+    for (size_t i = 0; i + 1 < ranges.size(); i++) {
+      std::string v = "ro" + std::to_string(i);
+      em.open_scope("for (int " + v + " = 0; " + v + " < " + std::to_string(range_extent(ranges[i])) + "; " + v + "++) {",
+                    "}");
+      em.define_range(ranges[i], v);
+      opened++;
+    }
+    em.open_scope("if (active) for (int rj = rlane * " + std::to_string(V) + "; rj < " + std::to_string(L) +
+                      "; rj += " + std::to_string(T * V) + ") {",
+                  "}");
+    em.define_range(r_in, "rj");
+    opened++;
+    std::string group;
+    if (V == 4) {
+      em.set_lane_range(r_in, 4);
+      std::vector<std::string> lanes;
+      for (int u = 0; u < 4; u++) lanes.push_back(em.val(R.src(0), u));
+      group = combine(rop, combine(rop, combine(rop, lanes[0], lanes[1]), lanes[2]), lanes[3]);
+    } else {
+      group = em.val(R.src(0), 0);
+    }
+    em.line(acc + " = " + combine(rop, acc, group) + ";");
+    if (V == 4) em.clear_lane_range();
+    for (size_t i = 0; i < opened; i++) em.close_scope();
+    // Tree across the T threads of this output.
+    if (T > 1) {
+      int tw = std::min(T, 64);
+      std::string wr = wave_reduce(acc, tw, rop, dt);
+      std::istringstream is(wr);
+      std::string l;
+      while (std::getline(is, l)) em.line(l);
+    }
+    if (T > 64) {
+      int nw = T / 64;
+      em.line(std::string("__shared__ ") + ctype(dt) + " fg_part[4];");
+      em.line("if ((tid & 63) == 0) fg_part[tid >> 6] = " + acc + ";");
+      em.line("__syncthreads();");
+      em.line("{ const int g0 = (tid >> 6) & ~" + std::to_string(nw - 1) + "; " + acc + " = fg_part[g0];");
+      for (int w = 1; w < nw; w++) em.line("  " + acc + " = " + combine(rop, acc, "fg_part[g0+" + std::to_string(w) + "]") + ";");
+      em.line("}");
+    }
+    em.remember_here(RR, lane, acc);
+    return acc;
+  };
+  std::string v = em.val(ki.value, 0);
+  (void)result;
+  em.line("if (active && rlane == 0) " + pname(ki.out_param) + "[" + em.idx(ki.out_index, 0) + "] = " + v + ";");
+  RenderedKernel rk;
+  rk.name = name;
+  rk.kind = kernel_class_name(KernelClass::RowReduce);
+  rk.source = std::string(kPrelude) + signature(ki, name, 256) + " {\n" + em.code() + "}\n";
+  rk.block[0] = 256;
+  rk.grid[0] = static_cast<unsigned>((NOUT + OPW - 1) / OPW);
+  return rk;
+}
+
+// ── ColumnReduce ────────────────────────────────────────────────────────────
+RenderedKernel render_column_reduce(const KernelInfo& ki, const std::string& name) {
+  const UOp& R = ki.reduces[0];
+  Op rop = R.arg().rop;
+  DType dt = R.dtype();
+  const UOp r = R.src(1);
+  int64_t L = range_extent(r);
+  UOp fast = pick_fast_output(ki);
+  int64_t fext = 1;
+  for (size_t i = 0; i < ki.out_ranges.size(); i++)
+    if (ki.out_ranges[i] == fast) fext = ki.out_ext[i];
+  int V = fext % 4 == 0 ? 4 : 1;
+  int TX = std::min<int64_t>(64, std::max<int64_t>(1, pow2_floor((fext + V - 1) / V)));
+  int TR = 256 / TX;
+  int64_t per_f = (fext + static_cast<int64_t>(TX) * V - 1) / (static_cast<int64_t>(TX) * V);  // blocks along fast
+  int64_t other = total_outputs(ki) / fext;
+  Emitter em;
+  em.line("const int tid = threadIdx.x;");
+  em.line("const int tx = tid % " + std::to_string(TX) + ", tr = tid / " + std::to_string(TX) + ";");
+  em.line("const int fbase = (int)(blockIdx.x % " + std::to_string(per_f) + ") * " + std::to_string(TX * V) + " + tx * " +
+          std::to_string(V) + ";");
+  em.line("const long orest = blockIdx.x / " + std::to_string(per_f) + ";");
+  em.line("const bool active = fbase < " + std::to_string(fext) + ";");
+  // Inactive threads still evaluate hoisted loads: clamp them in bounds.
+  em.line("const int fcl = active ? fbase : 0;");
+  em.define_range(fast, "fcl");
+  decode_outputs(em, ki, "orest", fast);
+  em.set_lane_base_aligned(true);
+  if (V == 4) em.set_lane_range(fast, 4);
+  std::vector<std::string> accs(V);
+  em.reduce_cb_ = [&](const UOp& RR, int lane) -> std::string {
+    FG_CHECK(RR == R, "column reduce renders exactly one reduction");
+    if (lane == 0) {
+      for (int u = 0; u < V; u++) {
+        accs[u] = "cacc" + std::to_string(u);
+        em.line(std::string(ctype(dt)) + " " + accs[u] + " = " + init_lit(rop, dt) + ";");
+      }
+      em.open_scope("if (active) for (int rr = tr; rr < " + std::to_string(L) + "; rr += " + std::to_string(TR) + ") {", "}");
+      em.define_range(r, "rr");
+      for (int u = 0; u < V; u++) em.line(accs[u] + " = " + combine(rop, accs[u], em.val(R.src(0), u)) + ";");
+      em.close_scope();
+      em.line(std::string("__shared__ ") + ctype(dt) + " fg_col[" + std::to_string(TR) + "][" + std::to_string(TX * V) + "];");
+      for (int u = 0; u < V; u++)
+        em.line("fg_col[tr][tx*" + std::to_string(V) + "+" + std::to_string(u) + "] = " + accs[u] + ";");
+      em.line("__syncthreads();");
+      em.line("if (tr == 0) {");
+      for (int u = 0; u < V; u++) {
+        em.line("  " + accs[u] + " = fg_col[0][tx*" + std::to_string(V) + "+" + std::to_string(u) + "];");
+        em.line("  for (int q = 1; q < " + std::to_string(TR) + "; q++) " + accs[u] + " = " +
+                combine(rop, accs[u], "fg_col[q][tx*" + std::to_string(V) + "+" + std::to_string(u) + "]") + ";");
+      }
+      em.line("}");
+      for (int u = 0; u < V; u++) em.remember_here(RR, u, accs[u]);
+    }
+    return accs[lane];
+  };
+  std::vector<std::string> vals;
+  for (int u = 0; u < V; u++) vals.push_back(em.val(ki.value, u));
+  for (int u = 0; u < V; u++) {
+    std::string guard = "active && tr == 0";
+    if (V == 1 || fext % 4 != 0) guard += " && fbase + " + std::to_string(u) + " < " + std::to_string(fext);
+    em.line("if (" + guard + ") " + pname(ki.out_param) + "[" + em.idx(ki.out_index, u) + "] = " + vals[u] + ";");
+  }
+  RenderedKernel rk;
+  rk.name = name;
+  rk.kind = kernel_class_name(KernelClass::ColumnReduce);
+  rk.source = std::string(kPrelude) + signature(ki, name, 256) + " {\n" + em.code() + "}\n";
+  rk.block[0] = 256;
+  rk.grid[0] = static_cast<unsigned>(per_f * other);
+  return rk;
+}
+
+// ── GEMM (fp32 MFMA) ────────────────────────────────────────────────────────
+// One GEMM operand: an elementwise expression (a bare load, or e.g. the ReLU
+// of a load that the reference leaves unmaterialised) over the reduce range
+// and exactly one output range. Its tile loader evaluates the expression.
+struct GemmOperand {
+  UOp expr;
+  UOp rout;     // the output range this operand varies with
+  Affine lead;  // index of its first load that moves with the reduce range
+};
+
+struct GemmMatch {
+  UOp R;              // the reduction
+  UOp rm, rn, rk;     // output rows, output cols, reduce range
+  int64_t M = 0, N = 0, K = 0;
+  GemmOperand a, b;   // a pairs with rm, b with rn
+};
+
+bool gemm_operand(const UOp& e, const UOp& rk, const KernelInfo& ki, GemmOperand* op) {
+  if (e.dtype() != DType::F32()) return false;
+  auto lds = loads_in(e);
+  if (lds.empty()) return false;
+  UOp rout;
+  bool have_lead = false;
+  for (auto& n : e.toposort()) {
+    if (n.op() == Op::Reduce) return false;
+    if (n.op() == Op::Range && n != rk) {
+      if (rout && rout != n) return false;
+      rout = n;
+    }
+  }
+  for (auto& ld : lds) {
+    if (ld.src(0).src(0) == ki.out_param) return false;  // in-place tiles would race
+    Affine a = affine_of(ld.src(0).src(1));
+    if (!a.ok || a.has_scalar_terms()) return false;
+    if (!have_lead && a.coef(rk) != 0) {
+      op->lead = a;
+      have_lead = true;
+    }
+  }
+  if (!rout || !have_lead) return false;
+  op->expr = e;
+  op->rout = rout;
+  return true;
+}
+
+bool match_gemm(const KernelInfo& ki, GemmMatch* g) {
+  if (ki.reduces.size() != 1 || ki.out_ranges.size() != 2) return false;
+  const UOp& R = ki.reduces[0];
+  if (R.arg().rop != Op::Add || R.srcs().size() != 2 || R.dtype() != DType::F32()) return false;
+  const UOp& v = R.src(0);
+  if (v.op() != Op::Mul) return false;
+  const UOp& rk = R.src(1);
+  GemmOperand x, y;
+  if (!gemm_operand(v.src(0), rk, ki, &x) || !gemm_operand(v.src(1), rk, ki, &y)) return false;
+  if (x.rout == y.rout) return false;
+  Affine ao = affine_of(ki.out_index);
+  if (!ao.ok) return false;
+  // Tile columns follow the output range with the smaller store stride so
+  // epilogue stores coalesce.
+  int64_t cx = std::llabs(ao.coef(x.rout)), cy = std::llabs(ao.coef(y.rout));
+  bool swap = cx < cy;
+  g->R = R;
+  g->rk = rk;
+  g->a = swap ? y : x;
+  g->b = swap ? x : y;
+  g->rm = g->a.rout;
+  g->rn = g->b.rout;
+  g->M = range_extent(g->rm);
+  g->N = range_extent(g->rn);
+  g->K = range_extent(rk);
+  if (g->M < 16 || g->N < 16 || g->M * g->N * g->K < (1LL << 18)) return false;
+  return true;
+}
+
+RenderedKernel render_gemm(const KernelInfo& ki, const GemmMatch& g, const std::string& name) {
+  const int64_t M = g.M, N = g.N, K = g.K;
+  // Tile: 128x128 when that still gives a few hundred tiles, else 64-wide.
+  int BM = 128, BN = 128;
+  if ((M + 127) / 128 * ((N + 127) / 128) < 256) {
+    BM = M >= 128 && (M + 63) / 64 * ((N + 63) / 64) < 128 ? 128 : 64;
+    BN = 64;
+  }
+  if (N <= 64) BN = 64;
+  if (M <= 64) BM = 64;
+  const int BK = 16;
+  const int PAD = 4;
+
+  std::ostringstream s;
+  s << kPrelude;
+  s << "#define M_ " << M << "\n#define N_ " << N << "\n#define K_ " << K << "\n";
+  s << "#define BM " << BM << "\n#define BN " << BN << "\n#define BK " << BK << "\n#define PAD " << PAD << "\n";
+  s << signature(ki, name, 256) << " {\n";
+  s << R"(  __shared__ float As[2][BK][BM + PAD];
+  __shared__ float Bs[2][BK][BN + PAD];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int nbm = (M_ + BM - 1) / BM, nbn = (N_ + BN - 1) / BN, nb = nbm * nbn;
+  int bid = blockIdx.x;
+  // Blocks are dispatched round-robin over the 8 XCDs; give each XCD a
+  // contiguous run of tiles so neighbouring tiles share its L2.
+  if (nb % 8 == 0) bid = (bid % 8) * (nb / 8) + bid / 8;
+  const int GM = 8;
+  const int group = bid / (GM * nbn), first_m = group * GM;
+  const int gsz = (nbm - first_m) < GM ? (nbm - first_m) : GM;
+  const int tm = first_m + (bid % (GM * nbn)) % gsz, tn = (bid % (GM * nbn)) / gsz;
+  const int m0 = tm * BM, n0 = tn * BN;
+  // 2x2 waves; each wave owns a (BM/2)x(BN/2) block of 32x32 MFMA tiles.
+  constexpr int WM = BM / 2, WN = BN / 2, TM = WM / 32, TN = WN / 32;
+  const int wm = (wave >> 1) * WM, wn = (wave & 1) * WN;
+  floatx16 acc[TM][TN];
+  #pragma unroll
+  for (int i = 0; i < TM; i++)
+    #pragma unroll
+    for (int j = 0; j < TN; j++)
+      #pragma unroll
+      for (int e = 0; e < 16; e++) acc[i][j][e] = 0.0f;
+  constexpr int AE = BM * BK / 256, BE = BN * BK / 256;  // elements per thread per stage
+  float ra[AE], rb[BE];
+)";
+  // Global -> register loaders. Staging modes: 0 = 4 consecutive k per thread
+  // (unit stride along k: 16-byte loads), 1 = 4 consecutive rows per thread
+  // (unit stride along m/n), 2 = one element at a time. The operand expression
+  // is rendered per element group by the emitter, vectorising unit-stride loads.
+  auto loader = [&](const char* X, const GemmOperand& op, int BX, int64_t ext, const char* dim) {
+    int64_t so = op.lead.coef(op.rout), sk = op.lead.coef(g.rk);
+    int md = 2;
+    if (sk == 1 && K % 4 == 0) md = 0;
+    else if (so == 1 && ext % 4 == 0) md = 1;
+    bool k_fast = std::llabs(sk) <= std::llabs(so);  // mode 2 mapping
+    auto body = [&](const std::string& dst, int lanes_along_k, int lanes_along_r) {
+      Emitter em;
+      em.define_range(op.rout, "gr");
+      em.define_range(g.rk, "gk");
+      int V = 1;
+      if (lanes_along_k) {
+        em.set_lane_range(g.rk, 4);
+        V = 4;
+      } else if (lanes_along_r) {
+        em.set_lane_range(op.rout, 4);
+        V = 4;
+      }
+      std::vector<std::string> vals;
+      for (int u = 0; u < V; u++) vals.push_back(em.val(op.expr, u));
+      std::ostringstream b;
+      std::istringstream is(em.code());
+      std::string ln;
+      while (std::getline(is, ln)) b << "        " << ln << "\n";
+      for (int u = 0; u < V; u++) b << "        " << dst << (V > 1 ? "[" + std::to_string(u) + "]" : "") << " = " << vals[u] << ";\n";
+      return b.str();
+    };
+    std::ostringstream l;
+    l << "  auto load_" << X << " = [&](int k0) {\n";
+    if (md == 0 || md == 1) {
+      l << "    #pragma unroll\n    for (int j = 0; j < " << BX << " * BK / 1024; j++) {\n";
+      if (md == 0) {
+        l << "      const int r = tid / 4 + 64 * j, kq = (tid % 4) * 4;\n";
+        l << "      const int gr = " << dim << "0 + r, gk = k0 + kq;\n";
+      } else {
+        l << "      const int kk = tid / (" << BX << " / 4) + (256 / (" << BX << " / 4)) * j, r = (tid % (" << BX
+          << " / 4)) * 4;\n";
+        l << "      const int gr = " << dim << "0 + r, gk = k0 + kk;\n";
+      }
+      l << "      float* dst = &r" << X << "[4*j];\n";
+      l << "      if (gr < " << ext << " && gk < K_) {\n" << body("dst", md == 0, md == 1) << "      } else {\n";
+      l << "        dst[0] = 0.0f; dst[1] = 0.0f; dst[2] = 0.0f; dst[3] = 0.0f;\n      }\n    }\n";
+    } else {
+      l << "    #pragma unroll\n    for (int e = 0; e < " << BX << " * BK / 256; e++) {\n";
+      if (k_fast) l << "      const int i = tid + 256 * e, r = i / BK, kk = i % BK;\n";
+      else l << "      const int i = tid + 256 * e, kk = i / " << BX << ", r = i % " << BX << ";\n";
+      l << "      const int gr = " << dim << "0 + r, gk = k0 + kk;\n";
+      l << "      if (gr < " << ext << " && gk < K_) {\n" << body("r" + std::string(X) + "[e]", 0, 0)
+        << "      } else {\n        r" << X << "[e] = 0.0f;\n      }\n    }\n";
+    }
+    l << "  };\n";
+    l << "  auto store_" << X << " = [&](int buf) {\n";
+    const char* S = X[0] == 'a' ? "As" : "Bs";
+    if (md == 0) {
+      l << "    #pragma unroll\n    for (int j = 0; j < " << BX << " * BK / 1024; j++) {\n";
+      l << "      const int r = tid / 4 + 64 * j, kq = (tid % 4) * 4;\n";
+      l << "      #pragma unroll\n      for (int q = 0; q < 4; q++) " << S << "[buf][kq + q][r] = r" << X << "[4*j+q];\n    }\n";
+    } else if (md == 1) {
+      l << "    #pragma unroll\n    for (int j = 0; j < " << BX << " * BK / 1024; j++) {\n";
+      l << "      const int kk = tid / (" << BX << " / 4) + (256 / (" << BX << " / 4)) * j, r = (tid % (" << BX
+        << " / 4)) * 4;\n";
+      l << "      *(float4*)(&" << S << "[buf][kk][r]) = make_float4(r" << X << "[4*j], r" << X << "[4*j+1], r" << X
+        << "[4*j+2], r" << X << "[4*j+3]);\n    }\n";
+    } else {
+      l << "    #pragma unroll\n    for (int e = 0; e < " << BX << " * BK / 256; e++) {\n";
+      if (k_fast) l << "      const int i = tid + 256 * e, r = i / BK, kk = i % BK;\n";
+      else l << "      const int i = tid + 256 * e, kk = i / " << BX << ", r = i % " << BX << ";\n";
+      l << "      " << S << "[buf][kk][r] = r" << X << "[e];\n    }\n";
+    }
+    l << "  };\n";
+    return l.str();
+  };
+  s << loader("a", g.a, BM, M, "m");
+  s << loader("b", g.b, BN, N, "n");
+  s << R"(  const int KT = (K_ + BK - 1) / BK;
+  load_a(0); load_b(0);
+  store_a(0); store_b(0);
+  __syncthreads();
+  for (int kt = 0; kt < KT; kt++) {
+    const int cur = kt & 1;
+    if (kt + 1 < KT) { load_a((kt + 1) * BK); load_b((kt + 1) * BK); }
+    #pragma unroll
+    for (int kk = 0; kk < BK; kk += 2) {
+      const int kr = kk + (lane >> 5);
+      float af[TM], bf[TN];
+      #pragma unroll
+      for (int i = 0; i < TM; i++) af[i] = As[cur][kr][wm + i * 32 + (lane & 31)];
+      #pragma unroll
+      for (int j = 0; j < TN; j++) bf[j] = Bs[cur][kr][wn + j * 32 + (lane & 31)];
+      #pragma unroll
+      for (int i = 0; i < TM; i++)
+        #pragma unroll
+        for (int j = 0; j < TN; j++)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[i], bf[j], acc[i][j], 0, 0, 0);
+    }
+    if (kt + 1 < KT) { store_a(cur ^ 1); store_b(cur ^ 1); }
+    __syncthreads();
+  }
+  // 32x32 accumulator layout: element e of lane l is row 8*(e/4) + 4*(l/32) + e%4, column l%32.
+  #pragma unroll
+  for (int i = 0; i < TM; i++)
+    #pragma unroll
+    for (int j = 0; j < TN; j++)
+      #pragma unroll
+      for (int e = 0; e < 16; e++) {
+        const int grow = m0 + wm + i * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
+        const int gcol = n0 + wn + j * 32 + (lane & 31);
+        if (grow < M_ && gcol < N_) {
+          const float gacc = acc[i][j][e];
+)";
+  // Epilogue: everything outside the reduction, per output element.
+  Emitter em;
+  em.define_range(g.rm, "grow");
+  em.define_range(g.rn, "gcol");
+  em.reduce_cb_ = [&](const UOp& RR, int lane) -> std::string {
+    FG_CHECK(RR == g.R, "gemm epilogue sees one reduction");
+    (void)lane;
+    return "gacc";
+  };
+  std::string v = em.val(ki.value, 0);
+  em.line(pname(ki.out_param) + "[" + em.idx(ki.out_index, 0) + "] = " + v + ";");
+  std::istringstream is(em.code());
+  std::string l;
+  while (std::getline(is, l)) s << "        " << l << "\n";
+  s << "        }\n      }\n}\n";
+  RenderedKernel rk;
+  rk.name = name;
+  rk.kind = kernel_class_name(KernelClass::Gemm);
+  rk.source = s.str();
+  rk.block[0] = 256;
+  rk.grid[0] = static_cast<unsigned>(((M + BM - 1) / BM) * ((N + BN - 1) / BN));
+  return rk;
+}
+
+// Whether an in-place kernel reads its destination at an index other than
+// the one it stores to (the reference executes such a kernel sequentially).
+bool reads_dest_elsewhere(const KernelInfo& ki) {
+  for (auto& ld : loads_in(ki.value)) {
+    if (ld.src(0).src(0) != ki.out_param) continue;
+    if (ld.src(0).src(1) != ki.out_index) return true;
+  }
+  return false;
+}
+
+}  // namespace
+
+KernelClass classify_kernel(const UOp& kernel) {
+  KernelInfo ki = analyze_kernel(kernel);
+  if (ki.reduces.empty()) return KernelClass::Elementwise;
+  if (ki.reduces.size() > 1) return KernelClass::Serial;
+  GemmMatch g;
+  if (match_gemm(ki, &g)) return KernelClass::Gemm;
+  const UOp& R = ki.reduces[0];
+  // A reduction nested in another reduction's value renders serially.
+  for (auto& n : R.src(0).toposort())
+    if (n.op() == Op::Reduce) return KernelClass::Serial;
+  if (R.srcs().size() < 2) return KernelClass::Serial;
+  for (auto& ld : loads_in(R.src(0)))
+    if (!affine_of(ld.src(0).src(1)).ok) return KernelClass::Serial;
+  const UOp r_in = R.srcs().back();
+  UOp fast = pick_fast_output(ki);
+  int row = 0, col = 0;
+  for (auto& ld : loads_in(R.src(0))) {
+    Affine a = affine_of(ld.src(0).src(1));
+    if (a.coef(r_in) == 1) row++;
+    else if (fast && a.coef(fast) == 1) col++;
+  }
+  if (!fast || row >= col) return KernelClass::RowReduce;
+  if (R.srcs().size() == 2) return KernelClass::ColumnReduce;
+  return KernelClass::Serial;
+}
+
+RenderedKernel render_hip(const UOp& kernel, const std::string& name, int force_class) {
+  KernelInfo ki = analyze_kernel(kernel);
+  FG_CHECK(!reads_dest_elsewhere(ki),
+           "in-place update reads its destination at another index; the HIP device runs kernels in parallel and "
+           "cannot reproduce the sequential CPU order");
+  KernelClass k = force_class >= 0 ? static_cast<KernelClass>(force_class) : classify_kernel(kernel);
+  std::vector<std::pair<int, DType>> params;
+  for (auto& [slot, p] : ki.params) params.emplace_back(slot, p.dtype());
+  RenderedKernel rk;
+  switch (k) {
+    case KernelClass::Gemm: {
+      GemmMatch g;
+      FG_CHECK(match_gemm(ki, &g), "kernel does not match the MFMA GEMM pattern");
+      rk = render_gemm(ki, g, name);
+      break;
+    }
+    case KernelClass::Elementwise:
+      if (!ki.reduces.empty()) return render_hip(kernel, name, static_cast<int>(KernelClass::Serial));
+      rk = render_elementwise(ki, name);
+      break;
+    case KernelClass::RowReduce: rk = render_row_reduce(ki, name); break;
+    case KernelClass::ColumnReduce: rk = render_column_reduce(ki, name); break;
+    case KernelClass::Serial: rk = render_serial(ki, name); break;
+  }
+  rk.params = params;
+  return rk;
+}
+
+}  // namespace fg

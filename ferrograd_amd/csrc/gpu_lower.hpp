@@ -1,0 +1,50 @@
+// gfx950 lowering of rangeified kernels: kernel classification (the GPU
+// optimize passes) and HIP source generation (the HIP codegen target).
+#pragma once
+
+#include <map>
+#include <string>
+#include <vector>
+
+#include "device.hpp"
+#include "ir.hpp"
+
+namespace fg {
+
+// An int32 index expression as c0 + sum(coef * term), where each term is a
+// Range or a ParamScalar. Rangeify only builds Add/Mul/Const over those
+// (schedule/indexing.rs:42-62, 102-175), so every index is affine.
+struct Affine {
+  bool ok = true;
+  int64_t c0 = 0;
+  std::vector<std::pair<UOp, int64_t>> terms;
+  int64_t coef(const UOp& t) const;
+  bool has_scalar_terms() const;
+};
+Affine affine_of(const UOp& e);
+
+// The shape of one rangeified kernel: Sink(End(r0, ... End(rn, Store(idx, v)))).
+struct KernelInfo {
+  UOp store, out_index, value, out_param;
+  std::vector<UOp> out_ranges;  // outermost first
+  std::vector<int64_t> out_ext;
+  std::vector<UOp> reduces;     // Reduce nodes in the stored value
+  std::vector<std::pair<int, UOp>> params;  // slot -> ParamBuffer / ParamScalar
+};
+KernelInfo analyze_kernel(const UOp& sink);
+int64_t range_extent(const UOp& r);
+
+// Lowering classes, in the order they are tried.
+enum class KernelClass { Gemm, Elementwise, RowReduce, ColumnReduce, Serial };
+const char* kernel_class_name(KernelClass k);
+
+// Symbolic cleanup plus the GPU range retagging (size-1 reduce ranges become
+// the constant 0; output ranges become GLOBAL).
+UOp gpu_optimize(const UOp& rangeified);
+
+// Render a gfx950 HIP kernel (source + launch geometry) for an optimized
+// kernel. `force` selects a class for tests (Serial is always valid).
+RenderedKernel render_hip(const UOp& kernel, const std::string& name, int force_class = -1);
+KernelClass classify_kernel(const UOp& kernel);
+
+}  // namespace fg

@@ -1,0 +1,140 @@
+// The HIP device: implements the Device interface (src/device.rs:275-332) on
+// top of the C-ABI in include/ferrograd_hip.h, with the gfx950 lowering in
+// gpu_lower.cpp as its optimize/render stages.
+#include <cstdlib>
+#include <cstring>
+
+#include "../../include/ferrograd_hip.h"
+#include "device.hpp"
+#include "gpu_lower.hpp"
+
+namespace fg {
+
+namespace {
+
+void check(int rc, const char* what) {
+  if (rc != FG_OK) fail(std::string(what) + ": " + fg_hip_last_error());
+}
+
+struct HipProgram : Program {
+  fg_prog* prog = nullptr;
+  ~HipProgram() override { fg_hip_program_free(prog); }
+};
+
+class HipDevice : public Device {
+ public:
+  DeviceId id() const override { return DeviceId::Hip; }
+
+  fg_ctx* ctx() {
+    if (!ctx_) {
+      int ord = 0;
+      if (const char* e = std::getenv("FG_HIP_DEVICE")) ord = std::atoi(e);
+      check(fg_hip_init(ord, &ctx_), "fg_hip_init");
+    }
+    return ctx_;
+  }
+
+  Buffer allocate(DType dtype, size_t numel) override {  // cpu.rs:277-280 (zero-filled)
+    Buffer b = reserve_buffer(dtype, numel);
+    realize_storage(*b, true);
+    b->known_zero = true;
+    return b;
+  }
+
+  void realize_storage(BufferInner& b, bool zero) override {
+    if (b.realized) return;
+    void* p = nullptr;
+    check(fg_hip_alloc(ctx(), b.nbytes(), zero ? 1 : 0, &p), "fg_hip_alloc");
+    b.storage = p;
+    b.realized = true;
+  }
+
+  void release(BufferInner& b) override {
+    if (!b.realized || !ctx_) return;
+    fg_hip_free(ctx_, b.storage);
+    b.storage = nullptr;
+    b.realized = false;
+  }
+
+  void copy_from_host(const Buffer& b, const void* src, size_t nbytes) override {  // cpu.rs:282-302
+    FG_CHECK(b->device == DeviceId::Hip, "HIP backend received non-HIP buffer " + std::to_string(b->id));
+    b->ensure_allocated();
+    FG_CHECK(nbytes == b->nbytes(), "copy_from_host: expected " + std::to_string(b->nbytes()) + " bytes, got " +
+                                        std::to_string(nbytes));
+    check(fg_hip_copy_h2d(ctx(), b->storage, src, nbytes), "fg_hip_copy_h2d");
+    b->known_zero = false;
+  }
+
+  std::vector<uint8_t> copy_to_host(const Buffer& b) override {  // cpu.rs:304-316
+    FG_CHECK(b->device == DeviceId::Hip, "HIP backend received non-HIP buffer " + std::to_string(b->id));
+    FG_CHECK(b->realized, "copy_to_host called on unrealized or non-HIP buffer");
+    std::vector<uint8_t> out(b->nbytes());
+    check(fg_hip_copy_d2h(ctx(), out.data(), b->storage, out.size()), "fg_hip_copy_d2h");
+    return out;
+  }
+
+  UOp optimize(const UOp& rangeified) override { return gpu_optimize(rangeified); }
+
+  RenderedKernel render(const UOp& optimized, const std::string& name) override {
+    return render_hip(optimized, name);
+  }
+
+  std::shared_ptr<Program> compile(const RenderedKernel& rk, size_t num_args) override {
+    auto p = std::make_shared<HipProgram>();
+    FG_CHECK(rk.params.size() == num_args || rk.params.empty(),
+             "kernel declares " + std::to_string(rk.params.size()) + " parameters but is launched with " +
+                 std::to_string(num_args));
+    check(fg_hip_compile(ctx(), rk.source.c_str(), rk.name.c_str(), static_cast<int>(num_args), &p->prog),
+          "compile failed");
+    p->num_args = num_args;
+    p->meta = rk;
+    return p;
+  }
+
+  void execute(Program& prog, std::vector<KernelArg>& args) override {  // cpu.rs:328-380
+    auto& p = static_cast<HipProgram&>(prog);
+    FG_CHECK(args.size() == p.num_args,
+             "expected " + std::to_string(p.num_args) + " kernel args, got " + std::to_string(args.size()));
+    std::vector<fg_arg> a(args.size());
+    for (size_t i = 0; i < args.size(); i++) {
+      std::memset(&a[i], 0, sizeof(fg_arg));
+      switch (args[i].kind) {
+        case KernelArg::Kind::Buffer:
+          FG_CHECK(args[i].buffer->device == DeviceId::Hip && args[i].buffer->realized,
+                   "HIP backend received unrealized or non-HIP buffer");
+          a[i].kind = FG_ARG_PTR;
+          a[i].v.p = args[i].buffer->storage;
+          break;
+        case KernelArg::Kind::I32: a[i].kind = FG_ARG_I32; a[i].v.i = args[i].i; break;
+        case KernelArg::Kind::F32: a[i].kind = FG_ARG_F32; a[i].v.f = args[i].f; break;
+        case KernelArg::Kind::Bool: a[i].kind = FG_ARG_BOOL; a[i].v.b = args[i].b ? 1 : 0; break;
+      }
+    }
+    check(fg_hip_launch(ctx(), p.prog, a.data(), static_cast<int>(a.size()), p.meta.grid, p.meta.block,
+                        p.meta.lds_bytes),
+          "execution failed");
+  }
+
+  void synchronize() override {
+    if (ctx_) check(fg_hip_sync(ctx_), "fg_hip_sync");
+  }
+
+  bool fuse_elementwise() const override {
+    const char* e = std::getenv("FG_FUSE");
+    return !(e && std::strcmp(e, "0") == 0);
+  }
+
+ private:
+  fg_ctx* ctx_ = nullptr;
+};
+
+}  // namespace
+
+Device* make_hip_device() { return new HipDevice(); }
+
+fg_ctx* hip_context() {
+  auto& d = static_cast<HipDevice&>(get_device(DeviceId::Hip));
+  return d.ctx();
+}
+
+}  // namespace fg

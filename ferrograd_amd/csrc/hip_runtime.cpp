@@ -1,0 +1,380 @@
+// HIP runtime behind the C-ABI in include/ferrograd_hip.h: hiprtc compile with
+// an on-disk code-object cache, module load, kernel launch, a size-keyed
+// caching allocator and host copies. Replaces src/device/cpu.rs:151-394
+// (clang subprocess + dlopen + libffi) for the MI355X.
+#include <dlfcn.h>
+#include <hip/hip_runtime.h>
+#include <hip/hiprtc.h>
+#include <sys/stat.h>
+#include <unistd.h>
+
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <fstream>
+#include <mutex>
+#include <sstream>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+#include "../../include/ferrograd_hip.h"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int set_err(int code, const std::string& msg) {
+  g_last_error = msg;
+  return code;
+}
+
+#define HIP_TRY(expr)                                                                            \
+  do {                                                                                           \
+    hipError_t _e = (expr);                                                                      \
+    if (_e != hipSuccess)                                                                        \
+      return set_err(FG_ERR_HIP, std::string(#expr) + ": " + hipGetErrorString(_e));             \
+  } while (0)
+
+// Options every generated kernel is compiled with. -ffp-contract=off keeps each
+// product and sum separately rounded, as the reference's one-statement-per-op C
+// is (codegen/clang.rs:203-239). Packed fp32 instructions are disabled.
+const char* kRtcOptions[] = {"--offload-arch=gfx950", "-O3", "-ffp-contract=off", "-Xclang", "-target-feature",
+                             "-Xclang", "-packed-fp32-ops", "-std=c++17"};
+constexpr int kNumRtcOptions = sizeof(kRtcOptions) / sizeof(kRtcOptions[0]);
+
+uint64_t fnv1a(const std::string& s, uint64_t h = 1469598103934665603ULL) {
+  for (unsigned char c : s) {
+    h ^= c;
+    h *= 1099511628211ULL;
+  }
+  return h;
+}
+
+void cache_anchor() {}
+
+// Code objects live in `_kcache/` next to this shared library unless
+// FG_KERNEL_CACHE names another directory.
+std::string cache_dir() {
+  if (const char* e = std::getenv("FG_KERNEL_CACHE")) return e;
+  static std::string dir = [] {
+    Dl_info info;
+    std::string d = "/tmp";
+    if (dladdr(reinterpret_cast<void*>(&cache_anchor), &info) && info.dli_fname) {
+      std::string f = info.dli_fname;
+      auto pos = f.rfind('/');
+      if (pos != std::string::npos) d = f.substr(0, pos);
+    }
+    return d + "/_kcache";
+  }();
+  return dir;
+}
+
+bool read_file(const std::string& path, std::vector<char>* out) {
+  std::ifstream f(path, std::ios::binary);
+  if (!f) return false;
+  f.seekg(0, std::ios::end);
+  auto n = f.tellg();
+  if (n <= 0) return false;
+  out->resize(static_cast<size_t>(n));
+  f.seekg(0);
+  f.read(out->data(), n);
+  return static_cast<bool>(f);
+}
+
+void write_file_atomic(const std::string& path, const std::vector<char>& data) {
+  std::string tmp = path + ".tmp" + std::to_string(getpid());
+  {
+    std::ofstream f(tmp, std::ios::binary);
+    if (!f) return;
+    f.write(data.data(), static_cast<std::streamsize>(data.size()));
+    if (!f) return;
+  }
+  std::rename(tmp.c_str(), path.c_str());
+}
+
+}  // namespace
+
+struct fg_prog {
+  hipModule_t module = nullptr;
+  hipFunction_t func = nullptr;
+  int num_args = 0;
+  std::string name;
+};
+
+struct fg_ctx {
+  int device = 0;
+  hipStream_t stream = nullptr;
+  hipEvent_t events[64] = {};
+  // Caching allocator: exact-size free lists. Blocks are only reused by work
+  // queued later on the same stream, so reuse needs no synchronisation.
+  std::unordered_map<size_t, std::vector<void*>> free_blocks;
+  std::unordered_map<void*, size_t> sizes;
+  size_t cached_bytes = 0;
+  // Pinned staging for small host->device copies, used as a ring: a region is
+  // reused only after the stream has passed the copy that read it.
+  char* staging = nullptr;
+  size_t staging_size = 0;
+  size_t staging_head = 0;
+  hipEvent_t staging_event = nullptr;
+  bool staging_event_pending = false;
+};
+
+namespace {
+constexpr size_t kAllocGranule = 256;
+constexpr size_t kSmallCopy = 1 << 16;
+constexpr size_t kStagingBytes = 8 << 20;
+constexpr size_t kMaxCachedBytes = size_t(96) << 30;
+
+size_t round_up(size_t n) { return (n + kAllocGranule - 1) / kAllocGranule * kAllocGranule; }
+}  // namespace
+
+extern "C" {
+
+const char* fg_hip_last_error(void) { return g_last_error.c_str(); }
+
+int fg_hip_init(int ordinal, fg_ctx** out) {
+  if (!out) return set_err(FG_ERR_INVALID, "fg_hip_init: null out");
+  int count = 0;
+  HIP_TRY(hipGetDeviceCount(&count));
+  if (ordinal < 0 || ordinal >= count)
+    return set_err(FG_ERR_INVALID, "fg_hip_init: device ordinal " + std::to_string(ordinal) + " out of range (" +
+                                       std::to_string(count) + " devices)");
+  HIP_TRY(hipSetDevice(ordinal));
+  auto* c = new fg_ctx();
+  c->device = ordinal;
+  hipError_t e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking);
+  if (e != hipSuccess) {
+    delete c;
+    return set_err(FG_ERR_HIP, std::string("hipStreamCreate: ") + hipGetErrorString(e));
+  }
+  for (auto& ev : c->events) HIP_TRY(hipEventCreate(&ev));
+  HIP_TRY(hipEventCreateWithFlags(&c->staging_event, hipEventDisableTiming));
+  HIP_TRY(hipHostMalloc(reinterpret_cast<void**>(&c->staging), kStagingBytes, hipHostMallocDefault));
+  c->staging_size = kStagingBytes;
+  *out = c;
+  return FG_OK;
+}
+
+int fg_hip_destroy(fg_ctx* c) {
+  if (!c) return FG_OK;
+  hipStreamSynchronize(c->stream);
+  fg_hip_trim(c);
+  for (auto& ev : c->events) hipEventDestroy(ev);
+  hipEventDestroy(c->staging_event);
+  hipHostFree(c->staging);
+  hipStreamDestroy(c->stream);
+  delete c;
+  return FG_OK;
+}
+
+int fg_hip_alloc(fg_ctx* c, size_t nbytes, int zero, void** dptr) {
+  if (!c || !dptr) return set_err(FG_ERR_INVALID, "fg_hip_alloc: null argument");
+  size_t sz = round_up(nbytes == 0 ? 1 : nbytes);
+  void* p = nullptr;
+  auto it = c->free_blocks.find(sz);
+  if (it != c->free_blocks.end() && !it->second.empty()) {
+    p = it->second.back();
+    it->second.pop_back();
+    c->cached_bytes -= sz;
+  } else {
+    hipError_t e = hipMalloc(&p, sz);
+    if (e != hipSuccess) {
+      // Give cached blocks back and retry once.
+      hipStreamSynchronize(c->stream);
+      fg_hip_trim(c);
+      HIP_TRY(hipMalloc(&p, sz));
+    }
+    c->sizes[p] = sz;
+  }
+  if (zero) HIP_TRY(hipMemsetAsync(p, 0, sz, c->stream));
+  *dptr = p;
+  return FG_OK;
+}
+
+int fg_hip_free(fg_ctx* c, void* p) {
+  if (!c) return set_err(FG_ERR_INVALID, "fg_hip_free: null context");
+  if (!p) return FG_OK;
+  auto it = c->sizes.find(p);
+  if (it == c->sizes.end()) return set_err(FG_ERR_INVALID, "fg_hip_free: pointer was not allocated by fg_hip_alloc");
+  size_t sz = it->second;
+  if (c->cached_bytes + sz > kMaxCachedBytes) {
+    HIP_TRY(hipStreamSynchronize(c->stream));
+    c->sizes.erase(it);
+    HIP_TRY(hipFree(p));
+    return FG_OK;
+  }
+  c->free_blocks[sz].push_back(p);
+  c->cached_bytes += sz;
+  return FG_OK;
+}
+
+int fg_hip_trim(fg_ctx* c) {
+  if (!c) return FG_OK;
+  HIP_TRY(hipStreamSynchronize(c->stream));
+  for (auto& kv : c->free_blocks) {
+    for (void* p : kv.second) {
+      c->sizes.erase(p);
+      HIP_TRY(hipFree(p));
+    }
+  }
+  c->free_blocks.clear();
+  c->cached_bytes = 0;
+  return FG_OK;
+}
+
+int fg_hip_copy_h2d(fg_ctx* c, void* dst, const void* src, size_t n) {
+  if (!c || (!dst && n) || (!src && n)) return set_err(FG_ERR_INVALID, "fg_hip_copy_h2d: null argument");
+  if (n == 0) return FG_OK;
+  if (n <= kSmallCopy) {
+    // Stage through pinned memory so the copy can stay asynchronous.
+    if (c->staging_head + n > c->staging_size) {
+      if (c->staging_event_pending) HIP_TRY(hipEventSynchronize(c->staging_event));
+      c->staging_head = 0;
+    }
+    char* s = c->staging + c->staging_head;
+    std::memcpy(s, src, n);
+    c->staging_head = (c->staging_head + n + 255) / 256 * 256;
+    HIP_TRY(hipMemcpyAsync(dst, s, n, hipMemcpyHostToDevice, c->stream));
+    HIP_TRY(hipEventRecord(c->staging_event, c->stream));
+    c->staging_event_pending = true;
+    return FG_OK;
+  }
+  HIP_TRY(hipMemcpyAsync(dst, src, n, hipMemcpyHostToDevice, c->stream));
+  HIP_TRY(hipStreamSynchronize(c->stream));
+  return FG_OK;
+}
+
+int fg_hip_copy_d2h(fg_ctx* c, void* dst, const void* src, size_t n) {
+  if (!c || (!dst && n) || (!src && n)) return set_err(FG_ERR_INVALID, "fg_hip_copy_d2h: null argument");
+  if (n == 0) return fg_hip_sync(c);
+  HIP_TRY(hipMemcpyAsync(dst, src, n, hipMemcpyDeviceToHost, c->stream));
+  HIP_TRY(hipStreamSynchronize(c->stream));
+  return FG_OK;
+}
+
+int fg_hip_copy_d2d(fg_ctx* c, void* dst, const void* src, size_t n) {
+  if (!c) return set_err(FG_ERR_INVALID, "fg_hip_copy_d2d: null context");
+  if (n == 0) return FG_OK;
+  HIP_TRY(hipMemcpyAsync(dst, src, n, hipMemcpyDeviceToDevice, c->stream));
+  return FG_OK;
+}
+
+int fg_hip_compile(fg_ctx* c, const char* source, const char* func, int num_args, fg_prog** out) {
+  if (!source || !func || !out) return set_err(FG_ERR_INVALID, "fg_hip_compile: null argument");
+  std::string src(source);
+  std::string key_material = src;
+  for (int i = 0; i < kNumRtcOptions; i++) key_material += std::string("\n") + kRtcOptions[i];
+  char hex[32];
+  std::snprintf(hex, sizeof(hex), "%016llx", static_cast<unsigned long long>(fnv1a(key_material)));
+  std::string dir = cache_dir();
+  std::string path = dir + "/" + hex + ".co";
+  std::vector<char> code;
+  if (!read_file(path, &code)) {
+    hiprtcProgram prog;
+    hiprtcResult r = hiprtcCreateProgram(&prog, source, (std::string(func) + ".hip").c_str(), 0, nullptr, nullptr);
+    if (r != HIPRTC_SUCCESS) return set_err(FG_ERR_COMPILE, std::string("hiprtcCreateProgram: ") + hiprtcGetErrorString(r));
+    r = hiprtcCompileProgram(prog, kNumRtcOptions, kRtcOptions);
+    if (r != HIPRTC_SUCCESS) {
+      size_t ls = 0;
+      hiprtcGetProgramLogSize(prog, &ls);
+      std::string log(ls, '\0');
+      if (ls) hiprtcGetProgramLog(prog, &log[0]);
+      hiprtcDestroyProgram(&prog);
+      return set_err(FG_ERR_COMPILE, "hiprtc compilation failed:\n" + log);
+    }
+    size_t cs = 0;
+    hiprtcGetCodeSize(prog, &cs);
+    code.resize(cs);
+    hiprtcGetCode(prog, code.data());
+    hiprtcDestroyProgram(&prog);
+    mkdir(dir.c_str(), 0755);
+    write_file_atomic(path, code);
+  }
+  if (!c) {
+    // Compile-only use (no device): the code object is now cached.
+    *out = nullptr;
+    return FG_OK;
+  }
+  auto* p = new fg_prog();
+  p->num_args = num_args;
+  p->name = func;
+  hipError_t e = hipModuleLoadData(&p->module, code.data());
+  if (e != hipSuccess) {
+    delete p;
+    return set_err(FG_ERR_HIP, std::string("hipModuleLoadData: ") + hipGetErrorString(e));
+  }
+  e = hipModuleGetFunction(&p->func, p->module, func);
+  if (e != hipSuccess) {
+    hipModuleUnload(p->module);
+    delete p;
+    return set_err(FG_ERR_SYMBOL, std::string("symbol '") + func + "' not found: " + hipGetErrorString(e));
+  }
+  *out = p;
+  return FG_OK;
+}
+
+int fg_hip_program_free(fg_prog* p) {
+  if (!p) return FG_OK;
+  if (p->module) hipModuleUnload(p->module);
+  delete p;
+  return FG_OK;
+}
+
+int fg_hip_program_num_args(const fg_prog* p) { return p ? p->num_args : -1; }
+
+int fg_hip_launch(fg_ctx* c, fg_prog* p, const fg_arg* args, int nargs, const unsigned grid[3],
+                  const unsigned block[3], unsigned lds) {
+  if (!c || !p || !grid || !block) return set_err(FG_ERR_INVALID, "fg_hip_launch: null argument");
+  if (nargs != p->num_args)
+    return set_err(FG_ERR_ARGS, "expected " + std::to_string(p->num_args) + " kernel args, got " + std::to_string(nargs));
+  if (block[0] * block[1] * block[2] == 0 || block[0] * block[1] * block[2] > 1024)
+    return set_err(FG_ERR_INVALID, "fg_hip_launch: block size must be in [1, 1024]");
+  if (grid[0] == 0 || grid[1] == 0 || grid[2] == 0) return set_err(FG_ERR_INVALID, "fg_hip_launch: empty grid");
+  void* params[64];
+  if (nargs > 64) return set_err(FG_ERR_ARGS, "fg_hip_launch: at most 64 arguments");
+  for (int i = 0; i < nargs; i++) {
+    switch (args[i].kind) {
+      case FG_ARG_PTR: params[i] = const_cast<void**>(&args[i].v.p); break;
+      case FG_ARG_I32: params[i] = const_cast<int32_t*>(&args[i].v.i); break;
+      case FG_ARG_F32: params[i] = const_cast<float*>(&args[i].v.f); break;
+      case FG_ARG_BOOL: params[i] = const_cast<uint8_t*>(&args[i].v.b); break;
+      default: return set_err(FG_ERR_ARGS, "fg_hip_launch: unknown argument kind " + std::to_string(args[i].kind));
+    }
+  }
+  HIP_TRY(hipModuleLaunchKernel(p->func, grid[0], grid[1], grid[2], block[0], block[1], block[2], lds, c->stream,
+                                params, nullptr));
+  return FG_OK;
+}
+
+int fg_hip_sync(fg_ctx* c) {
+  if (!c) return set_err(FG_ERR_INVALID, "fg_hip_sync: null context");
+  HIP_TRY(hipStreamSynchronize(c->stream));
+  return FG_OK;
+}
+
+int fg_hip_event_record(fg_ctx* c, int slot) {
+  if (!c || slot < 0 || slot >= 64) return set_err(FG_ERR_INVALID, "fg_hip_event_record: bad slot");
+  HIP_TRY(hipEventRecord(c->events[slot], c->stream));
+  return FG_OK;
+}
+
+int fg_hip_event_elapsed_ms(fg_ctx* c, int a, int b, float* ms) {
+  if (!c || a < 0 || a >= 64 || b < 0 || b >= 64 || !ms) return set_err(FG_ERR_INVALID, "fg_hip_event_elapsed_ms: bad slot");
+  HIP_TRY(hipEventSynchronize(c->events[b]));
+  HIP_TRY(hipEventElapsedTime(ms, c->events[a], c->events[b]));
+  return FG_OK;
+}
+
+int fg_hip_device_info(fg_ctx* c, int* cu, int* clk, size_t* lds, char* arch, size_t arch_len) {
+  if (!c) return set_err(FG_ERR_INVALID, "fg_hip_device_info: null context");
+  hipDeviceProp_t p;
+  HIP_TRY(hipGetDeviceProperties(&p, c->device));
+  if (cu) *cu = p.multiProcessorCount;
+  if (clk) *clk = p.clockRate;
+  if (lds) *lds = p.sharedMemPerBlock;
+  if (arch && arch_len) std::snprintf(arch, arch_len, "%s", p.gcnArchName);
+  return FG_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,483 @@
+// Kernel partitioning and rangeify.
+// schedule_many/should_materialize/parameterize*: src/schedule.rs:64-405.
+// rangeify + index pushing: src/schedule/rangeify.rs:42-206,
+// src/schedule/indexing.rs:22-242.
+#include "schedule.hpp"
+
+#include <algorithm>
+
+namespace fg {
+
+namespace {
+
+KernelArg scalar_input(const Arg& lit) {  // schedule.rs:247-257
+  switch (lit.kind) {
+    case Arg::Kind::Float: return KernelArg::f32(static_cast<float>(lit.f));
+    case Arg::Kind::Int:
+      FG_CHECK(lit.a >= INT32_MIN && lit.a <= INT32_MAX, "kernel scalar int must fit in i32");
+      return KernelArg::i32(static_cast<int32_t>(lit.a));
+    case Arg::Kind::Bool: return KernelArg::boolean(lit.a != 0);
+    default: fail("kernel scalar input must be a literal");
+  }
+}
+
+// schedule.rs:176-245. Replaces Buffers, Binds and constant Shrink starts with
+// numbered parameters; the output (if any) owns slot 0.
+std::pair<UOp, std::vector<KernelArg>> parameterize_inputs(const UOp& root, size_t slot_offset,
+                                                           const ScheduleOptions& opt) {
+  DeviceId device = root.device();
+  std::vector<KernelArg> inputs;
+  std::unordered_map<const BufferInner*, UOp> params;
+  UOpMap<UOp> scalar_params;
+  auto fn = [&](const UOp& node) -> UOp {
+    switch (node.op()) {
+      case Op::Buffer: {
+        const Buffer& h = node.arg().buf;
+        if (!h) return UOp();
+        if (opt.fuse && h->known_zero && node.dtype() == DType::F32()) {
+          // A buffer that still holds allocate()'s zeros reads as 0.0f at
+          // every index: the literal is the same value without the load.
+          UOp zero = UOp::make(Op::Const, node.dtype(), {UOp::device_uop(device)}, Arg::flt(0.0),
+                               true, kZeroBufferTag);
+          UOp base = UOp::reshape(zero, Shape{1});
+          if (h->numel == 1) return base;
+          return UOp::expand(base, Shape{h->numel});
+        }
+        auto it = params.find(h.get());
+        if (it != params.end()) return it->second;
+        size_t slot = inputs.size() + slot_offset;
+        inputs.push_back(KernelArg::buf(h));
+        UOp p = UOp::param_buffer(static_cast<int64_t>(slot), node.dtype(),
+                                  static_cast<int64_t>(h->numel), device);
+        params.emplace(h.get(), p);
+        return p;
+      }
+      case Op::Bind: {
+        const UOp& var = node.src(0);
+        auto it = scalar_params.find(var);
+        if (it != scalar_params.end()) return it->second;
+        size_t slot = inputs.size() + slot_offset;
+        inputs.push_back(scalar_input(node.src(1).arg()));
+        UOp p = UOp::param_scalar(static_cast<int64_t>(slot), node.dtype(), device);
+        scalar_params.emplace(var, p);
+        return p;
+      }
+      case Op::Shrink: {
+        Shape src_shape;
+        if (!node.src(0).shape_opt(&src_shape)) return UOp();
+        const auto& lens = node.arg().v;
+        bool changed = false;
+        std::vector<UOp> ns{node.src(0)};
+        for (size_t ax = 0; ax + 1 < node.srcs().size() && ax < lens.size(); ax++) {
+          const UOp& start = node.src(ax + 1);
+          if (static_cast<size_t>(lens[ax]) != src_shape[ax] && start.op() == Op::Const) {
+            size_t slot = inputs.size() + slot_offset;
+            inputs.push_back(scalar_input(start.arg()));
+            ns.push_back(UOp::param_scalar(static_cast<int64_t>(slot), start.dtype(), device));
+            changed = true;
+            continue;
+          }
+          ns.push_back(start);
+        }
+        for (size_t i = ns.size(); i < node.srcs().size(); i++) ns.push_back(node.src(i));
+        if (!changed) return UOp();
+        return UOp::make_new(Op::Shrink, node.dtype(), ns, node.arg());
+      }
+      default:
+        return UOp();
+    }
+  };
+  UOp out = graph_rewrite(root, fn);
+  return {out, inputs};
+}
+
+// schedule.rs:131-151
+ScheduleItem parameterize(const UOp& expr, const ScheduleOptions& opt) {
+  Device& backend = get_device(expr.device());
+  auto [p, inputs] = parameterize_inputs(expr, 1, opt);
+  Shape out_shape;
+  if (!p.shape_opt(&out_shape)) out_shape = Shape{1};
+  Buffer out = backend.reserve_buffer(expr.dtype(), numel(out_shape));
+  UOp out_param = UOp::param_buffer(0, expr.dtype(), static_cast<int64_t>(numel(out_shape)), expr.device());
+  UOp store = UOp::make_new(Op::Store, DType::Void(), {out_param, p}, Arg::none());
+  ScheduleItem item;
+  item.sink = UOp::sink({store});
+  item.inputs = std::move(inputs);
+  item.output_buffer = out;
+  item.out_shape = out_shape;
+  return item;
+}
+
+// schedule.rs:264-272
+UOpSet nested_reduce_inputs(const std::vector<UOp>& order) {
+  UOpSet feeds;
+  for (size_t i = order.size(); i-- > 0;) {
+    const UOp& n = order[i];
+    if (n.op() == Op::ReduceAxis || feeds.count(n))
+      for (auto& s : n.srcs()) feeds.insert(s);
+  }
+  return feeds;
+}
+
+// Reconvergence test for value-preserving fusion: every consumer path out of
+// `node` runs through elementwise nodes of the same shape and ends in one
+// elementwise node `d`, so computing `node` inside `d`'s kernel reads each
+// input element once (identical loads intern to one node).
+bool reconverges(const UOp& node, const UOpMap<std::vector<UOp>>& consumers, const UOpSet& roots,
+                 const UOpMap<size_t>& topo_idx) {
+  if (!is_alu(node.op())) return false;
+  Shape s;
+  if (!node.shape_opt(&s)) return false;
+  auto it = consumers.find(node);
+  if (it == consumers.end() || it->second.size() < 2) return false;
+  // Candidate: the latest consumer in topological order.
+  UOp d;
+  size_t best = 0;
+  for (auto& c : it->second) {
+    size_t k = topo_idx.at(c);
+    if (!d || k > best) { d = c; best = k; }
+  }
+  if (!is_alu(d.op())) return false;
+  Shape ds;
+  if (!d.shape_opt(&ds) || ds != s) return false;
+  // Every other consumer must flow only into d (or into nodes that do), via
+  // single-purpose elementwise nodes of the same shape, within a small depth.
+  std::function<bool(const UOp&, int)> flows_to_d = [&](const UOp& c, int depth) -> bool {
+    if (c == d) return true;
+    if (depth > 4 || roots.count(c) || !is_alu(c.op())) return false;
+    Shape cs;
+    if (!c.shape_opt(&cs) || cs != s) return false;
+    auto ci = consumers.find(c);
+    if (ci == consumers.end() || ci->second.empty()) return false;
+    for (auto& cc : ci->second)
+      if (!flows_to_d(cc, depth + 1)) return false;
+    return true;
+  };
+  for (auto& c : it->second)
+    if (!flows_to_d(c, 0)) return false;
+  return true;
+}
+
+// schedule.rs:289-335
+bool should_materialize(const UOp& node, const UOpSet& roots,
+                        const UOpMap<std::vector<UOp>>& consumers, const UOpSet& nested,
+                        const ScheduleOptions& opt, const UOpMap<size_t>& topo_idx) {
+  if (roots.count(node) || !node.has_shape()) return false;
+  switch (node.op()) {
+    case Op::Sink: case Op::Store: case Op::After: case Op::Assign: case Op::DefineAcc:
+    case Op::Buffer: case Op::Const: case Op::DefineVar: case Op::Bind:
+      return false;
+    default: break;
+  }
+  if (node.op() == Op::Contiguous) return true;
+  if (is_movement(node.op())) return false;
+  if (node.has_buffer_identity()) return false;
+  auto it = consumers.find(node);
+  if (it != consumers.end() && it->second.size() > 1) {
+    if (opt.fuse && reconverges(node, consumers, roots, topo_idx)) return false;
+    return true;
+  }
+  if (node.op() == Op::ReduceAxis && it != consumers.end()) {
+    for (auto& c : it->second)
+      if (is_alu(c.op())) return true;
+  }
+  return node.op() == Op::ReduceAxis && nested.count(node);
+}
+
+// schedule.rs:340-353
+UOp buffer_replacement(const ScheduleItem& item) {
+  FG_CHECK(item.output_buffer, "buffer_replacement requires an allocated output");
+  UOp b = UOp::buffer(item.output_buffer, item.output_buffer->dtype, item.sink.device());
+  return UOp::reshape(b, item.out_shape);
+}
+
+// schedule.rs:359-365
+bool assignment_effect(const UOp& root, UOp* store, UOp* value) {
+  if (root.op() != Op::After || root.srcs().size() != 2) return false;
+  if (root.src(1).op() != Op::Store) return false;
+  *store = root.src(1);
+  *value = root.src(0);
+  return true;
+}
+
+// schedule.rs:371-405
+UOp substitute_materialized(const UOp& root, const UOpMap<UOp>& replacements) {
+  auto order = root.toposort();
+  UOpMap<UOp> sub;
+  for (auto& node : order) {
+    if (node != root) {
+      auto r = replacements.find(node);
+      if (r != replacements.end()) {
+        sub[node] = r->second;
+        continue;
+      }
+    }
+    std::vector<UOp> ns;
+    bool changed = false;
+    for (auto& s : node.srcs()) {
+      auto it = sub.find(s);
+      ns.push_back(it == sub.end() ? s : it->second);
+      changed = changed || ns.back() != s;
+    }
+    sub[node] = changed ? (node.op() == Op::Sink ? UOp::sink(ns)
+                                                 : UOp::make_new(node.op(), node.dtype(), ns, node.arg()))
+                        : node;
+  }
+  auto it = sub.find(root);
+  return it == sub.end() ? root : it->second;
+}
+
+// Marks the store destination's buffer as written (it no longer holds zeros).
+void mark_written(const UOp& dest) {
+  UOp d = dest;
+  while (d && d.op() != Op::Buffer) {
+    if (d.srcs().empty()) return;
+    d = d.src(0);
+  }
+  if (d && d.arg().buf) d.arg().buf->known_zero = false;
+}
+
+}  // namespace
+
+// schedule.rs:156-170
+ScheduleItem parameterize_store(const UOp& store, const ScheduleOptions& opt) {
+  FG_CHECK(store.op() == Op::Store, "parameterize_store requires a Store root");
+  // The destination is about to be written: it must not fold to zeros in this
+  // kernel or any kernel scheduled after it.
+  mark_written(store.src(0));
+  auto [p, inputs] = parameterize_inputs(store, 0, opt);
+  ScheduleItem item;
+  item.sink = UOp::sink({p});
+  item.inputs = std::move(inputs);
+  return item;
+}
+
+// schedule.rs:64-126
+SchedulePlan schedule_many(const std::vector<UOp>& exprs, const ScheduleOptions& opt) {
+  FG_CHECK(!exprs.empty(), "schedule_many requires at least one root");
+  UOp uni = UOp::sink(exprs);
+  auto order = uni.toposort();
+  auto consumers = build_consumer_map(order);
+  auto nested = nested_reduce_inputs(order);
+  UOpSet roots(exprs.begin(), exprs.end());
+  UOpMap<size_t> topo_idx;
+  for (size_t i = 0; i < order.size(); i++) topo_idx[order[i]] = i;
+
+  SchedulePlan plan;
+  for (auto& node : order) {
+    if (!should_materialize(node, roots, consumers, nested, opt, topo_idx)) continue;
+    UOp kexpr = substitute_materialized(node, plan.replacements);
+    ScheduleItem item = parameterize(kexpr, opt);
+    plan.replacements[node] = buffer_replacement(item);
+    plan.items.push_back(std::move(item));
+  }
+  for (auto& expr : exprs) {
+    UOp fin = substitute_materialized(expr, plan.replacements);
+    UOp store, value;
+    if (assignment_effect(fin, &store, &value)) {
+      plan.items.push_back(parameterize_store(store, opt));
+      plan.replacements[expr] = value;
+    } else {
+      ScheduleItem item = parameterize(fin, opt);
+      plan.replacements[expr] = buffer_replacement(item);
+      plan.items.push_back(std::move(item));
+    }
+  }
+  return plan;
+}
+
+std::vector<ScheduleItem> schedule(const UOp& expr, const ScheduleOptions& opt) {
+  return schedule_many({expr}, opt).items;
+}
+
+// ── rangeify ────────────────────────────────────────────────────────────────
+namespace {
+
+// indexing.rs:42-62
+UOp flat_index(const std::vector<UOp>& idxs, const std::vector<size_t>& strides) {
+  FG_CHECK(idxs.size() == strides.size() && !idxs.empty(), "flat_index requires matching indices");
+  DeviceId d = idxs[0].device();
+  UOp acc;
+  for (size_t i = 0; i < idxs.size(); i++) {
+    if (strides[i] == 0) continue;
+    UOp term = strides[i] == 1
+                   ? idxs[i]
+                   : UOp::mul(idxs[i], UOp::const_int(static_cast<int64_t>(strides[i]), DType::I32(), idxs[i].device()));
+    acc = acc ? UOp::add(acc, term) : term;
+  }
+  return acc ? acc : UOp::const_int(0, DType::I32(), d);
+}
+
+UOp index_wrap(const UOp& src, const std::vector<UOp>& idxs) {  // indexing.rs:66-70
+  std::vector<UOp> s{src};
+  s.insert(s.end(), idxs.begin(), idxs.end());
+  return UOp::make_new(Op::Index, src.dtype(), s, Arg::none());
+}
+
+bool same_squeezed_dims(const Shape& a, const Shape& b) {  // indexing.rs:76-80
+  std::vector<size_t> x, y;
+  for (auto d : a) if (d != 1) x.push_back(d);
+  for (auto d : b) if (d != 1) y.push_back(d);
+  return x == y;
+}
+
+UOp rewrite_index_alu(const UOp& inner, const std::vector<UOp>& idxs) {  // indexing.rs:85-97
+  std::vector<UOp> ns;
+  for (auto& s : inner.srcs()) ns.push_back(index_wrap(s, idxs));
+  if (inner.has_tag()) return UOp::make(inner.op(), inner.dtype(), ns, inner.arg(), true, inner.tag());
+  return UOp::make_new(inner.op(), inner.dtype(), ns, inner.arg());
+}
+
+// indexing.rs:102-175
+UOp rewrite_index_movement(const UOp& inner, const std::vector<UOp>& idxs) {
+  const UOp& src = inner.src(0);
+  std::vector<UOp> ni;
+  switch (inner.op()) {
+    case Op::Shrink:
+      for (size_t ax = 0; ax < idxs.size(); ax++) {
+        const UOp& start = inner.src(ax + 1);
+        ni.push_back(start.is_zero() ? idxs[ax] : UOp::add(idxs[ax], start));
+      }
+      break;
+    case Op::Expand: {
+      Shape ss;
+      if (!src.shape_opt(&ss)) return UOp();
+      const auto& ex = inner.arg().v;
+      for (size_t ax = 0; ax < idxs.size(); ax++) {
+        if (ss[ax] == 1 && ex[ax] > 1) ni.push_back(UOp::const_int(0, DType::I32(), idxs[ax].device()));
+        else ni.push_back(idxs[ax]);
+      }
+      break;
+    }
+    case Op::Permute: {
+      auto inv = invert_permutation(inner.arg().usizes());
+      for (auto ax : inv) ni.push_back(idxs[ax]);
+      break;
+    }
+    case Op::Reshape: {
+      Shape ss;
+      if (!src.shape_opt(&ss)) return UOp();
+      Shape ds = inner.arg().usizes();
+      if (same_squeezed_dims(ss, ds)) {
+        std::vector<UOp> non1;
+        for (size_t i = 0; i < idxs.size(); i++) if (ds[i] != 1) non1.push_back(idxs[i]);
+        size_t next = 0;
+        for (auto d : ss) {
+          if (d == 1) ni.push_back(UOp::const_int(0, DType::I32(), src.device()));
+          else ni.push_back(non1[next++]);
+        }
+      } else {
+        ni.push_back(flat_index(idxs, contiguous_strides(ds)));
+      }
+      break;
+    }
+    case Op::Contiguous:
+      ni = idxs;
+      break;
+    default:
+      fail("rangeify only sends movement ops here");
+  }
+  return index_wrap(src, ni);
+}
+
+// indexing.rs:184-217
+UOp rewrite_index_reduce(const UOp& inner, const std::vector<UOp>& idxs) {
+  const UOp& src = inner.src(0);
+  Shape ss;
+  if (!src.shape_opt(&ss)) return UOp();
+  FG_CHECK(idxs.size() == ss.size(), "idxs should match source ndim");
+  const auto& axes = inner.arg().v;
+  std::vector<UOp> full, rr;
+  for (size_t ax = 0; ax < ss.size(); ax++) {
+    if (std::find(axes.begin(), axes.end(), static_cast<int64_t>(ax)) != axes.end()) {
+      UOp bound = UOp::const_int(static_cast<int64_t>(ss[ax]), DType::I32(), src.device());
+      UOp r = UOp::make_new(Op::Range, DType::I32(), {bound}, Arg::range(static_cast<int64_t>(ax), AxisKind::Reduce));
+      full.push_back(r);
+      rr.push_back(r);
+    } else {
+      full.push_back(idxs[ax]);
+    }
+  }
+  std::vector<UOp> srcs{index_wrap(src, full)};
+  srcs.insert(srcs.end(), rr.begin(), rr.end());
+  return UOp::make_new(Op::Reduce, inner.dtype(), srcs, Arg::reduce(inner.arg().rop, {}));
+}
+
+UOp rewrite_index_param(const UOp& inner, const std::vector<UOp>& idxs) {  // indexing.rs:233-242
+  FG_CHECK(idxs.size() == 1, "Param should have exactly one flat index");
+  UOp index = UOp::make_new(Op::Index, inner.dtype(), {inner, idxs[0]}, Arg::index(0));
+  return UOp::make_new(Op::Load, inner.dtype(), {index}, Arg::none());
+}
+
+UOp new_range(size_t axis, size_t size, DeviceId d) {  // rangeify.rs:42-52
+  if (size == 1) return UOp::const_int(0, DType::I32(), d);
+  return UOp::make_new(Op::Range, DType::I32(), {UOp::const_int(static_cast<int64_t>(size), DType::I32(), d)},
+                       Arg::range(static_cast<int64_t>(axis), AxisKind::Loop));
+}
+
+UOp chain_ends(const std::vector<UOp>& ranges, const UOp& body) {  // rangeify.rs:57-68
+  UOp cur = body;
+  for (size_t i = ranges.size(); i-- > 0;)
+    cur = UOp::make_new(Op::End, DType::Void(), {ranges[i], cur}, Arg::none());
+  return cur;
+}
+
+UOp store_output_index(const UOp& dest, const std::vector<UOp>& idxs) {  // rangeify.rs:75-96
+  if (dest.op() == Op::ParamBuffer || dest.op() == Op::Buffer) {
+    FG_CHECK(idxs.size() == 1, "store destination must be flattened before reaching ParamBuffer/Buffer");
+    return UOp::make_new(Op::Index, dest.dtype(), {dest, idxs[0]}, Arg::index(0));
+  }
+  if (is_movement(dest.op())) {
+    UOp moved = rewrite_index_movement(dest, idxs);
+    if (!moved) return UOp();
+    std::vector<UOp> rest(moved.srcs().begin() + 1, moved.srcs().end());
+    return store_output_index(moved.src(0), rest);
+  }
+  return UOp();
+}
+
+UOp rewrite_store_add_ranges(const UOp& store) {  // rangeify.rs:118-161
+  if (store.srcs().size() != 2) return UOp();
+  const UOp& out = store.src(0);
+  const UOp& expr = store.src(1);
+  Shape s;
+  if (!expr.shape_opt(&s)) return UOp();
+  DeviceId d = expr.device();
+  std::vector<UOp> ax;
+  for (size_t i = 0; i < s.size(); i++) ax.push_back(new_range(i, s[i], d));
+  UOp indexed = index_wrap(expr, ax);
+  UOp out_flat = flat_index(ax, contiguous_strides(s));
+  std::vector<UOp> out_ranges;
+  for (auto& r : ax) if (r.op() == Op::Range) out_ranges.push_back(r);
+  UOp out_idx = out.op() == Op::ParamBuffer
+                    ? UOp::make_new(Op::Index, out.dtype(), {out, out_flat}, Arg::index(0))
+                    : store_output_index(out, ax);
+  if (!out_idx) return UOp();
+  UOp ns = UOp::make_new(Op::Store, DType::Void(), {out_idx, indexed}, Arg::none());
+  return chain_ends(out_ranges, ns);
+}
+
+UOp rangeify_rule(const UOp& node) {  // rangeify.rs:173-194
+  if (node.op() == Op::Store) return rewrite_store_add_ranges(node);
+  if (node.op() == Op::Index && node.arg().kind == Arg::Kind::None) {
+    const UOp& inner = node.src(0);
+    std::vector<UOp> idxs(node.srcs().begin() + 1, node.srcs().end());
+    Op io = inner.op();
+    if (is_alu(io)) return rewrite_index_alu(inner, idxs);
+    switch (io) {
+      case Op::Expand: case Op::Permute: case Op::Reshape: case Op::Shrink: case Op::Contiguous:
+        return rewrite_index_movement(inner, idxs);
+      case Op::ReduceAxis: return rewrite_index_reduce(inner, idxs);
+      case Op::Const: case Op::ParamScalar: return inner;
+      case Op::ParamBuffer: return rewrite_index_param(inner, idxs);
+      default: return UOp();
+    }
+  }
+  return UOp();
+}
+
+}  // namespace
+
+UOp rangeify(const UOp& sink) { return graph_rewrite(sink, rangeify_rule); }
+
+}  // namespace fg

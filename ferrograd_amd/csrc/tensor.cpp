@@ -1,0 +1,697 @@
+// Tensor front end, realisation driver, autograd, Linear and SGD.
+// Follows src/tensor.rs, src/gradient.rs, src/nn.rs and src/optim.rs.
+#include "tensor.hpp"
+
+#include <chrono>
+#include <cmath>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <unordered_set>
+
+namespace fg {
+
+namespace {
+
+// tensor.rs:79-81 — weak handles to every live tensor.
+std::vector<std::weak_ptr<TensorInner>>& live_list() {
+  static auto* v = new std::vector<std::weak_ptr<TensorInner>>();
+  return *v;
+}
+
+size_t g_kernel_count = 0;  // tensor.rs:71
+
+// Lowering cache: scheduled kernel sink -> compiled program, per device. The
+// sink is interned, and rangeify/optimize/render are pure functions of it, so a
+// hit skips the host passes as well as the compile (the reference caches by
+// the lowered sink and re-runs the passes every realize: tensor.rs:804-846).
+UOpMap<std::shared_ptr<Program>>& lowering_cache(DeviceId d) {
+  static UOpMap<std::shared_ptr<Program>> caches[2];
+  return caches[static_cast<int>(d)];
+}
+
+}  // namespace
+
+RealizeStats& realize_stats() {
+  static RealizeStats s;
+  return s;
+}
+
+int debug_level() {  // tensor.rs:62-67
+  static int lvl = [] {
+    const char* e = std::getenv("DEBUG");
+    return e ? std::atoi(e) : 0;
+  }();
+  return lvl;
+}
+
+void clear_kernel_caches() {
+  for (int d = 0; d < 2; d++) {
+    lowering_cache(static_cast<DeviceId>(d)).clear();
+    if (has_device(static_cast<DeviceId>(d))) get_device(static_cast<DeviceId>(d)).clear_for_tests();
+  }
+}
+
+Tensor Tensor::from_uop(const UOp& u, bool rg) {  // tensor.rs:151-159
+  auto inner = std::make_shared<TensorInner>();
+  inner->uop = u;
+  inner->requires_grad = rg;
+  live_list().push_back(inner);
+  return Tensor(inner);
+}
+
+static std::vector<Tensor> live_tensors() {  // tensor.rs:201-214
+  std::vector<Tensor> out;
+  auto& l = live_list();
+  size_t w = 0;
+  for (size_t i = 0; i < l.size(); i++) {
+    if (auto p = l[i].lock()) {
+      out.emplace_back(p);
+      l[w++] = l[i];
+    }
+  }
+  l.resize(w);
+  return out;
+}
+
+UOp Tensor::uop() const { return p_->uop; }
+void Tensor::set_uop(const UOp& u) const { p_->uop = u; }
+
+// tensor.rs:222-252
+static void apply_map_to_tensors(const UOpMap<UOp>& replacements) {
+  if (replacements.empty()) return;
+  std::vector<std::pair<Tensor, UOp>> affected[2];
+  for (auto& t : live_tensors()) {
+    UOp cur = t.uop();
+    bool uses = false;
+    for (auto& n : cur.toposort())
+      if (replacements.count(n)) { uses = true; break; }
+    if (!uses) continue;
+    affected[static_cast<int>(cur.device())].emplace_back(t, cur);
+  }
+  for (auto& group : affected) {
+    if (group.empty()) continue;
+    std::vector<UOp> roots;
+    for (auto& [t, r] : group) roots.push_back(r);
+    UOp s = substitute_with_map(UOp::sink(roots), replacements);
+    for (size_t i = 0; i < group.size(); i++) {
+      const UOp& nr = s.src(i);
+      if (nr != group[i].second) group[i].first.set_uop(nr);
+    }
+  }
+}
+
+Tensor Tensor::from_bytes(const void* data, size_t nbytes, const Shape& shape, DType dtype, DeviceId dev) {
+  size_t n = fg::numel(shape);
+  FG_CHECK(nbytes == n * dtype.size_bytes(),
+           "data length " + std::to_string(nbytes / std::max<size_t>(1, dtype.size_bytes())) +
+               " doesn't match shape " + shape_str(shape));
+  Device& backend = get_device(dev);
+  Buffer b = backend.allocate(dtype, n);
+  backend.copy_from_host(b, data, nbytes);
+  return from_uop(UOp::reshape(UOp::buffer(b, dtype, dev), shape), false);
+}
+
+Tensor Tensor::new_f32(const std::vector<float>& data, const Shape& shape, DeviceId dev) {
+  return from_bytes(data.data(), data.size() * 4, shape, DType::F32(), dev);
+}
+
+Tensor Tensor::zeros(const Shape& shape, DeviceId dev, DType dtype) {  // tensor.rs:278-284
+  Device& backend = get_device(dev);
+  Buffer b = backend.allocate(dtype, fg::numel(shape));
+  return from_uop(UOp::reshape(UOp::buffer(b, dtype, dev), shape), false);
+}
+
+Tensor Tensor::ones(const Shape& shape, DeviceId dev, DType dtype) {  // tensor.rs:292-299
+  size_t n = fg::numel(shape);
+  switch (dtype.kind) {
+    case DTypeKind::F32: return full_f32(shape, 1.0f, dev);
+    case DTypeKind::I32: {
+      std::vector<int32_t> d(n, 1);
+      return from_bytes(d.data(), n * 4, shape, dtype, dev);
+    }
+    case DTypeKind::Bool: {
+      std::vector<uint8_t> d(n, 1);
+      return from_bytes(d.data(), n, shape, dtype, dev);
+    }
+    default: fail("ones requires a concrete dtype");
+  }
+}
+
+Tensor Tensor::full_f32(const Shape& shape, float v, DeviceId dev) {
+  std::vector<float> d(fg::numel(shape), v);
+  return new_f32(d, shape, dev);
+}
+
+Tensor Tensor::scalar_f32(float v, DeviceId dev) { return new_f32({v}, Shape{1}, dev); }
+
+DeviceId Tensor::device() const { return uop().device(); }
+DType Tensor::dtype() const { return uop().dtype(); }
+Shape Tensor::shape() const { return uop().shape(); }
+size_t Tensor::numel() const { return fg::numel(shape()); }
+size_t Tensor::ndim() const { return shape().size(); }
+
+bool Tensor::is_realized() const {  // tensor.rs:351-358
+  UOp u = uop();
+  if (u.op() == Op::Buffer) return true;
+  if (u.op() == Op::Reshape) return u.src(0).op() == Op::Buffer;
+  return false;
+}
+
+bool Tensor::requires_grad() const { return p_->requires_grad; }
+std::optional<Tensor> Tensor::grad() const {
+  if (!p_->grad) return std::nullopt;
+  return Tensor(p_->grad);
+}
+void Tensor::clear_grad() const { p_->grad.reset(); }
+Tensor Tensor::with_requires_grad(bool rg) const {
+  p_->requires_grad = rg;
+  return *this;
+}
+Tensor Tensor::detach() const { return from_uop(uop(), false); }
+
+Tensor Tensor::replace(const Tensor& o) const {  // tensor.rs:399-409
+  FG_CHECK(shape() == o.shape(), "replace: shape mismatch " + shape_str(shape()) + " != " + shape_str(o.shape()));
+  set_uop(o.uop());
+  return *this;
+}
+
+UOp Tensor::target_uop() const {  // tensor.rs:189-195
+  UOp cur = uop();
+  if (cur.op() == Op::After) return cur.src(0);
+  return cur;
+}
+
+Tensor Tensor::assign(const Tensor& o) const {  // tensor.rs:421-440
+  FG_CHECK(shape() == o.shape(), "assign: shape mismatch " + shape_str(shape()) + " != " + shape_str(o.shape()));
+  FG_CHECK(dtype() == o.dtype(), "assign: dtype mismatch");
+  FG_CHECK(device() == o.device(), "assign: device mismatch");
+  UOp target = target_uop();
+  FG_CHECK(target.has_buffer_identity(), "assign requires a tensor with concrete buffer identity");
+  UOp effect = UOp::store(target, o.uop());
+  set_uop(UOp::after(target, effect));
+  return *this;
+}
+
+Tensor Tensor::unary(Op op) const {
+  return from_uop(UOp::make_new(op, dtype(), {uop()}, Arg::none()), requires_grad());
+}
+
+Tensor Tensor::binary(const Tensor& o, Op op, DType out) const {  // tensor.rs:449-459
+  FG_CHECK(device() == o.device(), "binary ops require tensors on the same device");
+  FG_CHECK(shape() == o.shape(), std::string("shape mismatch for ") + op_name(op));
+  return from_uop(UOp::make_new(op, out, {uop(), o.uop()}, Arg::none()), requires_grad() || o.requires_grad());
+}
+
+Tensor Tensor::broadcasted(const Tensor& o, Op op, DType out) const {  // tensor.rs:461-467, 1068-1092
+  if (shape() == o.shape()) return binary(o, op, out);
+  FG_CHECK(device() == o.device(), "broadcast requires tensors on the same device");
+  Shape target;
+  FG_CHECK(broadcast_with(shape(), o.shape(), &target),
+           "broadcast: incompatible dims for " + shape_str(shape()) + " vs " + shape_str(o.shape()));
+  Tensor l = reshape(pad_left(shape(), target.size())).expand(target);
+  Tensor r = o.reshape(pad_left(o.shape(), target.size())).expand(target);
+  return l.binary(r, op, out);
+}
+
+Tensor Tensor::add(const Tensor& o) const { return broadcasted(o, Op::Add, dtype()); }
+Tensor Tensor::mul(const Tensor& o) const { return broadcasted(o, Op::Mul, dtype()); }
+Tensor Tensor::neg() const { return unary(Op::Neg); }
+Tensor Tensor::sub(const Tensor& o) const { return add(o.neg()); }
+Tensor Tensor::reciprocal() const { return unary(Op::Reciprocal); }
+Tensor Tensor::exp2() const { return unary(Op::Exp2); }
+Tensor Tensor::log2() const { return unary(Op::Log2); }
+Tensor Tensor::sqrt() const { return unary(Op::Sqrt); }
+
+Tensor Tensor::relu() const {  // tensor.rs:517-531
+  Tensor zero = zeros(shape(), device(), dtype());
+  Tensor cond = zero.binary(*this, Op::CmpLt, DType::Bool());
+  return from_uop(UOp::make_new(Op::Where, dtype(), {cond.uop(), uop(), zero.uop()}, Arg::none()), requires_grad());
+}
+
+Tensor Tensor::exp() const {  // tensor.rs:697-700 (f32 LOG2_E)
+  Tensor log2e = scalar_f32(1.44269504088896340736f, device());
+  return mul(log2e).exp2();
+}
+
+Tensor Tensor::log() const {  // tensor.rs:704-707 (f32 LN_2)
+  Tensor ln2 = scalar_f32(0.693147180559945309417f, device());
+  return log2().mul(ln2);
+}
+
+Tensor Tensor::reshape(const Shape& ns) const {  // tensor.rs:539-552
+  if (shape() == ns) return *this;
+  FG_CHECK(numel() == fg::numel(ns), "reshape: numel mismatch for " + shape_str(shape()) + " -> " + shape_str(ns));
+  return from_uop(UOp::reshape(uop(), ns), requires_grad());
+}
+
+Tensor Tensor::narrow(size_t dim, size_t start, size_t len) const {  // tensor.rs:561-603
+  Shape s = shape();
+  FG_CHECK(dim < s.size(), "narrow: dim " + std::to_string(dim) + " out of range");
+  size_t end = start + len;
+  FG_CHECK(end <= s[dim], "narrow: range [" + std::to_string(start) + ", " + std::to_string(end) +
+                              ") out of bounds for axis " + std::to_string(dim) + " with size " +
+                              std::to_string(s[dim]));
+  if (start == 0 && len == s[dim]) return *this;
+  std::vector<UOp> starts;
+  std::vector<size_t> lens;
+  for (size_t ax = 0; ax < s.size(); ax++) {
+    starts.push_back(UOp::const_int(ax == dim ? static_cast<int64_t>(start) : 0, DType::I32(), device()));
+    lens.push_back(ax == dim ? len : s[ax]);
+  }
+  return from_uop(UOp::shrink(uop(), starts, lens), requires_grad());
+}
+
+Tensor Tensor::permute(const std::vector<size_t>& order) const {  // tensor.rs:611-621
+  size_t nd = ndim();
+  FG_CHECK(order.size() == nd, "permute: wrong number of axes");
+  std::vector<bool> seen(nd, false);
+  for (auto ax : order) {
+    FG_CHECK(ax < nd, "permute: axis " + std::to_string(ax) + " out of range");
+    FG_CHECK(!seen[ax], "permute: axis " + std::to_string(ax) + " duplicated");
+    seen[ax] = true;
+  }
+  return from_uop(UOp::permute(uop(), order), requires_grad());
+}
+
+Tensor Tensor::contiguous() const {  // tensor.rs:625-630
+  if (is_realized()) return *this;
+  return from_uop(UOp::contiguous(uop()), requires_grad());
+}
+
+Tensor Tensor::expand(const Shape& ns) const {  // tensor.rs:638-657
+  if (shape() == ns) return *this;
+  Shape s = shape();
+  FG_CHECK(s.size() == ns.size(), "expand: rank mismatch for " + shape_str(s) + " -> " + shape_str(ns));
+  for (size_t i = 0; i < s.size(); i++)
+    FG_CHECK(s[i] == ns[i] || s[i] == 1, "expand: incompatible source shape " + shape_str(s) + " -> " + shape_str(ns));
+  return from_uop(UOp::expand(uop(), ns), requires_grad());
+}
+
+Tensor Tensor::sum(const std::vector<size_t>& axes) const {  // tensor.rs:665-675
+  size_t nd = ndim();
+  for (auto a : axes) FG_CHECK(a < nd, "sum: axes out of range for ndim " + std::to_string(nd));
+  return from_uop(UOp::reduce_axis(uop(), Op::Add, axes), requires_grad());
+}
+
+Tensor Tensor::max(const std::vector<size_t>& axes) const {  // tensor.rs:683-693
+  size_t nd = ndim();
+  for (auto a : axes) FG_CHECK(a < nd, "max: axes out of range for ndim " + std::to_string(nd));
+  return from_uop(UOp::reduce_axis(uop(), Op::Max, axes), requires_grad());
+}
+
+Tensor Tensor::log_softmax(size_t axis) const {  // tensor.rs:715-721
+  FG_CHECK(axis < ndim(), "log_softmax: axis " + std::to_string(axis) + " out of range");
+  Tensor mx = max({axis});
+  Tensor shifted = sub(mx);
+  Tensor se = shifted.exp().sum({axis});
+  return shifted.sub(se.log());
+}
+
+Tensor Tensor::cross_entropy(const Tensor& targets) const {  // tensor.rs:738-752
+  FG_CHECK(shape() == targets.shape(), "cross_entropy: target shape " + shape_str(targets.shape()) +
+                                            " must match logits shape " + shape_str(shape()));
+  size_t cax = ndim() != 1 ? 1 : 0;
+  Tensor lp = log_softmax(cax);
+  Tensor per = targets.mul(lp).sum({cax}).neg();
+  std::vector<size_t> red;
+  for (size_t i = 0; i < per.ndim(); i++) red.push_back(i);
+  Tensor scale = scalar_f32(1.0f / static_cast<float>(per.numel()), device());
+  return per.sum(red).mul(scale);
+}
+
+Tensor Tensor::matmul(const Tensor& other) const {  // tensor.rs:762-778
+  FG_CHECK(ndim() == 2, "matmul: lhs must be 2D");
+  FG_CHECK(other.ndim() == 2, "matmul: rhs must be 2D");
+  Shape ls = shape(), rs = other.shape();
+  size_t m = ls[0], k = ls[1], k2 = rs[0], n = rs[1];
+  FG_CHECK(k == k2, "matmul: inner dim mismatch (" + std::to_string(k) + " vs " + std::to_string(k2) + ")");
+  Tensor a = reshape({m, 1, k}).expand({m, n, k});
+  Tensor b = other.permute({1, 0}).contiguous().reshape({1, n, k}).expand({m, n, k});
+  return a.mul(b).sum({2}).reshape({m, n});
+}
+
+// tensor.rs:1097-1121
+static void assert_kernel_ready(const UOp& root) {
+  FG_CHECK(root.op() == Op::Sink, "render: root must be a Sink node");
+  for (auto& n : root.toposort()) {
+    switch (n.op()) {
+      case Op::DefineVar: case Op::Bind: case Op::Buffer: case Op::Shrink: case Op::Reshape:
+      case Op::Permute: case Op::Expand: case Op::Contiguous: case Op::ReduceAxis:
+        fail(std::string(op_name(n.op())) + " should be lowered before codegen");
+      default: break;
+    }
+  }
+}
+
+// tensor.rs:831-898
+static void execute_item(const ScheduleItem& item) {
+  Device& backend = get_device(item.sink.device());
+  int debug = debug_level();
+  size_t num_args = item.output_buffer ? item.inputs.size() + 1 : item.inputs.size();
+  auto& lc = lowering_cache(backend.id());
+  std::shared_ptr<Program> program;
+  auto hit = lc.find(item.sink);
+  if (hit != lc.end()) {
+    program = hit->second;
+    realize_stats().lowering_cache_hits++;
+    if (debug >= 1) {
+      size_t kid = g_kernel_count++;
+      std::fprintf(stderr, "*** %s %4zu  (cached)         arg %2zu\n", backend.id() == DeviceId::Hip ? "HIP" : "CPU",
+                   kid, num_args);
+    }
+  } else {
+    if (debug >= 3) std::fprintf(stderr, "━━━ rangeify [before] ━━━\n%s", item.sink.dump().c_str());
+    UOp rangeified = rangeify(item.sink);
+    if (debug >= 3) std::fprintf(stderr, "━━━ optimize [before] ━━━\n%s", rangeified.dump().c_str());
+    UOp optimized = backend.optimize(rangeified);
+    if (debug >= 3) std::fprintf(stderr, "━━━ codegen [before] ━━━\n%s", optimized.dump().c_str());
+    assert_kernel_ready(optimized);
+    program = backend.cached_program(optimized);
+    if (program) {
+      if (debug >= 1) {
+        size_t kid = g_kernel_count++;
+        std::fprintf(stderr, "*** %s %4zu  (cached)         arg %2zu\n",
+                     backend.id() == DeviceId::Hip ? "HIP" : "CPU", kid, num_args);
+      }
+    } else {
+      size_t kid = g_kernel_count++;
+      std::string name = "kernel_" + std::to_string(kid);
+      RenderedKernel rk = backend.render(optimized, name);
+      if (debug >= 4) std::fprintf(stderr, "%s\n", rk.source.c_str());
+      program = backend.compile(rk, num_args);
+      realize_stats().programs_compiled++;
+      if (debug >= 1)
+        std::fprintf(stderr, "*** %s %4zu  %-16s arg %2zu  [%s]\n", backend.id() == DeviceId::Hip ? "HIP" : "CPU", kid,
+                     name.c_str(), num_args, rk.kind.c_str());
+      backend.insert_program(optimized, program);
+    }
+    lc[item.sink] = program;
+  }
+
+  std::vector<KernelArg> args;
+  args.reserve(num_args);
+  if (item.output_buffer) {
+    // The store covers every output element, so the output needs no zero fill.
+    if (!item.output_buffer->is_realized()) backend.realize_storage(*item.output_buffer, false);
+    item.output_buffer->known_zero = false;
+    args.push_back(KernelArg::buf(item.output_buffer));
+  }
+  for (auto& in : item.inputs) {
+    if (in.kind == KernelArg::Kind::Buffer)
+      FG_CHECK(in.buffer->is_realized(), "scheduled input buffer missing");
+    args.push_back(in);
+  }
+  auto t0 = std::chrono::steady_clock::now();
+  backend.execute(*program, args);
+  realize_stats().kernels_launched++;
+  if (debug >= 2) {
+    backend.synchronize();
+    double ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
+    std::fprintf(stderr, "              exec time=%.3fms\n", ms);
+  }
+}
+
+void Tensor::realize_many(const std::vector<Tensor>& tensors) {  // tensor.rs:781-821
+  std::vector<UOp> roots;
+  UOpSet seen;
+  for (auto& t : tensors) {
+    if (t.is_realized()) continue;
+    UOp r = t.uop();
+    if (seen.insert(r).second) roots.push_back(r);
+  }
+  if (roots.empty()) return;
+  if (debug_level() >= 3) std::fprintf(stderr, "━━━ schedule [before] ━━━\n%s", UOp::sink(roots).dump().c_str());
+  ScheduleOptions opt;
+  opt.fuse = get_device(roots[0].device()).fuse_elementwise();
+  SchedulePlan plan = schedule_many(roots, opt);
+  for (auto& item : plan.items) execute_item(item);
+  apply_map_to_tensors(plan.replacements);
+}
+
+Tensor Tensor::realize() const {
+  realize_many({*this});
+  return *this;
+}
+
+Buffer Tensor::realized_buffer() const {
+  realize();
+  UOp u = uop();
+  UOp b;
+  if (u.op() == Op::Buffer) b = u;
+  else if (u.op() == Op::Reshape) b = u.src(0);
+  else fail("realized tensor must point at a buffer");
+  FG_CHECK(b.arg().kind == Arg::Kind::Buffer, "realized tensor must point at Arg::Buffer");
+  return b.arg().buf;
+}
+
+std::vector<uint8_t> Tensor::to_bytes() const {
+  Buffer b = realized_buffer();
+  return get_device(b->device).copy_to_host(b);
+}
+
+std::vector<float> Tensor::to_vec() const {  // tensor.rs:912-930
+  Buffer b = realized_buffer();
+  FG_CHECK(b->dtype == DType::F32(), "to_vec requires F32 tensor data");
+  auto bytes = get_device(b->device).copy_to_host(b);
+  std::vector<float> out(bytes.size() / 4);
+  std::memcpy(out.data(), bytes.data(), bytes.size());
+  return out;
+}
+
+std::vector<Tensor> Tensor::gradient(const std::vector<Tensor>& targets) const {  // tensor.rs:938-964
+  for (auto& t : targets) FG_CHECK(t.device() == device(), "gradient targets must share the same device");
+  UOp rg = UOp::full(shape(), DType::F32(), device(), 1.0);
+  std::vector<UOp> tu;
+  for (auto& t : targets)
+    if (t.requires_grad()) tu.push_back(t.uop());
+  auto gm = compute_gradient(uop(), rg, tu);
+  std::vector<Tensor> out;
+  for (auto& t : targets) {
+    auto it = gm.find(t.uop());
+    if (it != gm.end()) out.push_back(from_uop(it->second, false));
+    else out.push_back(from_uop(UOp::full(t.shape(), DType::F32(), t.device(), 0.0), false));
+  }
+  return out;
+}
+
+void Tensor::backward() const {  // tensor.rs:971-998
+  FG_CHECK(numel() == 1, "backward requires a scalar loss");
+  UOpSet all;
+  for (auto& n : uop().toposort()) all.insert(n);
+  std::vector<Tensor> targets;
+  for (auto& t : live_tensors())
+    if (t.requires_grad() && all.count(t.uop())) targets.push_back(t);
+  if (targets.empty()) return;
+  std::vector<UOp> tu;
+  for (auto& t : targets) tu.push_back(t.uop());
+  UOp rg = UOp::full(shape(), DType::F32(), device(), 1.0);
+  auto grads = compute_gradient(uop(), rg, tu);
+  for (auto& t : targets) {
+    auto it = grads.find(t.uop());
+    UOp g = it != grads.end() ? it->second : UOp::full(t.shape(), DType::F32(), t.device(), 0.0);
+    Tensor gt = from_uop(g, false);
+    auto existing = t.grad();
+    Tensor acc = existing ? existing->add(gt) : gt;
+    t.p_->grad = acc.p_;
+  }
+}
+
+// ── gradient.rs ─────────────────────────────────────────────────────────────
+namespace {
+
+UOp const_like(const UOp& n, double v) { return UOp::const_float(v, n.dtype(), n.device()); }
+
+UOp zero_like(const UOp& n) {  // gradient.rs:87-90
+  Shape s;
+  if (!n.shape_opt(&s)) s = Shape{1};
+  return UOp::full(s, n.dtype(), n.device(), 0.0);
+}
+
+// gradient.rs:97-205
+std::vector<UOp> gradient_for_op(const UOp& node, const UOp& grad) {
+  switch (node.op()) {
+    case Op::Add: return {grad, grad};
+    case Op::Mul: {
+      const UOp &x = node.src(0), &y = node.src(1);
+      return {UOp::mul(y, grad), UOp::mul(x, grad)};
+    }
+    case Op::Neg: return {UOp::neg(grad)};
+    case Op::Reciprocal: return {UOp::mul(UOp::neg(grad), UOp::mul(node, node))};
+    case Op::Exp2: return {UOp::mul(UOp::mul(node, const_like(node, 0.69314718055994530942)), grad)};
+    case Op::Log2:
+      return {UOp::mul(grad, UOp::reciprocal(UOp::mul(node.src(0), const_like(node, 0.69314718055994530942))))};
+    case Op::Sqrt: return {UOp::mul(grad, UOp::reciprocal(UOp::mul(const_like(node, 2.0), node)))};
+    case Op::Max: {
+      const UOp &x = node.src(0), &y = node.src(1);
+      UOp zero = const_like(node, 0.0);
+      UOp half = UOp::mul(grad, const_like(node, 0.5));
+      UOp xw = UOp::cmplt(y, x), yw = UOp::cmplt(x, y);
+      UOp xt = UOp::where(yw, zero, half);
+      UOp xg = UOp::where(xw, grad, xt);
+      UOp yt = UOp::where(xw, zero, half);
+      UOp yg = UOp::where(yw, grad, yt);
+      return {xg, yg};
+    }
+    case Op::CmpLt: return {UOp(), UOp()};
+    case Op::Where: {
+      const UOp& c = node.src(0);
+      UOp zero = const_like(node, 0.0);
+      return {UOp(), UOp::where(c, grad, zero), UOp::where(c, zero, grad)};
+    }
+    case Op::Reshape: return {UOp::reshape(grad, node.src(0).shape())};
+    case Op::Permute: return {UOp::permute(grad, invert_permutation(node.arg().usizes()))};
+    case Op::Expand: {
+      Shape ss = node.src(0).shape();
+      auto axes = expand_gradient_axes(ss, node.arg().usizes());
+      if (axes.empty()) return {grad};
+      return {UOp::reduce_axis(grad, Op::Add, axes)};
+    }
+    case Op::Contiguous: return {grad};
+    case Op::ReduceAxis: {
+      const UOp& src = node.src(0);
+      Shape ss = src.shape();
+      Op rop = node.arg().rop;
+      if (rop == Op::Add) return {UOp::expand(grad, ss)};
+      if (rop == Op::Max) {
+        DType dt = grad.dtype();
+        UOp mx = UOp::expand(node, ss);
+        UOp ge = UOp::expand(grad, ss);
+        UOp not_max = UOp::cmplt(src, mx);
+        UOp zero = UOp::const_float(0.0, dt, node.device());
+        UOp one = UOp::const_float(1.0, dt, node.device());
+        UOp mask = UOp::where(not_max, zero, one);
+        UOp count = UOp::reduce_axis(mask, Op::Add, node.arg().usizes());
+        UOp ce = UOp::expand(count, ss);
+        UOp weighted = UOp::mul(mask, UOp::reciprocal(ce));
+        return {UOp::mul(weighted, ge)};
+      }
+      fail("unsupported reduce op gradient");
+    }
+    case Op::Buffer: case Op::Const: return {};
+    default: fail(std::string("gradient not implemented for ") + op_name(node.op()));
+  }
+}
+
+UOpSet needed_nodes(const UOp& root, const std::vector<UOp>& targets,
+                    const UOpMap<std::vector<UOp>>& consumers) {  // gradient.rs:64-81
+  UOpSet needed;
+  std::vector<UOp> stack(targets.begin(), targets.end());
+  while (!stack.empty()) {
+    UOp n = stack.back();
+    stack.pop_back();
+    if (!needed.insert(n).second) continue;
+    auto it = consumers.find(n);
+    if (it != consumers.end()) stack.insert(stack.end(), it->second.begin(), it->second.end());
+  }
+  needed.insert(root);
+  return needed;
+}
+
+}  // namespace
+
+UOpMap<UOp> compute_gradient(const UOp& root, const UOp& root_grad, const std::vector<UOp>& targets) {
+  auto order = root.toposort();
+  auto consumers = build_consumer_map(order);
+  auto needed = needed_nodes(root, targets, consumers);
+  UOpMap<UOp> grads;
+  grads[root] = root_grad;
+  for (size_t i = order.size(); i-- > 0;) {
+    const UOp& node = order[i];
+    if (!needed.count(node)) continue;
+    auto gi = grads.find(node);
+    if (gi == grads.end()) continue;
+    UOp g = gi->second;
+    auto local = gradient_for_op(node, g);
+    for (size_t s = 0; s < node.srcs().size() && s < local.size(); s++) {
+      if (!local[s]) continue;
+      const UOp& src = node.src(s);
+      if (!needed.count(src)) continue;
+      auto ex = grads.find(src);
+      if (ex != grads.end()) ex->second = UOp::add(ex->second, local[s]);
+      else grads[src] = local[s];
+    }
+  }
+  UOpMap<UOp> result;
+  for (auto& t : targets) {
+    auto it = grads.find(t);
+    result[t] = it != grads.end() ? it->second : zero_like(t);
+  }
+  return result;
+}
+
+// ── nn.rs ───────────────────────────────────────────────────────────────────
+namespace {
+uint64_t g_init_seed = 42;  // nn.rs:12-14
+
+float next_unit_f32() {  // nn.rs:16-26
+  g_init_seed = g_init_seed * 6364136223846793005ULL + 1ULL;
+  return static_cast<float>(g_init_seed >> 33) / static_cast<float>(1ULL << 31);
+}
+}  // namespace
+
+void reset_init_seed(uint64_t seed) { g_init_seed = seed; }
+
+Tensor kaiming_normal(const Shape& shape, size_t fan_in, DeviceId dev) {  // nn.rs:28-47
+  size_t n = fg::numel(shape);
+  float stdv = std::sqrt(2.0f / static_cast<float>(fan_in));
+  std::vector<float> data;
+  data.reserve(n);
+  const float two_pi = 2.0f * 3.14159265358979323846f;
+  while (data.size() < n) {
+    float u1 = std::max(next_unit_f32(), 1.17549435e-38f);
+    float u2 = next_unit_f32();
+    float radius = std::sqrt(-2.0f * std::log(u1)) * stdv;
+    float theta = two_pi * u2;
+    data.push_back(radius * std::cos(theta));
+    if (data.size() < n) data.push_back(radius * std::sin(theta));
+  }
+  return Tensor::new_f32(data, shape, dev);
+}
+
+Linear Linear::create(size_t in, size_t out, DeviceId dev, bool with_bias) {  // nn.rs:77-92
+  Linear l;
+  l.weight = kaiming_normal({out, in}, in, dev).with_requires_grad(true);
+  if (with_bias) l.bias = Tensor::zeros({out}, dev, DType::F32()).with_requires_grad(true);
+  return l;
+}
+
+Tensor Linear::forward(const Tensor& x) const {  // nn.rs:97-104
+  Tensor w = weight.permute({1, 0});
+  Tensor logits = x.matmul(w);
+  if (bias) return logits.add(*bias);
+  return logits;
+}
+
+std::vector<Tensor> Linear::parameters() const {
+  std::vector<Tensor> p{weight};
+  if (bias) p.push_back(*bias);
+  return p;
+}
+
+// ── optim.rs ────────────────────────────────────────────────────────────────
+Sgd::Sgd(const std::vector<Tensor>& ps, float lr_) : lr(lr_) {  // optim.rs:23-41
+  FG_CHECK(!ps.empty(), "optimizer must have at least one parameter");
+  for (auto& p : ps) {
+    bool dup = false;
+    for (auto& e : params) dup = dup || e.ptr_eq(p);
+    if (!dup) params.push_back(p);
+  }
+}
+
+void Sgd::zero_grad() const {
+  for (auto& p : params) p.clear_grad();
+}
+
+void Sgd::step() const {  // optim.rs:60-71
+  for (auto& p : params) {
+    Tensor lrt = Tensor::scalar_f32(lr, p.device());
+    auto g = p.grad();
+    FG_CHECK(g.has_value(), "optimizer step requires parameter gradients");
+    Tensor update = p.detach().sub(g->mul(lrt));
+    p.assign(update);
+  }
+  Tensor::realize_many(params);
+}
+
+}  // namespace fg

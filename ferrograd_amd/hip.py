@@ -1,0 +1,152 @@
+"""ctypes binding of the device C-ABI (include/ferrograd_hip.h).
+
+This is the layer a Rust `HipDevice` would bind; tests use it to exercise the
+backend directly, the benchmark uses its events for kernel timing.
+"""
+from __future__ import annotations
+
+import ctypes
+
+from . import lib
+
+FG_ARG_PTR, FG_ARG_I32, FG_ARG_F32, FG_ARG_BOOL = 0, 1, 2, 3
+FG_OK, FG_ERR_HIP, FG_ERR_COMPILE, FG_ERR_SYMBOL, FG_ERR_ARGS, FG_ERR_INVALID = range(6)
+
+
+class _Val(ctypes.Union):
+    _fields_ = [("p", ctypes.c_void_p), ("i", ctypes.c_int32), ("f", ctypes.c_float), ("b", ctypes.c_uint8)]
+
+
+class Arg(ctypes.Structure):
+    _fields_ = [("kind", ctypes.c_int32), ("reserved", ctypes.c_int32), ("v", _Val)]
+
+    @staticmethod
+    def ptr(p):
+        a = Arg()
+        a.kind = FG_ARG_PTR
+        a.v.p = p
+        return a
+
+    @staticmethod
+    def i32(x):
+        a = Arg()
+        a.kind = FG_ARG_I32
+        a.v.i = x
+        return a
+
+    @staticmethod
+    def f32(x):
+        a = Arg()
+        a.kind = FG_ARG_F32
+        a.v.f = x
+        return a
+
+    @staticmethod
+    def boolean(x):
+        a = Arg()
+        a.kind = FG_ARG_BOOL
+        a.v.b = 1 if x else 0
+        return a
+
+
+_declared = False
+
+
+def api() -> ctypes.CDLL:
+    global _declared
+    l = lib()
+    if not _declared:
+        P, PP = ctypes.c_void_p, ctypes.POINTER(ctypes.c_void_p)
+        c_int, c_size = ctypes.c_int, ctypes.c_size_t
+        uint3 = ctypes.c_uint * 3
+        sigs = {
+            "fg_hip_init": (c_int, [c_int, PP]),
+            "fg_hip_destroy": (c_int, [P]),
+            "fg_hip_alloc": (c_int, [P, c_size, c_int, PP]),
+            "fg_hip_free": (c_int, [P, P]),
+            "fg_hip_trim": (c_int, [P]),
+            "fg_hip_copy_h2d": (c_int, [P, P, P, c_size]),
+            "fg_hip_copy_d2h": (c_int, [P, P, P, c_size]),
+            "fg_hip_copy_d2d": (c_int, [P, P, P, c_size]),
+            "fg_hip_compile": (c_int, [P, ctypes.c_char_p, ctypes.c_char_p, c_int, PP]),
+            "fg_hip_program_free": (c_int, [P]),
+            "fg_hip_program_num_args": (c_int, [P]),
+            "fg_hip_launch": (c_int, [P, P, ctypes.POINTER(Arg), c_int, uint3, uint3, ctypes.c_uint]),
+            "fg_hip_sync": (c_int, [P]),
+            "fg_hip_event_record": (c_int, [P, c_int]),
+            "fg_hip_event_elapsed_ms": (c_int, [P, c_int, c_int, ctypes.POINTER(ctypes.c_float)]),
+            "fg_hip_device_info": (c_int, [P, ctypes.POINTER(c_int), ctypes.POINTER(c_int), ctypes.POINTER(c_size),
+                                           ctypes.c_char_p, c_size]),
+            "fg_hip_last_error": (ctypes.c_char_p, []),
+        }
+        for name, (res, args) in sigs.items():
+            f = getattr(l, name)
+            f.restype = res
+            f.argtypes = args
+        _declared = True
+    return l
+
+
+def last_error() -> str:
+    return api().fg_hip_last_error().decode()
+
+
+class HipError(RuntimeError):
+    def __init__(self, code: int, msg: str):
+        super().__init__(f"[{code}] {msg}")
+        self.code = code
+
+
+def check(rc: int) -> None:
+    if rc != FG_OK:
+        raise HipError(rc, last_error())
+
+
+class Context:
+    """An fg_ctx (device + stream)."""
+
+    def __init__(self, ordinal: int = 0):
+        self.h = ctypes.c_void_p()
+        check(api().fg_hip_init(ordinal, ctypes.byref(self.h)))
+
+    def alloc(self, nbytes: int, zero: bool = True) -> int:
+        p = ctypes.c_void_p()
+        check(api().fg_hip_alloc(self.h, nbytes, int(zero), ctypes.byref(p)))
+        return p.value
+
+    def free(self, p: int) -> None:
+        check(api().fg_hip_free(self.h, p))
+
+    def h2d(self, dst: int, arr) -> None:
+        check(api().fg_hip_copy_h2d(self.h, dst, arr.ctypes.data, arr.nbytes))
+
+    def d2h(self, arr, src: int) -> None:
+        check(api().fg_hip_copy_d2h(self.h, arr.ctypes.data, src, arr.nbytes))
+
+    def compile(self, source: str, name: str, num_args: int) -> int:
+        p = ctypes.c_void_p()
+        check(api().fg_hip_compile(self.h, source.encode(), name.encode(), num_args, ctypes.byref(p)))
+        return p.value
+
+    def launch(self, prog: int, args, grid=(1, 1, 1), block=(64, 1, 1), lds: int = 0) -> None:
+        arr = (Arg * max(1, len(args)))(*args)
+        g = (ctypes.c_uint * 3)(*grid)
+        b = (ctypes.c_uint * 3)(*block)
+        check(api().fg_hip_launch(self.h, prog, arr, len(args), g, b, lds))
+
+    def sync(self) -> None:
+        check(api().fg_hip_sync(self.h))
+
+    def record(self, slot: int) -> None:
+        check(api().fg_hip_event_record(self.h, slot))
+
+    def elapsed_ms(self, a: int, b: int) -> float:
+        ms = ctypes.c_float()
+        check(api().fg_hip_event_elapsed_ms(self.h, a, b, ctypes.byref(ms)))
+        return ms.value
+
+    def info(self) -> dict:
+        cu, clk, lds = ctypes.c_int(), ctypes.c_int(), ctypes.c_size_t()
+        arch = ctypes.create_string_buffer(64)
+        check(api().fg_hip_device_info(self.h, ctypes.byref(cu), ctypes.byref(clk), ctypes.byref(lds), arch, 64))
+        return {"cu_count": cu.value, "clock_khz": clk.value, "lds_per_block": lds.value, "arch": arch.value.decode()}

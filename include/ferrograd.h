@@ -1,0 +1,105 @@
+/* ferrograd.h — C-ABI of the tensor front end that drives the MI355X path.
+ *
+ * Mirrors the reference's public Rust API (src/tensor.rs, src/nn.rs,
+ * src/optim.rs) so a host program (the Python package ferrograd_amd, a Rust
+ * shim, the benchmark) can build lazy graphs, realise them on a device and
+ * read results. Devices: 0 = cpu (only when the test oracle is loaded),
+ * 1 = hip (MI355X). Dtypes: 0 = f32, 1 = i32, 2 = bool.
+ *
+ * Every function returns 0 on success, nonzero on error; the message is in
+ * fg_last_error(). Handles are owned by the caller and released with the
+ * matching *_free. A tensor handle aliases shared tensor state, like a cloned
+ * reference Tensor (tensor.rs:30-38).
+ */
+#ifndef FERROGRAD_H
+#define FERROGRAD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct fg_tensor fg_tensor;
+typedef struct fg_linear fg_linear;
+typedef struct fg_sgd fg_sgd;
+
+enum { FG_DEV_CPU = 0, FG_DEV_HIP = 1 };
+enum { FG_F32 = 0, FG_I32 = 1, FG_BOOL = 2 };
+enum {
+  FG_UNARY_NEG = 0, FG_UNARY_RECIPROCAL, FG_UNARY_EXP2, FG_UNARY_LOG2, FG_UNARY_SQRT, FG_UNARY_RELU,
+  FG_UNARY_EXP, FG_UNARY_LOG, FG_UNARY_CONTIGUOUS, FG_UNARY_DETACH, FG_UNARY_ALIAS
+};
+enum { FG_BINARY_ADD = 0, FG_BINARY_MUL, FG_BINARY_SUB, FG_BINARY_MATMUL, FG_BINARY_CROSS_ENTROPY };
+enum { FG_REDUCE_SUM = 0, FG_REDUCE_MAX };
+enum { FG_MOVE_RESHAPE = 0, FG_MOVE_PERMUTE, FG_MOVE_EXPAND };
+
+const char* fg_last_error(void);
+
+/* Construction: Tensor::new / zeros / ones (tensor.rs:260-312). */
+int fg_tensor_from_data(int device, int dtype, const void* data, size_t nbytes, const int64_t* shape, int ndim,
+                        fg_tensor** out);
+int fg_tensor_zeros(int device, int dtype, const int64_t* shape, int ndim, fg_tensor** out);
+int fg_tensor_ones(int device, int dtype, const int64_t* shape, int ndim, fg_tensor** out);
+int fg_tensor_free(fg_tensor* t);
+
+/* Lazy ops (tensor.rs:442-778). */
+int fg_tensor_unary(fg_tensor* t, int op, fg_tensor** out);
+int fg_tensor_binary(fg_tensor* a, fg_tensor* b, int op, fg_tensor** out);
+int fg_tensor_reduce(fg_tensor* t, int op, const int64_t* axes, int naxes, fg_tensor** out);
+int fg_tensor_movement(fg_tensor* t, int op, const int64_t* arg, int narg, fg_tensor** out);
+int fg_tensor_narrow(fg_tensor* t, int64_t dim, int64_t start, int64_t len, fg_tensor** out);
+int fg_tensor_log_softmax(fg_tensor* t, int64_t axis, fg_tensor** out);
+
+/* In-place graph updates (tensor.rs:399-440). */
+int fg_tensor_assign(fg_tensor* t, fg_tensor* value);
+int fg_tensor_replace(fg_tensor* t, fg_tensor* value);
+
+/* Realisation and readback (tensor.rs:781-930). `nbytes` must equal the
+ * tensor's byte size. */
+int fg_tensor_realize_many(fg_tensor** ts, int n);
+int fg_tensor_read(fg_tensor* t, void* dst, size_t nbytes);
+
+/* Metadata. `ndim` is in/out: capacity of `shape` in, rank out. */
+int fg_tensor_shape(fg_tensor* t, int64_t* shape, int* ndim);
+int fg_tensor_info(fg_tensor* t, int* dtype, int* device, int* realized, int* requires_grad);
+int fg_tensor_set_requires_grad(fg_tensor* t, int requires_grad);
+int fg_tensor_same(fg_tensor* a, fg_tensor* b, int* same);
+
+/* Autograd (tensor.rs:938-998). fg_tensor_grad sets *out to NULL if none. */
+int fg_tensor_grad(fg_tensor* t, fg_tensor** out);
+int fg_tensor_backward(fg_tensor* loss);
+int fg_tensor_gradient(fg_tensor* loss, fg_tensor** targets, int n, fg_tensor** outs);
+
+/* nn::Linear (nn.rs:67-104) with the reference's seeded Kaiming init. */
+int fg_reset_init_seed(uint64_t seed);
+int fg_linear_new(int device, int64_t in_features, int64_t out_features, int bias, fg_linear** out);
+int fg_linear_forward(fg_linear* l, fg_tensor* x, fg_tensor** out);
+int fg_linear_num_params(fg_linear* l, int* n);
+int fg_linear_param(fg_linear* l, int i, fg_tensor** out);
+int fg_linear_free(fg_linear* l);
+
+/* optim::Sgd (optim.rs:16-71). */
+int fg_sgd_new(fg_tensor** params, int n, float lr, fg_sgd** out);
+int fg_sgd_zero_grad(fg_sgd* s);
+int fg_sgd_step(fg_sgd* s);
+int fg_sgd_free(fg_sgd* s);
+
+/* Device control and statistics. */
+int fg_synchronize(int device);
+int fg_stats(uint64_t* kernels_launched, uint64_t* programs_compiled, uint64_t* lowering_hits);
+int fg_clear_caches(void);
+
+/* Inspection for tests and tooling: schedule the roots (without running
+ * anything) and describe the plan as JSON; optionally render each kernel with
+ * the HIP code generator (no device needed). Two calls: with buf == NULL it
+ * plans and reports the JSON size in *needed; with a buffer it copies the
+ * JSON of the last plan on this thread. */
+int fg_debug_plan(fg_tensor** roots, int n, int fuse, int render_hip, char* buf, size_t len, size_t* needed);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FERROGRAD_H */

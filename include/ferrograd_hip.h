@@ -1,0 +1,106 @@
+/* ferrograd_hip.h — C-ABI of the MI355X device backend.
+ *
+ * These entry points replace the reference's CPU backend primitives behind its
+ * `Device` trait (src/device.rs:275-332) and its clang JIT
+ * (src/device/cpu.rs:151-394). A Rust `HipDevice` implementing that trait binds
+ * them one-to-one (binding stub in INTEGRATION.md):
+ *
+ *   Device::allocate        (device.rs:283, cpu.rs:277-280)  -> fg_hip_alloc(zero=1)
+ *   Buffer::ensure_allocated(device.rs:191-213)              -> fg_hip_alloc
+ *   Storage drop            (device.rs:66-70)                -> fg_hip_free
+ *   Device::copy_from_host  (device.rs:294, cpu.rs:282-302)  -> fg_hip_copy_h2d
+ *   Device::copy_to_host    (device.rs:302, cpu.rs:304-316)  -> fg_hip_copy_d2h
+ *   Device::compile         (device.rs:309-314, cpu.rs:151-208, 318-326) -> fg_hip_compile
+ *   Device::execute         (device.rs:321, cpu.rs:328-380)  -> fg_hip_launch
+ *   Program drop            (cpu.rs:95-106)                  -> fg_hip_program_free
+ *
+ * Every function returns 0 on success and a nonzero status otherwise; the
+ * message is available from fg_hip_last_error(). No exception crosses the ABI.
+ * Calls on one context are not thread-safe (the reference backend is !Send).
+ * All work is queued on the context's single stream in call order;
+ * fg_hip_copy_d2h returns after the data is on the host.
+ */
+#ifndef FERROGRAD_HIP_H
+#define FERROGRAD_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct fg_ctx fg_ctx;
+typedef struct fg_prog fg_prog;
+
+/* Kernel argument kinds, matching KernelArg (src/device.rs:242-251). */
+enum { FG_ARG_PTR = 0, FG_ARG_I32 = 1, FG_ARG_F32 = 2, FG_ARG_BOOL = 3 };
+
+typedef struct fg_arg {
+  int32_t kind; /* FG_ARG_* */
+  int32_t reserved;
+  union {
+    void* p;
+    int32_t i;
+    float f;
+    uint8_t b;
+  } v;
+} fg_arg;
+
+/* Status codes. */
+enum {
+  FG_OK = 0,
+  FG_ERR_HIP = 1,        /* a HIP runtime call failed */
+  FG_ERR_COMPILE = 2,    /* hiprtc rejected the source (log in last_error) */
+  FG_ERR_SYMBOL = 3,     /* the named kernel is not in the compiled module */
+  FG_ERR_ARGS = 4,       /* argument count or kind does not match */
+  FG_ERR_INVALID = 5     /* null handle, bad size, bad launch geometry */
+};
+
+/* Select device `ordinal`, create the context's stream. */
+int fg_hip_init(int device_ordinal, fg_ctx** out);
+int fg_hip_destroy(fg_ctx* ctx);
+
+/* Device memory. `zero` != 0 asks for zero-filled memory (the allocate
+ * contract, device.rs:282). Freed blocks are kept for reuse by later
+ * allocations of the same size; reuse is ordered on the context's stream. */
+int fg_hip_alloc(fg_ctx* ctx, size_t nbytes, int zero, void** dptr);
+int fg_hip_free(fg_ctx* ctx, void* dptr);
+/* Return cached free blocks to the driver. */
+int fg_hip_trim(fg_ctx* ctx);
+
+/* Host<->device copies. h2d returns once `src` may be reused; d2h returns once
+ * `dst` holds the data (all earlier work on the stream has completed). */
+int fg_hip_copy_h2d(fg_ctx* ctx, void* dst, const void* src, size_t nbytes);
+int fg_hip_copy_d2h(fg_ctx* ctx, void* dst, const void* src, size_t nbytes);
+int fg_hip_copy_d2d(fg_ctx* ctx, void* dst, const void* src, size_t nbytes);
+
+/* Compile HIP source for gfx950 with hiprtc and load kernel `func`. The code
+ * object is cached on disk keyed by a hash of source, options and target. */
+int fg_hip_compile(fg_ctx* ctx, const char* source, const char* func, int num_args, fg_prog** out);
+int fg_hip_program_free(fg_prog* prog);
+int fg_hip_program_num_args(const fg_prog* prog);
+
+/* Launch on the context's stream. `nargs` must equal the program's num_args. */
+int fg_hip_launch(fg_ctx* ctx, fg_prog* prog, const fg_arg* args, int nargs, const unsigned grid[3],
+                  const unsigned block[3], unsigned lds_bytes);
+
+/* Wait for all queued work. */
+int fg_hip_sync(fg_ctx* ctx);
+
+/* Timing events on the context's stream (slots 0..63). */
+int fg_hip_event_record(fg_ctx* ctx, int slot);
+int fg_hip_event_elapsed_ms(fg_ctx* ctx, int start_slot, int end_slot, float* ms);
+
+/* Device properties: CU count, clock (kHz), LDS per block, arch name. */
+int fg_hip_device_info(fg_ctx* ctx, int* cu_count, int* clock_khz, size_t* lds_per_block, char* arch,
+                       size_t arch_len);
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* fg_hip_last_error(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FERROGRAD_HIP_H */

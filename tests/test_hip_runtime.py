@@ -1,0 +1,167 @@
+"""The device C-ABI (include/ferrograd_hip.h), ported from the reference's
+backend tests (src/device/cpu.rs:415-649, src/device.rs:366-477) to HIP:
+compile-and-launch of hand-written kernels and the forceable error paths."""
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+ADD = r"""
+extern "C" __global__ void add(const float* a, const float* b, float* out, int n) {
+  int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) out[i] = a[i] + b[i];
+}"""
+
+MUL = r"""
+extern "C" __global__ void mul(float* out, const float* a, const float* b) {
+  int i = threadIdx.x;
+  if (i < 3) out[i] = a[i] * b[i];
+}"""
+
+NEG = r"""
+extern "C" __global__ void negate(float* output, const float* input) {
+  int i = threadIdx.x;
+  if (i < 3) output[i] = -input[i];
+}"""
+
+MIXED = r"""
+extern "C" __global__ void add_offset(float* out, const float* input, int offset, float scale) {
+  int i = threadIdx.x;
+  if (i < 2) out[i] = (input[offset + i] * scale);
+}"""
+
+SCALE_BOOL = r"""
+extern "C" __global__ void scale(const float* data, float* out, int n, float scalar, bool flip) {
+  int i = threadIdx.x;
+  if (i < n) out[i] = flip ? -data[i] * scalar : data[i] * scalar;
+}"""
+
+
+@pytest.fixture(scope="module")
+def ctx(fg):
+    from ferrograd_amd.hip import Context
+
+    return Context(0)
+
+
+def _upload(ctx, arr):
+    p = ctx.alloc(arr.nbytes)
+    ctx.h2d(p, arr)
+    return p
+
+
+def _download(ctx, p, n, dtype=np.float32):
+    out = np.empty(n, dtype=dtype)
+    ctx.d2h(out, p)
+    return out
+
+
+def test_device_info_is_gfx950(ctx):
+    info = ctx.info()
+    assert info["arch"].startswith("gfx950"), info
+    assert info["cu_count"] >= 256
+
+
+def test_compile_and_launch_add(ctx):  # cpu.rs:415-436
+    from ferrograd_amd.hip import Arg
+
+    prog = ctx.compile(ADD, "add", 4)
+    a = _upload(ctx, np.array([1, 2, 3], np.float32))
+    b = _upload(ctx, np.array([4, 5, 6], np.float32))
+    o = ctx.alloc(12)
+    ctx.launch(prog, [Arg.ptr(a), Arg.ptr(b), Arg.ptr(o), Arg.i32(3)], grid=(1, 1, 1), block=(64, 1, 1))
+    assert _download(ctx, o, 3).tolist() == [5.0, 7.0, 9.0]
+
+
+def test_device_mul_output_slot0(ctx):  # cpu.rs:559-583
+    from ferrograd_amd.hip import Arg
+
+    prog = ctx.compile(MUL, "mul", 3)
+    o = ctx.alloc(12)
+    a = _upload(ctx, np.array([2, 3, 4], np.float32))
+    b = _upload(ctx, np.array([5, 6, 7], np.float32))
+    ctx.launch(prog, [Arg.ptr(o), Arg.ptr(a), Arg.ptr(b)])
+    assert _download(ctx, o, 3).tolist() == [10.0, 18.0, 28.0]
+
+
+def test_device_unary(ctx):  # cpu.rs:585-608
+    from ferrograd_amd.hip import Arg
+
+    prog = ctx.compile(NEG, "negate", 2)
+    o = ctx.alloc(12)
+    i = _upload(ctx, np.array([1, -2, 3], np.float32))
+    ctx.launch(prog, [Arg.ptr(o), Arg.ptr(i)])
+    assert _download(ctx, o, 3).tolist() == [-1.0, 2.0, -3.0]
+
+
+def test_device_mixed_scalar_args(ctx):  # cpu.rs:610-637
+    from ferrograd_amd.hip import Arg
+
+    prog = ctx.compile(MIXED, "add_offset", 4)
+    o = ctx.alloc(8)
+    i = _upload(ctx, np.array([1, 2, 3, 4], np.float32))
+    ctx.launch(prog, [Arg.ptr(o), Arg.ptr(i), Arg.i32(1), Arg.f32(10.0)])
+    assert _download(ctx, o, 2).tolist() == [20.0, 30.0]
+
+
+def test_scalar_and_bool_args(ctx):  # cpu.rs:461-482 plus the u8 bool ABI (cpu.rs:108-113)
+    from ferrograd_amd.hip import Arg
+
+    prog = ctx.compile(SCALE_BOOL, "scale", 5)
+    d = _upload(ctx, np.array([1, 2, 3, 4], np.float32))
+    o = ctx.alloc(16)
+    ctx.launch(prog, [Arg.ptr(d), Arg.ptr(o), Arg.i32(4), Arg.f32(3.0), Arg.boolean(False)])
+    assert _download(ctx, o, 4).tolist() == [3.0, 6.0, 9.0, 12.0]
+    ctx.launch(prog, [Arg.ptr(d), Arg.ptr(o), Arg.i32(4), Arg.f32(3.0), Arg.boolean(True)])
+    assert _download(ctx, o, 4).tolist() == [-3.0, -6.0, -9.0, -12.0]
+
+
+def test_alloc_is_zeroed(ctx):  # device.rs:366-377, cpu.rs:277-280
+    p = ctx.alloc(4096, zero=True)
+    assert not _download(ctx, p, 1024).any()
+    ctx.free(p)
+    q = ctx.alloc(4096, zero=True)  # a reused block is zeroed again
+    assert not _download(ctx, q, 1024).any()
+
+
+def test_bad_source_is_compile_error(ctx):  # cpu.rs:484-497, 639-649
+    from ferrograd_amd.hip import FG_ERR_COMPILE, HipError
+
+    with pytest.raises(HipError) as e:
+        ctx.compile("this is not valid HIP!", "nope", 1)
+    assert e.value.code == FG_ERR_COMPILE
+    assert "hiprtc compilation failed" in str(e.value)
+
+
+def test_wrong_symbol_is_symbol_error(ctx):  # cpu.rs:499-516
+    from ferrograd_amd.hip import FG_ERR_SYMBOL, HipError
+
+    src = 'extern "C" __global__ void real_name(float* a, int n) {}'
+    with pytest.raises(HipError) as e:
+        ctx.compile(src, "wrong_name", 2)
+    assert e.value.code == FG_ERR_SYMBOL
+
+
+def test_wrong_arg_count_is_rejected(ctx):  # cpu.rs:331-336
+    from ferrograd_amd.hip import FG_ERR_ARGS, Arg, HipError
+
+    prog = ctx.compile(NEG, "negate", 2)
+    o = ctx.alloc(12)
+    with pytest.raises(HipError) as e:
+        ctx.launch(prog, [Arg.ptr(o)])
+    assert e.value.code == FG_ERR_ARGS
+    assert "expected 2 kernel args, got 1" in str(e.value)
+
+
+def test_events_time_kernels(ctx):
+    from ferrograd_amd.hip import Arg
+
+    prog = ctx.compile(ADD, "add", 4)
+    n = 1 << 20
+    a = ctx.alloc(4 * n)
+    b = ctx.alloc(4 * n)
+    o = ctx.alloc(4 * n)
+    ctx.record(0)
+    ctx.launch(prog, [Arg.ptr(a), Arg.ptr(b), Arg.ptr(o), Arg.i32(n)], grid=(n // 256, 1, 1), block=(256, 1, 1))
+    ctx.record(1)
+    assert ctx.elapsed_ms(0, 1) > 0.0

@@ -1,0 +1,198 @@
+"""HIP path vs the oracle CPU device on identical programs and inputs.
+
+Bars (north star): bit-exact for integer/index kernels, elementwise fp32
+within 1e-5 relative (checked bit-exact here: both sides round each op once),
+reductions and matmuls within 1e-4 * sum|terms| per element.
+"""
+import numpy as np
+import pytest
+
+from conftest import rel_err_bound, seeded
+
+pytestmark = pytest.mark.gpu
+
+
+def both(fn, cpu):
+    """Run fn(device) on the oracle CPU device and on HIP."""
+    return fn(cpu), fn("hip")
+
+
+# ── the reference's tensor tests (src/tensor.rs:1133-1313) on HIP ──────────
+def test_roundtrip(fg, hip):
+    t = fg.Tensor.new([1.0, 2.0, 3.0], [3], hip)
+    assert t.shape == (3,) and t.is_realized()
+    assert t.to_vec() == [1.0, 2.0, 3.0]
+
+
+def test_add_mul_relu(fg, hip):
+    a = fg.Tensor.new([1.0, 2.0, 3.0], [3], hip)
+    b = fg.Tensor.new([4.0, 5.0, 6.0], [3], hip)
+    assert a.add(b).to_vec() == [5.0, 7.0, 9.0]
+    c = fg.Tensor.new([2.0, 3.0, 4.0], [3], hip)
+    d = fg.Tensor.new([5.0, 6.0, 7.0], [3], hip)
+    assert c.mul(d).to_vec() == [10.0, 18.0, 28.0]
+    x = fg.Tensor.new([1.0, -2.0, 3.0, -4.0], [4], hip)
+    assert x.relu().to_vec() == [1.0, 0.0, 3.0, 0.0]
+
+
+def test_log_softmax_known_values(fg, hip):
+    r = fg.Tensor.new([0.0, 1.0], [1, 2], hip).log_softmax(1).realize().to_vec()
+    assert abs(r[0] - (-1.3132616)) < 1e-5 and abs(r[1] - (-0.31326166)) < 1e-5
+
+
+def test_cross_entropy_known_value(fg, hip):
+    logits = fg.Tensor.new([2.0, 0.0, 0.0, 2.0], [2, 2], hip)
+    targets = fg.Tensor.new([1.0, 0.0, 0.0, 1.0], [2, 2], hip)
+    assert abs(logits.cross_entropy(targets).realize().to_vec()[0] - 0.12692805) < 1e-5
+
+
+def test_sum_narrow_contiguous(fg, hip):
+    x = fg.Tensor.new([1.0, 2, 3, 4, 5, 6], [2, 3], hip)
+    assert x.sum([0]).to_vec() == [5.0, 7.0, 9.0]
+    n = x.narrow(0, 1, 1)
+    assert n.shape == (1, 3) and n.to_vec() == [4.0, 5.0, 6.0]
+    c = x.permute([1, 0]).contiguous()
+    assert c.shape == (3, 2) and c.to_vec() == [1.0, 4.0, 2.0, 5.0, 3.0, 6.0]
+
+
+def test_gradients(fg, hip):
+    x = fg.Tensor.new([1.0, 2, 3, 4], [2, 2], hip).narrow(0, 1, 1)
+    w = fg.Tensor.new([10.0, 20.0], [2, 1], hip).with_requires_grad(True)
+    g = x.matmul(w).sum([0, 1]).gradient([w])
+    assert g[0].to_vec() == [3.0, 4.0] and not g[0].requires_grad()
+    x2 = fg.Tensor.new([1.0, 2, 3, 4, 5, 6], [2, 3], hip).with_requires_grad(True)
+    g2 = x2.permute([1, 0]).contiguous().sum([0, 1]).gradient([x2])
+    assert g2[0].to_vec() == [1.0] * 6
+
+
+def test_realize_idempotent_and_aliasing(fg, hip):
+    a = fg.Tensor.new([1.0, 2.0], [2], hip)
+    b = a.add(fg.Tensor.new([3.0, 4.0], [2], hip))
+    assert b.realize().realize().to_vec() == [4.0, 6.0]
+    left = fg.Tensor.zeros([2], hip)
+    alias = left.alias()
+    left.replace(fg.Tensor.new([5.0, 7.0], [2], hip))
+    assert alias.to_vec() == [5.0, 7.0]
+
+
+def test_assign_in_place(fg, hip):
+    t = fg.Tensor.new([1.0, 2.0], [2], hip)
+    alias = t.alias()
+    t.assign(fg.Tensor.new([8.0, 9.0], [2], hip))
+    fg.Tensor.realize_many([t])
+    assert t.to_vec() == [8.0, 9.0] and alias.to_vec() == [8.0, 9.0]
+
+
+def test_backward_stores_gradients(fg, hip):
+    x = fg.Tensor.new([3.0], [1], hip).with_requires_grad(True)
+    y = fg.Tensor.new([5.0], [1], hip).with_requires_grad(True)
+    x.mul(y).sum([0]).backward()
+    assert x.grad().to_vec() == [5.0] and y.grad().to_vec() == [3.0]
+
+
+def test_int_and_bool_roundtrip(fg, hip):
+    t = fg.Tensor.new(np.array([1, 2, 3], np.int32), [3], hip).realize()
+    assert t.dtype == fg.I32 and t.numpy().tolist() == [1, 2, 3]
+    b = fg.Tensor.new([True, False, True], [3], hip).realize()
+    assert b.dtype == fg.BOOL and b.raw_bytes() == bytes([1, 0, 1])
+
+
+def test_demo_closed_form(fg, hip):  # examples/demo.rs:17-30
+    x = fg.Tensor.new([1.0, 2.0, 3.0, 4.0], [2, 2], hip)
+    w = fg.Tensor.new([0.1, 0.2, 0.3, 0.4], [2, 2], hip).with_requires_grad(True)
+    b = fg.Tensor.new([0.5, 0.6], [1, 2], hip).with_requires_grad(True)
+    loss = x.matmul(w).add(b).sum([0, 1])
+    # Realising the loss first would rewrite its graph to a buffer and leave
+    # backward() no path to w (tensor.rs:222-252, 971-980), as in the
+    # reference; the gradient pass runs before the loss is read.
+    loss.backward()
+    assert abs(loss.to_vec()[0] - 7.6) < 1e-5
+    np.testing.assert_allclose(w.grad().to_vec(), [4.0, 4.0, 6.0, 6.0], rtol=1e-6)
+    np.testing.assert_allclose(b.grad().to_vec(), [2.0, 2.0], rtol=1e-6)
+    fg.Sgd([w], 0.1).step()
+    np.testing.assert_allclose(w.to_vec(), [-0.3, -0.2, -0.3, -0.2], atol=1e-6)
+
+
+# ── benchmark configs at parity-test sizes ─────────────────────────────────
+def c1(fg, dev, x):
+    t = fg.Tensor.new(x, list(x.shape), dev)
+    return t.mul(fg.Tensor.scalar(0.5, dev)).add(fg.Tensor.scalar(1.0, dev)).relu().sum([1]).numpy()
+
+
+def c2(fg, dev, a, b, c):
+    ta, tb, tc = (fg.Tensor.new(v, list(v.shape), dev) for v in (a, b, c))
+    return ta.mul(tb).add(tc).relu().numpy()
+
+
+def c3(fg, dev, x, w, b):
+    tx = fg.Tensor.new(x, list(x.shape), dev)
+    tw = fg.Tensor.new(w, list(w.shape), dev)
+    tb = fg.Tensor.new(b, list(b.shape), dev)
+    return tx.matmul(tw.permute([1, 0])).add(tb).numpy()
+
+
+@pytest.mark.parametrize("n", [4, 4096, 1 << 20, 1000, 6])
+def test_c2_elementwise_bit_exact(fg, cpu, n):
+    r = seeded(2)
+    a, b, c = (r.uniform(-1, 1, n).astype(np.float32) for _ in range(3))
+    want, got = both(lambda d: c2(fg, d, a, b, c), cpu)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("shape", [(64, 64), (256, 512), (3, 5), (4096, 4096)])
+def test_c1_row_reduce(fg, cpu, shape):
+    x = seeded(1).standard_normal(shape).astype(np.float32)
+    want, got = both(lambda d: c1(fg, d, x), cpu)
+    scale = np.maximum(x * 0.5 + 1.0, 0).sum(1)
+    assert got.shape == want.shape == (shape[0], 1)
+    got, want = got[:, 0], want[:, 0]
+    assert rel_err_bound(got, want, scale, 1e-4) <= 1.0
+
+
+@pytest.mark.parametrize("mnk", [(64, 64, 64), (256, 128, 784), (128, 10, 128), (512, 512, 512), (100, 70, 30)])
+def test_c3_linear_forward(fg, cpu, mnk):
+    m, n, k = mnk
+    r = seeded(5)
+    x = r.standard_normal((m, k)).astype(np.float32)
+    w = r.uniform(-1 / 64, 1 / 64, (n, k)).astype(np.float32)
+    b = r.standard_normal(n).astype(np.float32)
+    want, got = both(lambda d: c3(fg, d, x, w, b), cpu)
+    scale = np.abs(x).astype(np.float64) @ np.abs(w).T.astype(np.float64) + np.abs(b)
+    assert rel_err_bound(got, want, scale, 1e-4) <= 1.0
+    exact = x.astype(np.float64) @ w.T.astype(np.float64) + b
+    assert rel_err_bound(got, exact, scale, 1e-4) <= 1.0
+
+
+def mlp_step(fg, dev, x, t, hidden, seed=42, lr=0.01, steps=1):
+    fg.reset_init_seed(seed)
+    dims = [x.shape[1]] + list(hidden) + [t.shape[1]]
+    layers = [fg.Linear(dims[i], dims[i + 1], dev) for i in range(len(dims) - 1)]
+    params = [p for l in layers for p in l.parameters()]
+    opt = fg.Sgd(params, lr)
+    tx = fg.Tensor.new(x, list(x.shape), dev)
+    tt = fg.Tensor.new(t, list(t.shape), dev)
+    losses = []
+    for _ in range(steps):
+        h = tx
+        for i, l in enumerate(layers):
+            h = l(h)
+            if i + 1 < len(layers):
+                h = h.relu()
+        loss = h.cross_entropy(tt)
+        opt.zero_grad()
+        loss.backward()
+        opt.step()
+        losses.append(loss.to_vec()[0])
+    return losses, [p.numpy() for p in params]
+
+
+@pytest.mark.parametrize("batch,hidden,steps", [(8, (16,), 2), (256, (128,), 2), (64, (96, 64), 1)])
+def test_mlp_train_step(fg, cpu, batch, hidden, steps):
+    r = seeded(7)
+    x = r.uniform(0, 1, (batch, 784)).astype(np.float32)
+    labels = np.floor(r.uniform(0, 1, batch) * 10).astype(np.int64)
+    t = np.eye(10, dtype=np.float32)[labels]
+    (lc, pc), (lh, ph) = both(lambda d: mlp_step(fg, d, x, t, hidden, steps=steps), cpu)
+    np.testing.assert_allclose(lh, lc, rtol=1e-4)
+    for a, b in zip(ph, pc):
+        np.testing.assert_allclose(a, b, rtol=1e-4, atol=1e-6)
