@@ -1,0 +1,262 @@
+#!/usr/bin/env python3
+"""Benchmark of ferrograd's realize path on one MI355X.
+
+Primary line (the `value`): C2, the pure elementwise bandwidth config
+`(a*b + c).relu()` over 2^26 f32 elements, as HBM GB/s of algorithmic traffic
+(3 reads + 1 write). A step is one realise of that lazy graph (schedule,
+lowering-cache lookup, launch) with the inputs resident in HBM.
+
+Also measured and reported under "secondary": C1 (fused elementwise + row
+reduction, GB/s), C3 (Linear forward x@W^T+b, MFMA fp32 TFLOP/s), C4 and C5
+(MLP train steps/s plus the GEMM kernels' share of the fp32 MFMA peak).
+
+Kernel durations come from HIP events recorded around every launch on the
+device's own stream during the timed region (fg_hip_profile_*). The CPU
+baseline is the oracle's restated reference clang backend on one pinned core.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--only c2] [--no-cpu]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import subprocess
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "fused-kernel HBM GB/s & MFMA fp32 TFLOP/s; MLP train steps/s (1 GPU)"
+HBM_PEAK_GBS = 8000.0           # MI355X HBM3E
+FP32_MFMA_PEAK_TFLOPS = 157.3   # MI355X dense fp32 matrix
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def timed(fg, ctx, step, steps: int, warmup: int):
+    """Run `step` warmup times untimed, then `steps` times between two device
+    synchronisations with launch profiling on. Returns (ms/step, profile)."""
+    for _ in range(warmup):
+        step()
+    fg.synchronize()
+    ctx.profile_read()  # drop anything recorded before
+    ctx.profile(True)
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    fg.synchronize()
+    t1 = time.perf_counter()
+    ctx.profile(False)
+    prof = ctx.profile_read()
+    return (t1 - t0) * 1000.0 / steps, prof
+
+
+def by_kernel(prof, steps):
+    """Average per-step device ms per kernel symbol."""
+    agg = {}
+    for r in prof:
+        agg.setdefault(r["kernel"], []).append(r["ms"])
+    return {k: {"calls_per_step": len(v) / steps, "avg_ms": float(np.mean(v)), "total_ms_per_step": float(np.sum(v)) / steps}
+            for k, v in agg.items()}
+
+
+def dominant(kern):
+    name = max(kern, key=lambda k: kern[k]["total_ms_per_step"])
+    return name, kern[name]
+
+
+def cpu_baseline(config: str):
+    try:
+        r = subprocess.run([sys.executable, "-m", "oracle.cpu_bench", config], cwd=ROOT, capture_output=True,
+                           text=True, timeout=300)
+        if r.returncode != 0:
+            log(f"cpu baseline {config} failed: {r.stderr[-2000:]}")
+            return None
+        return json.loads(r.stdout.strip().splitlines()[-1])
+    except Exception as e:  # noqa: BLE001
+        log(f"cpu baseline {config} failed: {e}")
+        return None
+
+
+def bench_c2(fg, ctx, steps, warmup):
+    from ferrograd_amd import Tensor
+
+    n = 1 << 26
+    r = np.random.default_rng(2)
+    a, b, c = (Tensor.new(r.uniform(-1, 1, n).astype(np.float32), [n], "hip") for _ in range(3))
+    holder = {}
+
+    def step():
+        holder["out"] = a.mul(b).add(c).relu().realize()
+
+    ms, prof = timed(fg, ctx, step, steps, warmup)
+    kern = by_kernel(prof, steps)
+    name, dk = dominant(kern)
+    alg = 4 * n * 4
+    return {"ms_per_step": ms, "gbs": alg / (ms / 1e3) / 1e9, "kernels": kern, "dominant": name,
+            "roofline": {"bound": "hbm", "achieved": alg / (dk["avg_ms"] / 1e3) / 1e9, "peak": HBM_PEAK_GBS,
+                         "unit": "GB/s", "frac": alg / (dk["avg_ms"] / 1e3) / 1e9 / HBM_PEAK_GBS, "traffic": None,
+                         "kernel": name, "algorithmic_bytes": alg, "kernel_avg_ms": dk["avg_ms"]}}
+
+
+def bench_c1(fg, ctx, steps, warmup):
+    from ferrograd_amd import Tensor
+
+    # Six distinct inputs (6 x 64 MiB > the 256 MB Infinity Cache) rotate so
+    # every step streams from HBM.
+    xs = [Tensor.new(np.random.default_rng(1 + i).standard_normal((4096, 4096)).astype(np.float32), [4096, 4096], "hip")
+          for i in range(6)]
+    s0, s1 = Tensor.scalar(0.5, "hip"), Tensor.scalar(1.0, "hip")
+    it = {"i": 0, "out": None}
+
+    def step():
+        x = xs[it["i"] % len(xs)]
+        it["i"] += 1
+        it["out"] = x.mul(s0).add(s1).relu().sum([1]).realize()
+
+    ms, prof = timed(fg, ctx, step, steps, warmup)
+    kern = by_kernel(prof, steps)
+    name, dk = dominant(kern)
+    alg = 4096 * 4096 * 4 + 4096 * 4
+    ach = alg / (dk["avg_ms"] / 1e3) / 1e9
+    return {"ms_per_step": ms, "gbs": alg / (ms / 1e3) / 1e9, "kernels": kern,
+            "roofline": {"bound": "hbm", "achieved": ach, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": ach / HBM_PEAK_GBS, "kernel": name, "kernel_avg_ms": dk["avg_ms"]}}
+
+
+def bench_c3(fg, ctx, steps, warmup):
+    from ferrograd_amd import Tensor
+
+    r = np.random.default_rng(5)
+    x = Tensor.new(r.standard_normal((4096, 4096)).astype(np.float32), [4096, 4096], "hip")
+    w = Tensor.new(np.random.default_rng(6).uniform(-1 / 64, 1 / 64, (4096, 4096)).astype(np.float32), [4096, 4096],
+                   "hip")
+    b = Tensor.zeros([4096], "hip")
+    holder = {}
+
+    def step():
+        holder["y"] = x.matmul(w.permute([1, 0])).add(b).realize()
+
+    ms, prof = timed(fg, ctx, step, steps, warmup)
+    kern = by_kernel(prof, steps)
+    gemm = [k for k in kern if k.endswith("_gemm")]
+    flops = 2 * 4096 ** 3
+    g = kern[gemm[0]] if gemm else dominant(kern)[1]
+    tf = flops / (g["avg_ms"] / 1e3) / 1e12
+    return {"ms_per_step": ms, "tflops_step": flops / (ms / 1e3) / 1e12, "kernels": kern,
+            "roofline": {"bound": "mfma", "achieved": tf, "peak": FP32_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
+                         "frac": tf / FP32_MFMA_PEAK_TFLOPS, "kernel": gemm[0] if gemm else None,
+                         "kernel_avg_ms": g["avg_ms"]}}
+
+
+def mlp_gemm_flops(batch, dims):
+    """Forward + backward GEMM FLOPs of one step (x needs no gradient)."""
+    f = 0
+    for i in range(len(dims) - 1):
+        k, n = dims[i], dims[i + 1]
+        f += 2 * batch * k * n          # forward
+        f += 2 * batch * k * n          # dW
+        if i > 0:
+            f += 2 * batch * k * n      # dX
+    return f
+
+
+def bench_mlp(fg, ctx, steps, warmup, batch, dims):
+    from ferrograd_amd.mlp import mlp_setup
+
+    step, _ = mlp_setup(fg, "hip", batch=batch, dims=dims)
+    losses = []
+    ms, prof = timed(fg, ctx, lambda: losses.append(step()), steps, warmup)
+    kern = by_kernel(prof, steps)
+    gemm_ms = sum(v["total_ms_per_step"] for k, v in kern.items() if k.endswith("_gemm"))
+    dev_ms = sum(v["total_ms_per_step"] for v in kern.values())
+    flops = mlp_gemm_flops(batch, dims)
+    return {"ms_per_step": ms, "steps_per_s": 1e3 / ms, "device_ms_per_step": dev_ms,
+            "kernels_per_step": sum(v["calls_per_step"] for v in kern.values()),
+            "gemm_flops_per_step": flops, "gemm_ms_per_step": gemm_ms,
+            "mfma_frac_of_gemm_kernels": (flops / (gemm_ms / 1e3) / 1e12 / FP32_MFMA_PEAK_TFLOPS) if gemm_ms else None,
+            "loss_first_last": [losses[0], losses[-1]] if losses else None, "kernels": kern}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--only", default=None, help="run one config: c1,c2,c3,c4,c5")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--kernels", action="store_true", help="include per-kernel tables")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one MI355X; --gpus {args.gpus} is not supported in this build "
+              "(multi-GPU sharding is design-only, see DESIGN.md)", file=sys.stderr)
+        sys.exit(2)
+
+    import ferrograd_amd as fg
+    from ferrograd_amd.hip import Context
+
+    ctx = Context.of_device()
+    info = ctx.info()
+    log(f"device: {info}")
+    only = set(args.only.split(",")) if args.only else {"c1", "c2", "c3", "c4", "c5"}
+    sec = {}
+    t_start = time.time()
+    if "c2" in only:
+        c2 = bench_c2(fg, ctx, args.steps, args.warmup)
+        log(f"c2: {c2['gbs']:.1f} GB/s per step, kernel {c2['roofline']['achieved']:.1f} GB/s "
+            f"({100 * c2['roofline']['frac']:.1f}% of HBM peak)")
+    if "c1" in only:
+        sec["c1"] = bench_c1(fg, ctx, args.steps, args.warmup)
+        log(f"c1: {sec['c1']['gbs']:.1f} GB/s, kernel {sec['c1']['roofline']['achieved']:.1f} GB/s")
+    if "c3" in only:
+        sec["c3"] = bench_c3(fg, ctx, max(5, args.steps // 2), args.warmup)
+        log(f"c3: gemm {sec['c3']['roofline']['achieved']:.1f} TFLOP/s ({100 * sec['c3']['roofline']['frac']:.1f}%)")
+    if "c4" in only:
+        sec["c4"] = bench_mlp(fg, ctx, args.steps, args.warmup, 256, (784, 128, 10))
+        log(f"c4: {sec['c4']['steps_per_s']:.1f} steps/s")
+    if "c5" in only:
+        sec["c5"] = bench_mlp(fg, ctx, max(3, args.steps // 4), 2, 8192, (784, 4096, 4096, 10))
+        log(f"c5: {sec['c5']['steps_per_s']:.2f} steps/s, gemm {sec['c5']['mfma_frac_of_gemm_kernels']}")
+    log(f"gpu legs took {time.time() - t_start:.1f}s")
+
+    cpu = {}
+    if not args.no_cpu:
+        for c in sorted(only & {"c1", "c2", "c3", "c4"}):
+            cpu[c] = cpu_baseline(c)
+            log(f"cpu {c}: {cpu[c]}")
+    for c, v in cpu.items():
+        if c in sec and v:
+            sec[c]["cpu_baseline"] = v
+    if not args.kernels:
+        for v in sec.values():
+            v.pop("kernels", None)
+
+    if "c2" in only:
+        c2cpu = cpu.get("c2")
+        line = {
+            "metric": METRIC, "value": c2["gbs"], "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+            "warmup": args.warmup, "ms_per_step": c2["ms_per_step"], "higher_is_better": True, "scaling": "weak",
+            "vs_baseline": None, "dtype": "f32", "data": "synthetic (seeded U(-1,1))",
+            "config": {"workload": "C2: out = (a*b + c).relu(), a,b,c f32[2^26], one fused kernel (3 reads + 1 write)",
+                       "elements": 1 << 26, "algorithmic_bytes_per_step": 4 * (1 << 26) * 4},
+            "roofline": c2["roofline"],
+            "cpu_baseline": ({"value": c2cpu["value"], "unit": "GB/s", "cores": c2cpu["cores"], "kind": c2cpu["kind"],
+                              "sample": c2cpu["sample"]} if c2cpu else None),
+            "device": info, "secondary": sec,
+        }
+    else:
+        k = sorted(sec)[0]
+        line = {"metric": METRIC, "value": None, "unit": None, "n_gpus": 1, "steps": args.steps,
+                "warmup": args.warmup, "config": {"workload": ",".join(sorted(only))}, "secondary": sec,
+                "device": info}
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()

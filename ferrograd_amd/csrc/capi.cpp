@@ -314,6 +314,13 @@ int fg_synchronize(int device) {
   return guard([&] { fg::get_device(to_dev(device)).synchronize(); });
 }
 
+int fg_device_context(int device, void** ctx) {
+  return guard([&] {
+    FG_CHECK(device == FG_DEV_HIP, "fg_device_context: only the HIP device has a context");
+    *ctx = fg::hip_context_raw();
+  });
+}
+
 int fg_stats(uint64_t* k, uint64_t* p, uint64_t* h) {
   auto& s = fg::realize_stats();
   if (k) *k = s.kernels_launched;
@@ -375,8 +382,8 @@ int fg_debug_plan(fg_tensor** roots, int n, int fuse, int render, char* buf, siz
         os << "]";
         if (render) {
           fg::UOp k = fg::gpu_optimize(fg::rangeify(it.sink));
-          auto rk = fg::render_hip(k, "kernel_" + std::to_string(i));
-          os << ", \"class\": \"" << rk.kind << "\", \"grid\": [" << rk.grid[0] << ", " << rk.grid[1] << ", "
+          auto rk = fg::render_hip_stable(k);
+          os << ", \"name\": \"" << rk.name << "\", \"class\": \"" << rk.kind << "\", \"grid\": [" << rk.grid[0] << ", " << rk.grid[1] << ", "
              << rk.grid[2] << "], \"block\": [" << rk.block[0] << ", " << rk.block[1] << ", " << rk.block[2]
              << "], \"source\": \"" << json_escape(rk.source) << "\"";
         }

@@ -110,5 +110,7 @@ Device& get_device(DeviceId id);
 bool has_device(DeviceId id);
 void register_device(DeviceId id, Device* dev);
 Device* make_hip_device();
+// The HIP device's runtime context (an fg_ctx*), created on first use.
+void* hip_context_raw();
 
 }  // namespace fg

@@ -1126,6 +1126,10 @@ RenderedKernel render_hip(const UOp& kernel, const std::string& name, int force_
            "in-place update reads its destination at another index; the HIP device runs kernels in parallel and "
            "cannot reproduce the sequential CPU order");
   KernelClass k = force_class >= 0 ? static_cast<KernelClass>(force_class) : classify_kernel(kernel);
+  if (!ki.reduces.empty() && k == KernelClass::Elementwise) k = KernelClass::Serial;
+  // The symbol carries the lowering class so profiles name what ran.
+  static const char* suffix[] = {"_gemm", "_ew", "_rowred", "_colred", "_serial"};
+  const std::string sym = name + suffix[static_cast<int>(k)];
   std::vector<std::pair<int, DType>> params;
   for (auto& [slot, p] : ki.params) params.emplace_back(slot, p.dtype());
   RenderedKernel rk;
@@ -1133,18 +1137,36 @@ RenderedKernel render_hip(const UOp& kernel, const std::string& name, int force_
     case KernelClass::Gemm: {
       GemmMatch g;
       FG_CHECK(match_gemm(ki, &g), "kernel does not match the MFMA GEMM pattern");
-      rk = render_gemm(ki, g, name);
+      rk = render_gemm(ki, g, sym);
       break;
     }
-    case KernelClass::Elementwise:
-      if (!ki.reduces.empty()) return render_hip(kernel, name, static_cast<int>(KernelClass::Serial));
-      rk = render_elementwise(ki, name);
-      break;
-    case KernelClass::RowReduce: rk = render_row_reduce(ki, name); break;
-    case KernelClass::ColumnReduce: rk = render_column_reduce(ki, name); break;
-    case KernelClass::Serial: rk = render_serial(ki, name); break;
+    case KernelClass::Elementwise: rk = render_elementwise(ki, sym); break;
+    case KernelClass::RowReduce: rk = render_row_reduce(ki, sym); break;
+    case KernelClass::ColumnReduce: rk = render_column_reduce(ki, sym); break;
+    case KernelClass::Serial: rk = render_serial(ki, sym); break;
   }
   rk.params = params;
+  return rk;
+}
+
+// Kernel symbols are named by a hash of their source, so the same kernel gets
+// the same name (and the same cached code object) in every process.
+RenderedKernel render_hip_stable(const UOp& kernel) {
+  static const std::string kPlaceholder = "FGKERNELNAME";
+  RenderedKernel rk = render_hip(kernel, kPlaceholder);
+  uint64_t h = 1469598103934665603ULL;
+  for (unsigned char c : rk.source) {
+    h ^= c;
+    h *= 1099511628211ULL;
+  }
+  char hex[32];
+  std::snprintf(hex, sizeof(hex), "k%012llx", static_cast<unsigned long long>(h & 0xffffffffffffULL));
+  auto replace_all = [&](std::string& s) {
+    for (size_t p = s.find(kPlaceholder); p != std::string::npos; p = s.find(kPlaceholder, p))
+      s.replace(p, kPlaceholder.size(), hex);
+  };
+  replace_all(rk.source);
+  replace_all(rk.name);
   return rk;
 }
 

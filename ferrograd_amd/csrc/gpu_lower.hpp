@@ -45,6 +45,8 @@ UOp gpu_optimize(const UOp& rangeified);
 // Render a gfx950 HIP kernel (source + launch geometry) for an optimized
 // kernel. `force` selects a class for tests (Serial is always valid).
 RenderedKernel render_hip(const UOp& kernel, const std::string& name, int force_class = -1);
+// render_hip with the symbol named by a hash of the source ("k<hash>_<class>").
+RenderedKernel render_hip_stable(const UOp& kernel);
 KernelClass classify_kernel(const UOp& kernel);
 
 }  // namespace fg

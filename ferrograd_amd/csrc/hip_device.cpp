@@ -76,7 +76,8 @@ class HipDevice : public Device {
   UOp optimize(const UOp& rangeified) override { return gpu_optimize(rangeified); }
 
   RenderedKernel render(const UOp& optimized, const std::string& name) override {
-    return render_hip(optimized, name);
+    (void)name;  // symbols are content-named so code objects cache across runs
+    return render_hip_stable(optimized);
   }
 
   std::shared_ptr<Program> compile(const RenderedKernel& rk, size_t num_args) override {
@@ -132,7 +133,7 @@ class HipDevice : public Device {
 
 Device* make_hip_device() { return new HipDevice(); }
 
-fg_ctx* hip_context() {
+void* hip_context_raw() {
   auto& d = static_cast<HipDevice&>(get_device(DeviceId::Hip));
   return d.ctx();
 }

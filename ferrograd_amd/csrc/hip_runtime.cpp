@@ -118,6 +118,15 @@ struct fg_ctx {
   size_t staging_head = 0;
   hipEvent_t staging_event = nullptr;
   bool staging_event_pending = false;
+  // Launch profiling.
+  bool profiling = false;
+  std::vector<hipEvent_t> event_pool;
+  struct Rec {
+    std::string name;
+    hipEvent_t a, b;
+  };
+  std::vector<Rec> records;
+  std::string profile_json;
 };
 
 namespace {
@@ -342,8 +351,56 @@ int fg_hip_launch(fg_ctx* c, fg_prog* p, const fg_arg* args, int nargs, const un
       default: return set_err(FG_ERR_ARGS, "fg_hip_launch: unknown argument kind " + std::to_string(args[i].kind));
     }
   }
+  hipEvent_t ea = nullptr, eb = nullptr;
+  if (c->profiling) {
+    for (hipEvent_t* e : {&ea, &eb}) {
+      if (!c->event_pool.empty()) {
+        *e = c->event_pool.back();
+        c->event_pool.pop_back();
+      } else {
+        HIP_TRY(hipEventCreate(e));
+      }
+    }
+    HIP_TRY(hipEventRecord(ea, c->stream));
+  }
   HIP_TRY(hipModuleLaunchKernel(p->func, grid[0], grid[1], grid[2], block[0], block[1], block[2], lds, c->stream,
                                 params, nullptr));
+  if (c->profiling) {
+    HIP_TRY(hipEventRecord(eb, c->stream));
+    c->records.push_back({p->name, ea, eb});
+  }
+  return FG_OK;
+}
+
+int fg_hip_profile_enable(fg_ctx* c, int on) {
+  if (!c) return set_err(FG_ERR_INVALID, "fg_hip_profile_enable: null context");
+  c->profiling = on != 0;
+  return FG_OK;
+}
+
+int fg_hip_profile_read(fg_ctx* c, char* buf, size_t len, size_t* needed) {
+  if (!c) return set_err(FG_ERR_INVALID, "fg_hip_profile_read: null context");
+  if (!buf) {
+    HIP_TRY(hipStreamSynchronize(c->stream));
+    std::ostringstream os;
+    os << "[";
+    for (size_t i = 0; i < c->records.size(); i++) {
+      float ms = 0.f;
+      HIP_TRY(hipEventElapsedTime(&ms, c->records[i].a, c->records[i].b));
+      os << (i ? ", " : "") << "{\"kernel\": \"" << c->records[i].name << "\", \"ms\": " << ms << "}";
+      c->event_pool.push_back(c->records[i].a);
+      c->event_pool.push_back(c->records[i].b);
+    }
+    os << "]";
+    c->records.clear();
+    c->profile_json = os.str();
+  }
+  if (needed) *needed = c->profile_json.size() + 1;
+  if (buf && len) {
+    size_t m = std::min(len - 1, c->profile_json.size());
+    std::memcpy(buf, c->profile_json.data(), m);
+    buf[m] = '\0';
+  }
   return FG_OK;
 }
 

@@ -77,6 +77,9 @@ def api() -> ctypes.CDLL:
             "fg_hip_event_elapsed_ms": (c_int, [P, c_int, c_int, ctypes.POINTER(ctypes.c_float)]),
             "fg_hip_device_info": (c_int, [P, ctypes.POINTER(c_int), ctypes.POINTER(c_int), ctypes.POINTER(c_size),
                                            ctypes.c_char_p, c_size]),
+            "fg_hip_profile_enable": (c_int, [P, c_int]),
+            "fg_hip_profile_read": (c_int, [P, ctypes.c_char_p, c_size, ctypes.POINTER(c_size)]),
+            "fg_device_context": (c_int, [c_int, PP]),
             "fg_hip_last_error": (ctypes.c_char_p, []),
         }
         for name, (res, args) in sigs.items():
@@ -105,9 +108,35 @@ def check(rc: int) -> None:
 class Context:
     """An fg_ctx (device + stream)."""
 
-    def __init__(self, ordinal: int = 0):
+    def __init__(self, ordinal: int = 0, handle: int | None = None):
         self.h = ctypes.c_void_p()
-        check(api().fg_hip_init(ordinal, ctypes.byref(self.h)))
+        if handle is not None:
+            self.h = ctypes.c_void_p(handle)
+        else:
+            check(api().fg_hip_init(ordinal, ctypes.byref(self.h)))
+
+    @staticmethod
+    def of_device() -> "Context":
+        """The HIP device's own context: the stream realised kernels run on."""
+        h = ctypes.c_void_p()
+        rc = api().fg_device_context(1, ctypes.byref(h))
+        if rc != 0:
+            from . import FerrogradError
+
+            raise FerrogradError(api().fg_last_error().decode())
+        return Context(handle=h.value)
+
+    def profile(self, on: bool) -> None:
+        check(api().fg_hip_profile_enable(self.h, int(on)))
+
+    def profile_read(self) -> list:
+        import json
+
+        need = ctypes.c_size_t()
+        check(api().fg_hip_profile_read(self.h, None, 0, ctypes.byref(need)))
+        buf = ctypes.create_string_buffer(need.value + 1)
+        check(api().fg_hip_profile_read(self.h, buf, need.value + 1, ctypes.byref(need)))
+        return json.loads(buf.value.decode())
 
     def alloc(self, nbytes: int, zero: bool = True) -> int:
         p = ctypes.c_void_p()

@@ -86,8 +86,11 @@ int fg_sgd_zero_grad(fg_sgd* s);
 int fg_sgd_step(fg_sgd* s);
 int fg_sgd_free(fg_sgd* s);
 
-/* Device control and statistics. */
+/* Device control and statistics. fg_device_context returns the HIP device's
+ * fg_ctx (include/ferrograd_hip.h) — the stream every realised kernel runs
+ * on — for event timing and launch profiling. */
 int fg_synchronize(int device);
+int fg_device_context(int device, void** ctx);
 int fg_stats(uint64_t* kernels_launched, uint64_t* programs_compiled, uint64_t* lowering_hits);
 int fg_clear_caches(void);
 

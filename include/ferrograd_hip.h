@@ -92,6 +92,13 @@ int fg_hip_sync(fg_ctx* ctx);
 int fg_hip_event_record(fg_ctx* ctx, int slot);
 int fg_hip_event_elapsed_ms(fg_ctx* ctx, int start_slot, int end_slot, float* ms);
 
+/* Launch profiling: while enabled, every fg_hip_launch on the context is
+ * bracketed by two events on its stream. fg_hip_profile_read waits for the
+ * stream and returns, as JSON, [{"kernel": name, "ms": duration}, ...] for the
+ * launches since the last read (two calls: buf == NULL reports the size). */
+int fg_hip_profile_enable(fg_ctx* ctx, int on);
+int fg_hip_profile_read(fg_ctx* ctx, char* buf, size_t len, size_t* needed);
+
 /* Device properties: CU count, clock (kHz), LDS per block, arch name. */
 int fg_hip_device_info(fg_ctx* ctx, int* cu_count, int* clock_khz, size_t* lds_per_block, char* arch,
                        size_t arch_len);

@@ -1,0 +1,91 @@
+"""TEST INFRASTRUCTURE — CPU baseline leg of bench.py.
+
+Times the oracle CPU device (the reference's clang backend restated:
+clang -shared -O3 -march=native, one call per kernel on the calling thread,
+cpu.rs:151-208, 328-380) on a bounded sample of a benchmark config, pinned to
+one core like the reference. Prints one JSON object.
+
+Usage: python -m oracle.cpu_bench <c1|c2|c3|c4> [--core N]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+
+def _time(fn, runs: int, warmup: int = 1) -> float:
+    for _ in range(warmup):
+        fn()
+    ts = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    return statistics.median(ts)
+
+
+def main() -> None:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("config")
+    ap.add_argument("--core", type=int, default=None)
+    args = ap.parse_args()
+    cores = sorted(os.sched_getaffinity(0))
+    core = args.core if args.core is not None else cores[0]
+    os.sched_setaffinity(0, {core})
+
+    import numpy as np
+
+    import oracle
+    import ferrograd_amd as fg
+    from ferrograd_amd import Tensor
+
+    oracle.load()
+    dev = "cpu"
+    out = {"cores": 1, "kind": "port", "core": core}
+    if args.config == "c2":
+        n = 1 << 26
+        r = np.random.default_rng(2)
+        a, b, c = (Tensor.new(r.uniform(-1, 1, n).astype(np.float32), [n], dev) for _ in range(3))
+        step = lambda: a.mul(b).add(c).relu().realize()  # noqa: E731
+        t = _time(step, runs=5)
+        out.update(value=4 * n * 4 / t / 1e9, unit="GB/s", seconds=t,
+                   sample="full C2 (2^26 elements, 2 reference kernels), median of 5 after 1 warmup")
+    elif args.config == "c1":
+        x = Tensor.new(np.random.default_rng(1).standard_normal((4096, 4096)).astype(np.float32), [4096, 4096], dev)
+        s0, s1 = Tensor.scalar(0.5, dev), Tensor.scalar(1.0, dev)
+        step = lambda: x.mul(s0).add(s1).relu().sum([1]).realize()  # noqa: E731
+        t = _time(step, runs=5)
+        out.update(value=(4096 * 4096 * 4 + 4096 * 4) / t / 1e9, unit="GB/s", seconds=t,
+                   sample="full C1 ([4096,4096], 2 reference kernels), median of 5 after 1 warmup")
+    elif args.config == "c3":
+        rows = 256
+        r = np.random.default_rng(5)
+        x = Tensor.new(r.standard_normal((rows, 4096)).astype(np.float32), [rows, 4096], dev)
+        w = Tensor.new(r.uniform(-1 / 64, 1 / 64, (4096, 4096)).astype(np.float32), [4096, 4096], dev)
+        b = Tensor.zeros([4096], dev)
+        step = lambda: x.matmul(w.permute([1, 0])).add(b).realize()  # noqa: E731
+        t = _time(step, runs=3)
+        flops = 2 * rows * 4096 * 4096
+        out.update(value=flops / t / 1e12, unit="TFLOP/s", seconds=t,
+                   sample=f"C3 row block x[{rows},4096] @ W[4096,4096]^T + b (1/16 of the rows), median of 3")
+    elif args.config == "c4":
+        from ferrograd_amd.mlp import mlp_setup
+
+        step, _ = mlp_setup(fg, dev, batch=256, dims=(784, 128, 10))
+        t = _time(step, runs=10, warmup=2)
+        out.update(value=1.0 / t, unit="steps/s", seconds=t, sample="C4 train step, median of 10 after 2 warmup")
+    else:
+        raise SystemExit(f"unknown config {args.config}")
+    print(json.dumps(out))
+
+
+if __name__ == "__main__":
+    main()
