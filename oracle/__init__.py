@@ -39,3 +39,22 @@ def load() -> ctypes.CDLL:
             raise RuntimeError("fg_oracle_register failed")
         _loaded = l
     return _loaded
+
+
+def plan_c(roots) -> list:
+    """Oracle C source of every kernel the reference schedule makes for `roots`."""
+    import json
+
+    l = load()
+    l.fg_oracle_plan_c.restype = ctypes.c_int
+    l.fg_oracle_plan_c.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.c_int, ctypes.c_char_p, ctypes.c_size_t,
+                                   ctypes.POINTER(ctypes.c_size_t)]
+    arr = (ctypes.c_void_p * max(1, len(roots)))(*[t._h.value for t in roots])
+    need = ctypes.c_size_t()
+    rc = l.fg_oracle_plan_c(arr, len(roots), None, 0, ctypes.byref(need))
+    buf = ctypes.create_string_buffer(need.value + 1)
+    l.fg_oracle_plan_c(arr, len(roots), buf, need.value + 1, ctypes.byref(need))
+    out = json.loads(buf.value.decode())
+    if rc != 0:
+        raise RuntimeError(out.get("error", "fg_oracle_plan_c failed"))
+    return out["kernels"]

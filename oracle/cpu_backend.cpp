@@ -37,8 +37,9 @@
 #include <sstream>
 
 #include "device.hpp"
-#include "gpu_lower.hpp"  // Affine/KernelInfo helpers are IR utilities, not HIP codegen
 #include "ir.hpp"
+#include "schedule.hpp"
+#include "tensor.hpp"
 
 namespace fg {
 namespace oracle {
@@ -610,10 +611,64 @@ int fg_oracle_register(void) {
   return 0;
 }
 
-// Render the oracle C for a kernel plan without compiling (debugging aid).
-int fg_oracle_render_c(const char** out) {
-  (void)out;
-  return 0;
+}  // extern "C"
+
+// Same layout as the front end's handle (ferrograd_amd/csrc/capi.cpp).
+struct fg_tensor {
+  fg::Tensor t;
+};
+
+extern "C" {
+
+// Schedule `roots` with the reference's rules (no fusion) and return, as JSON,
+// the oracle C source of every kernel: {"kernels": ["...", ...]}. Two calls:
+// buf == NULL plans and reports the size; a second call copies the result.
+int fg_oracle_plan_c(fg_tensor** roots, int n, char* buf, size_t len, size_t* needed) {
+  static std::string last;
+  if (buf) {
+    size_t m = len ? std::min(len - 1, last.size()) : 0;
+    if (len) {
+      std::memcpy(buf, last.data(), m);
+      buf[m] = '\0';
+    }
+    if (needed) *needed = last.size() + 1;
+    return 0;
+  }
+  try {
+    std::vector<fg::UOp> rs;
+    fg::UOpSet seen;
+    for (int i = 0; i < n; i++) {
+      if (roots[i]->t.is_realized()) continue;
+      fg::UOp u = roots[i]->t.uop();
+      if (seen.insert(u).second) rs.push_back(u);
+    }
+    std::ostringstream os;
+    os << "{\"kernels\": [";
+    if (!rs.empty()) {
+      auto plan = fg::schedule_many(rs, fg::ScheduleOptions{});
+      for (size_t i = 0; i < plan.items.size(); i++) {
+        fg::UOp k = fg::oracle::reference_optimize(fg::rangeify(plan.items[i].sink),
+                                                   fg::oracle::parse_opt(std::getenv("OPT")));
+        std::string src = fg::oracle::render_c(k, "kernel_" + std::to_string(i));
+        os << (i ? ", " : "") << "\"";
+        for (char c : src) {
+          if (c == '"') os << "\\\"";
+          else if (c == '\\') os << "\\\\";
+          else if (c == '\n') os << "\\n";
+          else os << c;
+        }
+        os << "\"";
+      }
+    }
+    os << "]}";
+    last = os.str();
+    if (needed) *needed = last.size() + 1;
+    return 0;
+  } catch (const std::exception& e) {
+    last = std::string("{\"error\": \"") + e.what() + "\"}";
+    if (needed) *needed = last.size() + 1;
+    return 1;
+  }
 }
 
 }  // extern "C"

@@ -1,0 +1,132 @@
+"""Kernel partitioning (src/schedule.rs) — the reference's schedule tests
+(schedule.rs:421-570) through the public API, plus the value-preserving fusion
+the HIP device enables. CPU only: plans are inspected, not run."""
+import numpy as np
+import pytest
+
+
+def plan(fg, roots, fuse=False, render=False):
+    return fg.debug_plan(roots, fuse=fuse, render_hip=render)["items"]
+
+
+def test_nested_reductions_materialize_via_shared_buffer(fg, cpu):  # schedule.rs:421-434
+    x = fg.Tensor.new([1.0, 2.0, 3.0, 4.0], [2, 2], cpu)
+    items = plan(fg, [x.sum([1]).sum([0])])
+    assert len(items) == 2
+    assert items[1]["inputs"][0] == {"buffer": items[0]["output"]}
+
+
+def test_shared_subexpression_materializes_once(fg, cpu):  # schedule.rs:436-464
+    left = fg.Tensor.new([1.0, 2, 3, 4], [2, 2], cpu)
+    right = fg.Tensor.new([10.0, 20, 30, 40], [2, 2], cpu)
+    shared = left.add(right)
+    root = shared.sum([1]).add(shared.max([1]))
+    items = plan(fg, [root])
+    assert len(items) == 4
+    assert items[1]["inputs"][0] == {"buffer": items[0]["output"]}
+    assert items[2]["inputs"][0] == {"buffer": items[0]["output"]}
+    assert items[3]["inputs"][0] == {"buffer": items[1]["output"]}
+    assert items[3]["inputs"][1] == {"buffer": items[2]["output"]}
+
+
+def test_each_shrink_occurrence_gets_its_own_scalar(fg, cpu):  # schedule.rs:466-490
+    x = fg.Tensor.new([1.0, 2, 3, 4, 5, 6], [3, 2], cpu)
+    items = plan(fg, [x.narrow(0, 0, 2).add(x.narrow(0, 1, 2))])
+    scalars = [i for it in items for i in it["inputs"] if "i32" in i or "f32" in i or "bool" in i]
+    assert len(scalars) == 2
+    assert sorted(s["i32"] for s in scalars) == [0, 1]
+
+
+def test_store_turns_shrink_start_into_scalar(fg, cpu):  # schedule.rs:492-506
+    src = fg.Tensor.new([1.0, 2, 3, 4, 5, 6], [3, 2], cpu)
+    dst = fg.Tensor.new([0.0, 0, 0, 0], [2, 2], cpu)
+    dst.assign(src.narrow(0, 1, 2))
+    items = plan(fg, [dst])
+    assert len(items) == 1 and items[0]["output"] is None
+    ins = items[0]["inputs"]
+    assert "buffer" in ins[0] and "buffer" in ins[1] and ins[2] == {"i32": 1}
+
+
+def test_shared_movement_view_does_not_materialize(fg, cpu):  # schedule.rs:508-537
+    left = fg.Tensor.new([1.0, 2, 3, 4], [2, 2], cpu)
+    right = fg.Tensor.new([10.0, 20, 30, 40], [2, 2], cpu)
+    moved = left.add(right).reshape([4]).reshape([2, 2])
+    items = plan(fg, [moved.sum([1]).add(moved.max([1]))])
+    # The reshape chain is a view; the Add under it still has two consumers
+    # through the shared view only, so it is not materialised.
+    assert len(items) == 3
+    assert all("buffer" in i for i in items[0]["inputs"][:2])
+    assert items[2]["inputs"][0] == {"buffer": items[0]["output"]}
+    assert items[2]["inputs"][1] == {"buffer": items[1]["output"]}
+
+
+def test_shared_view_stays_inlined_for_assignments(fg, cpu):  # schedule.rs:539-570
+    left = fg.Tensor.new([1.0, 2, 3, 4], [2, 2], cpu)
+    right = fg.Tensor.new([10.0, 20, 30, 40], [2, 2], cpu)
+    dst_a = fg.Tensor.new([0.0] * 4, [2, 2], cpu)
+    dst_b = fg.Tensor.new([0.0] * 4, [2, 2], cpu)
+    moved = left.add(right).permute([1, 0])
+    dst_a.assign(moved)
+    dst_b.assign(moved)
+    items = plan(fg, [dst_a, dst_b])
+    assert len(items) == 2
+    assert all(it["output"] is None for it in items)
+    assert all(all("buffer" in i for i in it["inputs"][:3]) for it in items)
+
+
+def test_matmul_emits_contiguous_copy_then_reduce(fg, cpu):  # tensor.rs:762-778
+    x = fg.Tensor.new(np.ones((4, 8), np.float32), [4, 8], cpu)
+    w = fg.Tensor.new(np.ones((8, 6), np.float32), [8, 6], cpu)
+    items = plan(fg, [x.matmul(w)])
+    assert len(items) == 2
+    assert items[0]["out_shape"] == [6, 8]  # permute(...).contiguous()
+    assert {"buffer": items[0]["output"]} in items[1]["inputs"]
+
+
+def test_relu_input_materialised_without_fusion(fg, cpu):  # tensor.rs:517-531, schedule.rs:321-326
+    a, b, c = (fg.Tensor.new(np.ones(64, np.float32), [64], cpu) for _ in range(3))
+    items = plan(fg, [a.mul(b).add(c).relu()])
+    assert len(items) == 2
+    assert len(items[1]["inputs"]) == 2  # the zeros buffer and the materialised input
+
+
+def test_fusion_makes_c2_one_kernel_without_zero_buffer(fg, cpu):
+    a, b, c = (fg.Tensor.new(np.ones(64, np.float32), [64], cpu) for _ in range(3))
+    items = plan(fg, [a.mul(b).add(c).relu()], fuse=True)
+    assert len(items) == 1
+    assert len(items[0]["inputs"]) == 3  # a, b, c only: the zeros are a literal
+
+
+def test_fusion_makes_c1_one_kernel(fg, cpu):
+    x = fg.Tensor.new(np.ones((16, 16), np.float32), [16, 16], cpu)
+    y = x.mul(fg.Tensor.scalar(0.5, cpu)).add(fg.Tensor.scalar(1.0, cpu)).relu().sum([1])
+    items = plan(fg, [y], fuse=True)
+    assert len(items) == 1 and len(items[0]["inputs"]) == 3
+
+
+def test_fusion_keeps_nodes_with_diverging_consumers(fg, cpu):
+    # The pre-activation feeds relu and an unrelated sum: still materialised.
+    x = fg.Tensor.new(np.ones((8, 8), np.float32), [8, 8], cpu)
+    z = x.add(x)
+    items_ref = plan(fg, [z.relu(), z.sum([1])])
+    items_fused = plan(fg, [z.relu(), z.sum([1])], fuse=True)
+    assert len(items_fused) == len(items_ref)
+
+
+def test_zero_buffer_folds_only_while_it_holds_zeros(fg, cpu):
+    ones = fg.Tensor.new([1.0] * 4, [4], cpu)
+    z = fg.Tensor.zeros([4], cpu)
+    assert len(plan(fg, [z.add(ones)], fuse=True)[0]["inputs"]) == 1  # zeros became a literal
+    z.assign(fg.Tensor.new([1.0, 2.0, 3.0, 4.0], [4], cpu))
+    fg.Tensor.realize_many([z])
+    y = z.add(ones)
+    assert len(plan(fg, [y], fuse=True)[0]["inputs"]) == 2  # written: loaded again
+    assert y.to_vec() == [2.0, 3.0, 4.0, 5.0]
+
+
+def test_assign_in_same_schedule_disables_folding_for_later_kernels(fg, cpu):
+    z = fg.Tensor.zeros([4], cpu)
+    z.assign(fg.Tensor.new([1.0, 2.0, 3.0, 4.0], [4], cpu))
+    y = z.add(fg.Tensor.new([1.0] * 4, [4], cpu))
+    items = plan(fg, [z, y], fuse=True)
+    assert len(items) == 2 and len(items[1]["inputs"]) == 2
