@@ -29,6 +29,9 @@ struct BufferInner {
   // Holds the zeros `allocate` produced and nothing has written it since
   // (allocation contract: device.rs:282, cpu.rs:277-280).
   bool known_zero = false;
+  // Allocated as zeros but storage not created yet (the HIP device
+  // materialises zero-filled allocations on first use).
+  bool zero_init = false;
   size_t nbytes() const { return dtype.size_bytes() * numel; }
   bool is_realized() const { return realized; }
   void ensure_allocated();  // device.rs:191-213
@@ -50,6 +53,14 @@ struct KernelArg {
   static KernelArg boolean(bool x) { KernelArg a; a.kind = Kind::Bool; a.b = x; return a; }
 };
 
+// One kernel launch of a program.
+struct LaunchSpec {
+  std::string func;
+  unsigned grid[3] = {1, 1, 1};
+  unsigned block[3] = {1, 1, 1};
+  unsigned lds_bytes = 0;
+};
+
 // What a renderer hands to `Device::compile`: the source and everything the
 // launch needs that the reference's `compile(source, name, num_args)` lacks.
 struct RenderedKernel {
@@ -60,6 +71,12 @@ struct RenderedKernel {
   unsigned lds_bytes = 0;
   std::string kind;  // lowering class, for debug output and tests
   std::vector<std::pair<int, DType>> params;  // (slot, dtype) in launch order
+  // Multi-kernel programs: when non-empty these launches run in order instead
+  // of the single (name, grid, block) launch. With scratch_bytes > 0 the
+  // program owns a device scratch buffer passed as the last argument of every
+  // launch (partial results between passes; nothing needs zeroing).
+  std::vector<LaunchSpec> launches;
+  size_t scratch_bytes = 0;
 };
 
 struct Program {

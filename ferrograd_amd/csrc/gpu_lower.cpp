@@ -335,6 +335,7 @@ class Emitter {
     return unit && lane_base_aligned_;
   }
   void set_lane_base_aligned(bool b) { lane_base_aligned_ = b; }
+  void set_nontemporal_loads(bool b) { nt_loads_ = b; }
 
   std::string val(const UOp& n, int lane) {
     bool lane_dep = lane_range_ && depends_on(n, lane_range_);
@@ -357,9 +358,11 @@ class Emitter {
       FG_CHECK(ix.op() == Op::Index, "Load must read through Index");
       if (lane_dep && vec4_load(n)) {
         std::string v = fresh("vec");
-        const char* vt = n.dtype().kind == DTypeKind::F32 ? "float4" : "int4";
-        emit_at(si, std::string("const ") + vt + " " + v + " = *(const " + vt + "*)(" + pname(ix.src(0)) + "+" +
-                        idx(ix.src(1), 0) + ");");
+        const char* vt = n.dtype().kind == DTypeKind::F32 ? "fg_f4" : "fg_i4";
+        std::string addr = std::string("(const ") + vt + "*)(" + pname(ix.src(0)) + "+" + idx(ix.src(1), 0) + ")";
+        // Streaming kernels read each element once: non-temporal 16-byte loads.
+        std::string rhs = nt_loads_ ? "__builtin_nontemporal_load(" + addr + ")" : "*" + addr;
+        emit_at(si, std::string("const ") + vt + " " + v + " = " + rhs + ";");
         static const char* comp[4] = {".x", ".y", ".z", ".w"};
         for (int u = 0; u < 4; u++) remember(si, std::make_pair(n.get(), u), v + comp[u]);
         return v + comp[lane];
@@ -430,6 +433,7 @@ class Emitter {
   const UOpInner* lane_range_ = nullptr;
   int lanes_ = 1;
   bool lane_base_aligned_ = true;
+  bool nt_loads_ = false;
   int counter_ = 0;
 };
 
@@ -454,6 +458,8 @@ std::string signature(const KernelInfo& ki, const std::string& name, int block) 
 
 const char* kPrelude = R"(// generated by ferrograd_amd for gfx950
 typedef float floatx16 __attribute__((ext_vector_type(16)));
+typedef float fg_f4 __attribute__((ext_vector_type(4)));
+typedef int fg_i4 __attribute__((ext_vector_type(4)));
 // Cross-lane moves on 32-bit values. DPP row-local patterns for distances
 // inside a row of 16 lanes, ds_swizzle for 16, ds_bpermute for 32.
 #define FG_DPP(v, ctrl) __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), ctrl, 0xF, 0xF, false))
@@ -601,6 +607,7 @@ RenderedKernel render_serial(const KernelInfo& ki, const std::string& name) {
 // ── Elementwise ─────────────────────────────────────────────────────────────
 RenderedKernel render_elementwise(const KernelInfo& ki, const std::string& name) {
   Emitter em;
+  em.set_nontemporal_loads(true);
   UOp fast = pick_fast_output(ki);
   int64_t T = total_outputs(ki);
   int V = 1;
@@ -686,6 +693,7 @@ RenderedKernel render_row_reduce(const KernelInfo& ki, const std::string& name) 
     }
   }
   Emitter em;
+  em.set_nontemporal_loads(true);
   em.line("const int tid = threadIdx.x;");
   em.line("const int rlane = tid % " + std::to_string(T) + ";");
   em.line("const long oid = (long)blockIdx.x * " + std::to_string(OPW) + " + tid / " + std::to_string(T) + ";");
@@ -755,6 +763,116 @@ RenderedKernel render_row_reduce(const KernelInfo& ki, const std::string& name) 
 }
 
 // ── ColumnReduce ────────────────────────────────────────────────────────────
+// Two-pass column reduction. Pass 1 (`<name>_part`): workgroup (block, chunk)
+// reduces rows [chunk*CH, (chunk+1)*CH) of its output block and writes one
+// partial per output to scratch[chunk][out]. Pass 2 (`<name>_fin`): one thread
+// per 4 outputs folds the partials in chunk order and applies the epilogue.
+RenderedKernel render_column_reduce_split(const KernelInfo& ki, const std::string& name, int V, int TX, int TR,
+                                          int64_t per_f, int64_t other, int64_t fext, int64_t nchunks) {
+  const UOp& R = ki.reduces[0];
+  Op rop = R.arg().rop;
+  DType dt = R.dtype();
+  const UOp r = R.src(1);
+  int64_t L = range_extent(r);
+  int64_t CH = (L + nchunks - 1) / nchunks;
+  nchunks = (L + CH - 1) / CH;
+  UOp fast = pick_fast_output(ki);
+  const int64_t NOUT = fext * other;
+  const std::string sig_extra = std::string(", ") + ctype(dt) + "* __restrict__ fg_scratch";
+  auto sig = [&](const std::string& fn) {
+    std::string s = signature(ki, fn, 256);
+    return s.substr(0, s.size() - 1) + sig_extra + ")";
+  };
+
+  // Pass 1: partial sums.
+  Emitter p1;
+  p1.set_nontemporal_loads(true);
+  p1.line("const int tid = threadIdx.x;");
+  p1.line("const int tx = tid % " + std::to_string(TX) + ", tr = tid / " + std::to_string(TX) + ";");
+  p1.line("const long cb = blockIdx.x % " + std::to_string(per_f * other) + ";");
+  p1.line("const int chunk = (int)(blockIdx.x / " + std::to_string(per_f * other) + ");");
+  p1.line("const int fbase = (int)(cb % " + std::to_string(per_f) + ") * " + std::to_string(TX * V) + " + tx * " +
+          std::to_string(V) + ";");
+  p1.line("const long orest = cb / " + std::to_string(per_f) + ";");
+  p1.line("const bool active = fbase < " + std::to_string(fext) + ";");
+  p1.line("const int fcl = active ? fbase : 0;");
+  p1.define_range(fast, "fcl");
+  decode_outputs(p1, ki, "orest", fast);
+  if (V == 4) p1.set_lane_range(fast, 4);
+  std::vector<std::string> accs(V);
+  for (int u = 0; u < V; u++) {
+    accs[u] = "cacc" + std::to_string(u);
+    p1.line(std::string(ctype(dt)) + " " + accs[u] + " = " + init_lit(rop, dt) + ";");
+  }
+  p1.line("const int r0 = chunk * " + std::to_string(CH) + ";");
+  p1.line("const int r1 = r0 + " + std::to_string(CH) + " < " + std::to_string(L) + " ? r0 + " + std::to_string(CH) +
+          " : " + std::to_string(L) + ";");
+  p1.open_scope("if (active) for (int rr = r0 + tr; rr < r1; rr += " + std::to_string(TR) + ") {", "}");
+  p1.define_range(r, "rr");
+  for (int u = 0; u < V; u++) p1.line(accs[u] + " = " + combine(rop, accs[u], p1.val(R.src(0), u)) + ";");
+  p1.close_scope();
+  p1.line(std::string("__shared__ ") + ctype(dt) + " fg_col[" + std::to_string(TR) + "][" + std::to_string(TX * V) + "];");
+  for (int u = 0; u < V; u++)
+    p1.line("fg_col[tr][tx*" + std::to_string(V) + "+" + std::to_string(u) + "] = " + accs[u] + ";");
+  p1.line("__syncthreads();");
+  p1.line("if (tr == 0 && active) {");
+  for (int u = 0; u < V; u++) {
+    std::string slot = "fg_col[q][tx*" + std::to_string(V) + "+" + std::to_string(u) + "]";
+    p1.line("  " + std::string(ctype(dt)) + " s" + std::to_string(u) + " = fg_col[0][tx*" + std::to_string(V) + "+" +
+            std::to_string(u) + "];");
+    p1.line("  for (int q = 1; q < " + std::to_string(TR) + "; q++) s" + std::to_string(u) + " = " +
+            combine(rop, "s" + std::to_string(u), slot) + ";");
+    std::string guard = (V == 1 || fext % 4 != 0) ? "if (fbase + " + std::to_string(u) + " < " + std::to_string(fext) + ") " : "";
+    p1.line("  " + guard + "fg_scratch[(long)chunk * " + std::to_string(NOUT) + "L + orest * " + std::to_string(fext) +
+            "L + fbase + " + std::to_string(u) + "] = s" + std::to_string(u) + ";");
+  }
+  p1.line("}");
+
+  // Pass 2: fold partials in chunk order, epilogue, store.
+  Emitter p2;
+  int64_t threads = NOUT / V;
+  p2.line("const long gid = (long)blockIdx.x * 256 + threadIdx.x;");
+  p2.line("if (gid >= " + std::to_string(threads) + "L) return;");
+  int64_t per = fext / V;
+  p2.line("const int fbase = (int)(gid % " + std::to_string(per) + ") * " + std::to_string(V) + ";");
+  p2.line("const long orest = gid / " + std::to_string(per) + ";");
+  p2.define_range(fast, "fbase");
+  decode_outputs(p2, ki, "orest", fast);
+  if (V == 4) p2.set_lane_range(fast, 4);
+  p2.reduce_cb_ = [&](const UOp& RR, int lane) -> std::string {
+    FG_CHECK(RR == R, "column reduce renders exactly one reduction");
+    std::string acc = "facc" + std::to_string(lane);
+    std::string lin = "orest * " + std::to_string(fext) + "L + fbase + " + std::to_string(lane);
+    p2.line(std::string(ctype(dt)) + " " + acc + " = fg_scratch[" + lin + "];");
+    p2.line("for (int c = 1; c < " + std::to_string(nchunks) + "; c++) " + acc + " = " +
+            combine(rop, acc, "fg_scratch[(long)c * " + std::to_string(NOUT) + "L + " + lin + "]") + ";");
+    p2.remember_here(RR, lane, acc);
+    return acc;
+  };
+  std::vector<std::string> vals;
+  for (int u = 0; u < V; u++) vals.push_back(p2.val(ki.value, u));
+  for (int u = 0; u < V; u++)
+    p2.line(pname(ki.out_param) + "[" + p2.idx(ki.out_index, u) + "] = " + vals[u] + ";");
+
+  RenderedKernel rk;
+  rk.name = name;
+  rk.kind = kernel_class_name(KernelClass::ColumnReduce);
+  rk.source = std::string(kPrelude) + sig(name + "_part") + " {\n" + p1.code() + "}\n" + sig(name + "_fin") + " {\n" +
+              p2.code() + "}\n";
+  LaunchSpec a, b;
+  a.func = name + "_part";
+  a.grid[0] = static_cast<unsigned>(per_f * other * nchunks);
+  a.block[0] = 256;
+  b.func = name + "_fin";
+  b.grid[0] = static_cast<unsigned>((threads + 255) / 256);
+  b.block[0] = 256;
+  rk.launches = {a, b};
+  rk.scratch_bytes = static_cast<size_t>(nchunks * NOUT) * dt.size_bytes();
+  rk.grid[0] = a.grid[0];
+  rk.block[0] = 256;
+  return rk;
+}
+
 RenderedKernel render_column_reduce(const KernelInfo& ki, const std::string& name) {
   const UOp& R = ki.reduces[0];
   Op rop = R.arg().rop;
@@ -770,7 +888,18 @@ RenderedKernel render_column_reduce(const KernelInfo& ki, const std::string& nam
   int TR = 256 / TX;
   int64_t per_f = (fext + static_cast<int64_t>(TX) * V - 1) / (static_cast<int64_t>(TX) * V);  // blocks along fast
   int64_t other = total_outputs(ki) / fext;
+  // Few output blocks cannot fill the chip: split the reduce range into
+  // chunks reduced by separate workgroups into scratch, then combine the
+  // chunks in a fixed order in a second pass (deterministic, no atomics).
+  int64_t blocks = per_f * other;
+  int64_t nchunks = 1;
+  if (blocks < 512) {
+    nchunks = std::min<int64_t>((1024 + blocks - 1) / blocks, L / (4 * TR));
+    nchunks = std::max<int64_t>(nchunks, 1);
+  }
+  if (nchunks > 1) return render_column_reduce_split(ki, name, V, TX, TR, per_f, other, fext, nchunks);
   Emitter em;
+  em.set_nontemporal_loads(true);
   em.line("const int tid = threadIdx.x;");
   em.line("const int tx = tid % " + std::to_string(TX) + ", tr = tid / " + std::to_string(TX) + ";");
   em.line("const int fbase = (int)(blockIdx.x % " + std::to_string(per_f) + ") * " + std::to_string(TX * V) + " + tx * " +

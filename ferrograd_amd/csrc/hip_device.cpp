@@ -17,8 +17,15 @@ void check(int rc, const char* what) {
 }
 
 struct HipProgram : Program {
-  fg_prog* prog = nullptr;
-  ~HipProgram() override { fg_hip_program_free(prog); }
+  fg_prog* prog = nullptr;             // single-launch programs
+  std::vector<fg_prog*> passes;        // multi-launch programs, in launch order
+  fg_ctx* ctx = nullptr;
+  void* scratch = nullptr;
+  ~HipProgram() override {
+    fg_hip_program_free(prog);
+    for (auto* p : passes) fg_hip_program_free(p);
+    if (scratch && ctx) fg_hip_free(ctx, scratch);
+  }
 };
 
 class HipDevice : public Device {
@@ -34,10 +41,13 @@ class HipDevice : public Device {
     return ctx_;
   }
 
-  Buffer allocate(DType dtype, size_t numel) override {  // cpu.rs:277-280 (zero-filled)
+  // cpu.rs:277-280 (zero-filled). Storage is created lazily: a buffer that is
+  // only ever folded to a literal 0 (relu's zeros) never touches HBM. Any read
+  // (kernel input, copy_to_host) or write materialises it first.
+  Buffer allocate(DType dtype, size_t numel) override {
     Buffer b = reserve_buffer(dtype, numel);
-    realize_storage(*b, true);
     b->known_zero = true;
+    b->zero_init = true;
     return b;
   }
 
@@ -47,6 +57,7 @@ class HipDevice : public Device {
     check(fg_hip_alloc(ctx(), b.nbytes(), zero ? 1 : 0, &p), "fg_hip_alloc");
     b.storage = p;
     b.realized = true;
+    b.zero_init = false;
   }
 
   void release(BufferInner& b) override {
@@ -58,17 +69,18 @@ class HipDevice : public Device {
 
   void copy_from_host(const Buffer& b, const void* src, size_t nbytes) override {  // cpu.rs:282-302
     FG_CHECK(b->device == DeviceId::Hip, "HIP backend received non-HIP buffer " + std::to_string(b->id));
-    b->ensure_allocated();
     FG_CHECK(nbytes == b->nbytes(), "copy_from_host: expected " + std::to_string(b->nbytes()) + " bytes, got " +
                                         std::to_string(nbytes));
+    realize_storage(*b, false);  // fully overwritten below
     check(fg_hip_copy_h2d(ctx(), b->storage, src, nbytes), "fg_hip_copy_h2d");
     b->known_zero = false;
   }
 
   std::vector<uint8_t> copy_to_host(const Buffer& b) override {  // cpu.rs:304-316
     FG_CHECK(b->device == DeviceId::Hip, "HIP backend received non-HIP buffer " + std::to_string(b->id));
-    FG_CHECK(b->realized, "copy_to_host called on unrealized or non-HIP buffer");
     std::vector<uint8_t> out(b->nbytes());
+    if (!b->realized && b->zero_init) return out;  // allocated zeros, never materialised
+    FG_CHECK(b->realized, "copy_to_host called on unrealized or non-HIP buffer");
     check(fg_hip_copy_d2h(ctx(), out.data(), b->storage, out.size()), "fg_hip_copy_d2h");
     return out;
   }
@@ -85,8 +97,27 @@ class HipDevice : public Device {
     FG_CHECK(rk.params.size() == num_args || rk.params.empty(),
              "kernel declares " + std::to_string(rk.params.size()) + " parameters but is launched with " +
                  std::to_string(num_args));
-    check(fg_hip_compile(ctx(), rk.source.c_str(), rk.name.c_str(), static_cast<int>(num_args), &p->prog),
-          "compile failed");
+    int extra = rk.scratch_bytes ? 1 : 0;
+    if (rk.launches.empty()) {
+      check(fg_hip_compile(ctx(), rk.source.c_str(), rk.name.c_str(), static_cast<int>(num_args) + extra, &p->prog),
+            "compile failed");
+    } else {
+      fg_prog* first = nullptr;
+      check(fg_hip_compile(ctx(), rk.source.c_str(), rk.launches[0].func.c_str(), static_cast<int>(num_args) + extra,
+                           &first),
+            "compile failed");
+      p->passes.push_back(first);
+      for (size_t i = 1; i < rk.launches.size(); i++) {
+        fg_prog* q = nullptr;
+        check(fg_hip_program_function(first, rk.launches[i].func.c_str(), static_cast<int>(num_args) + extra, &q),
+              "compile failed");
+        p->passes.push_back(q);
+      }
+    }
+    if (rk.scratch_bytes) {
+      p->ctx = ctx();
+      check(fg_hip_alloc(p->ctx, rk.scratch_bytes, 0, &p->scratch), "fg_hip_alloc (scratch)");
+    }
     p->num_args = num_args;
     p->meta = rk;
     return p;
@@ -111,9 +142,24 @@ class HipDevice : public Device {
         case KernelArg::Kind::Bool: a[i].kind = FG_ARG_BOOL; a[i].v.b = args[i].b ? 1 : 0; break;
       }
     }
-    check(fg_hip_launch(ctx(), p.prog, a.data(), static_cast<int>(a.size()), p.meta.grid, p.meta.block,
-                        p.meta.lds_bytes),
-          "execution failed");
+    if (p.scratch) {
+      fg_arg s;
+      std::memset(&s, 0, sizeof(s));
+      s.kind = FG_ARG_PTR;
+      s.v.p = p.scratch;
+      a.push_back(s);
+    }
+    if (p.passes.empty()) {
+      check(fg_hip_launch(ctx(), p.prog, a.data(), static_cast<int>(a.size()), p.meta.grid, p.meta.block,
+                          p.meta.lds_bytes),
+            "execution failed");
+      return;
+    }
+    for (size_t i = 0; i < p.passes.size(); i++) {
+      const LaunchSpec& l = p.meta.launches[i];
+      check(fg_hip_launch(ctx(), p.passes[i], a.data(), static_cast<int>(a.size()), l.grid, l.block, l.lds_bytes),
+            "execution failed");
+    }
   }
 
   void synchronize() override {

@@ -3,6 +3,7 @@
 // caching allocator and host copies. Replaces src/device/cpu.rs:151-394
 // (clang subprocess + dlopen + libffi) for the MI355X.
 #include <dlfcn.h>
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <hip/hiprtc.h>
 #include <sys/stat.h>
@@ -12,6 +13,7 @@
 #include <cstdlib>
 #include <cstring>
 #include <fstream>
+#include <memory>
 #include <mutex>
 #include <sstream>
 #include <string>
@@ -95,8 +97,15 @@ void write_file_atomic(const std::string& path, const std::vector<char>& data) {
 
 }  // namespace
 
-struct fg_prog {
+struct ModuleRef {
   hipModule_t module = nullptr;
+  ~ModuleRef() {
+    if (module) hipModuleUnload(module);
+  }
+};
+
+struct fg_prog {
+  std::shared_ptr<ModuleRef> module;
   hipFunction_t func = nullptr;
   int num_args = 0;
   std::string name;
@@ -308,14 +317,29 @@ int fg_hip_compile(fg_ctx* c, const char* source, const char* func, int num_args
   auto* p = new fg_prog();
   p->num_args = num_args;
   p->name = func;
-  hipError_t e = hipModuleLoadData(&p->module, code.data());
+  p->module = std::make_shared<ModuleRef>();
+  hipError_t e = hipModuleLoadData(&p->module->module, code.data());
   if (e != hipSuccess) {
     delete p;
     return set_err(FG_ERR_HIP, std::string("hipModuleLoadData: ") + hipGetErrorString(e));
   }
-  e = hipModuleGetFunction(&p->func, p->module, func);
+  e = hipModuleGetFunction(&p->func, p->module->module, func);
   if (e != hipSuccess) {
-    hipModuleUnload(p->module);
+    delete p;
+    return set_err(FG_ERR_SYMBOL, std::string("symbol '") + func + "' not found: " + hipGetErrorString(e));
+  }
+  *out = p;
+  return FG_OK;
+}
+
+int fg_hip_program_function(fg_prog* prog, const char* func, int num_args, fg_prog** out) {
+  if (!prog || !func || !out) return set_err(FG_ERR_INVALID, "fg_hip_program_function: null argument");
+  auto* p = new fg_prog();
+  p->module = prog->module;
+  p->num_args = num_args;
+  p->name = func;
+  hipError_t e = hipModuleGetFunction(&p->func, p->module->module, func);
+  if (e != hipSuccess) {
     delete p;
     return set_err(FG_ERR_SYMBOL, std::string("symbol '") + func + "' not found: " + hipGetErrorString(e));
   }
@@ -324,8 +348,6 @@ int fg_hip_compile(fg_ctx* c, const char* source, const char* func, int num_args
 }
 
 int fg_hip_program_free(fg_prog* p) {
-  if (!p) return FG_OK;
-  if (p->module) hipModuleUnload(p->module);
   delete p;
   return FG_OK;
 }
@@ -351,8 +373,10 @@ int fg_hip_launch(fg_ctx* c, fg_prog* p, const fg_arg* args, int nargs, const un
       default: return set_err(FG_ERR_ARGS, "fg_hip_launch: unknown argument kind " + std::to_string(args[i].kind));
     }
   }
-  hipEvent_t ea = nullptr, eb = nullptr;
   if (c->profiling) {
+    // Start/stop events attached to the dispatch itself, so the duration
+    // excludes any host gap before the launch reaches the queue.
+    hipEvent_t ea = nullptr, eb = nullptr;
     for (hipEvent_t* e : {&ea, &eb}) {
       if (!c->event_pool.empty()) {
         *e = c->event_pool.back();
@@ -361,14 +385,13 @@ int fg_hip_launch(fg_ctx* c, fg_prog* p, const fg_arg* args, int nargs, const un
         HIP_TRY(hipEventCreate(e));
       }
     }
-    HIP_TRY(hipEventRecord(ea, c->stream));
+    HIP_TRY(hipExtModuleLaunchKernel(p->func, grid[0] * block[0], grid[1] * block[1], grid[2] * block[2], block[0],
+                                     block[1], block[2], lds, c->stream, params, nullptr, ea, eb, 0));
+    c->records.push_back({p->name, ea, eb});
+    return FG_OK;
   }
   HIP_TRY(hipModuleLaunchKernel(p->func, grid[0], grid[1], grid[2], block[0], block[1], block[2], lds, c->stream,
                                 params, nullptr));
-  if (c->profiling) {
-    HIP_TRY(hipEventRecord(eb, c->stream));
-    c->records.push_back({p->name, ea, eb});
-  }
   return FG_OK;
 }
 

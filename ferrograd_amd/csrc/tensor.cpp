@@ -398,8 +398,11 @@ static void execute_item(const ScheduleItem& item) {
     args.push_back(KernelArg::buf(item.output_buffer));
   }
   for (auto& in : item.inputs) {
-    if (in.kind == KernelArg::Kind::Buffer)
-      FG_CHECK(in.buffer->is_realized(), "scheduled input buffer missing");
+    if (in.kind == KernelArg::Kind::Buffer && !in.buffer->is_realized()) {
+      // Zero-initialised allocations may be materialised lazily by the device.
+      FG_CHECK(in.buffer->zero_init, "scheduled input buffer missing");
+      backend.realize_storage(*in.buffer, true);
+    }
     args.push_back(in);
   }
   auto t0 = std::chrono::steady_clock::now();

@@ -80,6 +80,10 @@ int fg_hip_copy_d2d(fg_ctx* ctx, void* dst, const void* src, size_t nbytes);
 int fg_hip_compile(fg_ctx* ctx, const char* source, const char* func, int num_args, fg_prog** out);
 int fg_hip_program_free(fg_prog* prog);
 int fg_hip_program_num_args(const fg_prog* prog);
+/* Another kernel `func` of the module `prog` was loaded from (multi-kernel
+ * programs, e.g. a partial-sums pass and its finishing pass). The module
+ * stays loaded until every program sharing it is freed. */
+int fg_hip_program_function(fg_prog* prog, const char* func, int num_args, fg_prog** out);
 
 /* Launch on the context's stream. `nargs` must equal the program's num_args. */
 int fg_hip_launch(fg_ctx* ctx, fg_prog* prog, const fg_arg* args, int nargs, const unsigned grid[3],

@@ -24,7 +24,7 @@ def test_c2_is_one_vectorised_elementwise_kernel(fg, cpu):
     items = hip_plan(fg, [a.mul(b).add(c).relu()])
     assert [it["class"] for it in items] == ["elementwise"]
     src = items[0]["source"]
-    assert src.count("*(const float4*)") == 3 and "*(float4*)" in src
+    assert src.count("__builtin_nontemporal_load((const fg_f4*)") == 3 and "*(float4*)" in src
     compile_only(fg, src, items[0]["name"])
 
 

@@ -196,3 +196,49 @@ def test_mlp_train_step(fg, cpu, batch, hidden, steps):
     np.testing.assert_allclose(lh, lc, rtol=1e-4)
     for a, b in zip(ph, pc):
         np.testing.assert_allclose(a, b, rtol=1e-4, atol=1e-6)
+
+
+@pytest.mark.parametrize("shape", [(8192, 512), (1000, 12), (4096, 4096), (3, 257), (256, 128)])
+@pytest.mark.parametrize("op", ["sum", "max"])
+def test_column_reductions(fg, cpu, shape, op):
+    x = seeded(3).standard_normal(shape).astype(np.float32)
+
+    def run(dev):
+        t = fg.Tensor.new(x, list(shape), dev)
+        return (t.sum([0]) if op == "sum" else t.max([0])).numpy()[0]
+
+    want, got = both(run, cpu)
+    if op == "max":
+        assert np.array_equal(got, want)
+    else:
+        assert rel_err_bound(got, want, np.abs(x).sum(0), 1e-4) <= 1.0
+
+
+def test_bias_gradient_sgd_update_in_place(fg, cpu):
+    # b <- b - lr * sum_m g[m, :]: the column reduction with an in-place epilogue (K12).
+    g = seeded(4).standard_normal((8192, 4096)).astype(np.float32)
+    b0 = seeded(5).standard_normal(4096).astype(np.float32)
+
+    def run(dev):
+        b = fg.Tensor.new(b0, [4096], dev)
+        gt = fg.Tensor.new(g, [8192, 4096], dev)
+        b.assign(b.detach().sub(gt.sum([0]).reshape([4096]).mul(fg.Tensor.scalar(0.01, dev))))
+        fg.Tensor.realize_many([b])
+        return b.numpy()
+
+    want, got = both(run, cpu)
+    scale = np.abs(b0) + 0.01 * np.abs(g).sum(0)
+    assert rel_err_bound(got, want, scale, 1e-4) <= 1.0
+
+
+def test_lazy_zero_buffers(fg, hip):
+    z = fg.Tensor.zeros([1000], hip)
+    assert z.to_vec() == [0.0] * 1000
+    z2 = fg.Tensor.zeros([4, 4], hip)
+    assert z2.add(fg.Tensor.ones([4, 4], hip)).to_vec() == [1.0] * 16
+    z3 = fg.Tensor.zeros([3], hip)
+    z3.assign(fg.Tensor.new([1.0, 2.0, 3.0], [3], hip))
+    fg.Tensor.realize_many([z3])
+    assert z3.to_vec() == [1.0, 2.0, 3.0]
+    i0 = fg.Tensor.zeros([5], hip, dtype=fg.I32)
+    assert i0.numpy().tolist() == [0] * 5
