@@ -40,18 +40,24 @@ def log(*a):
 
 
 def timed(fg, ctx, step, steps: int, warmup: int):
-    """Run `step` warmup times untimed, then `steps` times between two device
-    synchronisations with launch profiling on. Returns (ms/step, profile)."""
+    """Run `step` warmup times untimed, then time `steps` steps between two
+    device synchronisations (the step rate), then run `steps` more with
+    dispatch-attached events on every launch (the per-kernel durations; the
+    events add host work, so they are kept out of the step-rate region).
+    Returns (ms/step, profile)."""
     for _ in range(warmup):
         step()
     fg.synchronize()
-    ctx.profile_read()  # drop anything recorded before
-    ctx.profile(True)
     t0 = time.perf_counter()
     for _ in range(steps):
         step()
     fg.synchronize()
     t1 = time.perf_counter()
+    ctx.profile_read()  # drop anything recorded before
+    ctx.profile(True)
+    for _ in range(steps):
+        step()
+    fg.synchronize()
     ctx.profile(False)
     prof = ctx.profile_read()
     return (t1 - t0) * 1000.0 / steps, prof
@@ -84,6 +90,24 @@ def cpu_baseline(config: str):
         return None
 
 
+def pmc_traffic(kernel: str):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 --pmc
+    FETCH_SIZE / WRITE_SIZE measurements (profiles/pmc_traffic.json), each
+    scaled by the factor a plain 1 GiB copy kernel calibrates. Kernel symbols
+    are content hashes of the generated source, so a kernel whose source
+    changed since it was measured gets None (unmeasured), never a stale
+    figure."""
+    try:
+        with open(os.path.join(ROOT, "profiles", "pmc_traffic.json")) as f:
+            t = json.load(f)
+    except (OSError, ValueError):
+        return None
+    k = t.get("kernels", {}).get(kernel)
+    if not k:
+        return None
+    return (k["fetch_kib"] * t["fetch_factor"] + k["write_kib"] * t["write_factor"]) * 1024.0
+
+
 def bench_c2(fg, ctx, steps, warmup):
     from ferrograd_amd import Tensor
 
@@ -101,8 +125,9 @@ def bench_c2(fg, ctx, steps, warmup):
     alg = 4 * n * 4
     return {"ms_per_step": ms, "gbs": alg / (ms / 1e3) / 1e9, "kernels": kern, "dominant": name,
             "roofline": {"bound": "hbm", "achieved": alg / (dk["avg_ms"] / 1e3) / 1e9, "peak": HBM_PEAK_GBS,
-                         "unit": "GB/s", "frac": alg / (dk["avg_ms"] / 1e3) / 1e9 / HBM_PEAK_GBS, "traffic": None,
-                         "kernel": name, "algorithmic_bytes": alg, "kernel_avg_ms": dk["avg_ms"]}}
+                         "unit": "GB/s", "frac": alg / (dk["avg_ms"] / 1e3) / 1e9 / HBM_PEAK_GBS,
+                         "traffic": pmc_traffic(name), "kernel": name, "algorithmic_bytes": alg,
+                         "kernel_avg_ms": dk["avg_ms"]}}
 
 
 def bench_c1(fg, ctx, steps, warmup):
@@ -184,6 +209,29 @@ def bench_mlp(fg, ctx, steps, warmup, batch, dims):
             "loss_first_last": [losses[0], losses[-1]] if losses else None, "kernels": kern}
 
 
+COPY_SRC = r"""
+extern "C" __global__ void __launch_bounds__(256) fg_copy_probe(float4* __restrict__ dst, const float4* __restrict__ src, int n4) {
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  if (i < n4) dst[i] = src[i];
+}"""
+
+
+def copy_probe(nbytes: int = 1 << 30, reps: int = 5) -> None:
+    """Launch a plain copy of `nbytes` (read + write) `reps` times: the
+    reference kernel whose FETCH_SIZE / WRITE_SIZE counters calibrate the
+    byte counts of the generated kernels under rocprofv3 --pmc."""
+    from ferrograd_amd.hip import Arg, Context
+
+    ctx = Context(0)
+    src, dst = ctx.alloc(nbytes), ctx.alloc(nbytes)
+    prog = ctx.compile(COPY_SRC, "fg_copy_probe", 3)
+    n4 = nbytes // 16
+    for _ in range(reps):
+        ctx.launch(prog, [Arg.ptr(dst), Arg.ptr(src), Arg.i32(n4)], grid=((n4 + 255) // 256, 1, 1), block=(256, 1, 1))
+    ctx.sync()
+    print(json.dumps({"copy_probe_bytes_read": nbytes, "copy_probe_bytes_written": nbytes, "launches": reps}))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -192,7 +240,11 @@ def main():
     ap.add_argument("--only", default=None, help="run one config: c1,c2,c3,c4,c5")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--kernels", action="store_true", help="include per-kernel tables")
+    ap.add_argument("--copy-probe", action="store_true", help="only run the 1 GiB copy calibration kernel")
     args = ap.parse_args()
+    if args.copy_probe:
+        copy_probe()
+        return
     if args.gpus != 1:
         print(f"bench.py measures one MI355X; --gpus {args.gpus} is not supported in this build "
               "(multi-GPU sharding is design-only, see DESIGN.md)", file=sys.stderr)

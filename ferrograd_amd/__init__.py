@@ -88,6 +88,7 @@ def _declare(l: ctypes.CDLL) -> None:
         "fg_synchronize": (c_int, [c_int]),
         "fg_stats": (c_int, [ctypes.POINTER(ctypes.c_uint64)] * 3),
         "fg_clear_caches": (c_int, []),
+        "fg_host_times": (c_int, [ctypes.POINTER(ctypes.c_uint64)]),
         "fg_debug_plan": (c_int, [PP, c_int, c_int, c_int, ctypes.c_char_p, c_size, ctypes.POINTER(c_size)]),
     }
     for name, (res, args) in sigs.items():
@@ -415,7 +416,11 @@ def synchronize(device="hip") -> None:
 def stats() -> dict:
     k, p, h = ctypes.c_uint64(), ctypes.c_uint64(), ctypes.c_uint64()
     lib().fg_stats(ctypes.byref(k), ctypes.byref(p), ctypes.byref(h))
-    return {"kernels_launched": k.value, "programs_compiled": p.value, "lowering_cache_hits": h.value}
+    t = (ctypes.c_uint64 * 5)()
+    lib().fg_host_times(t)
+    names = ("schedule", "lower", "launch", "apply_map", "backward")
+    return {"kernels_launched": k.value, "programs_compiled": p.value, "lowering_cache_hits": h.value,
+            "host_ms": {n: t[i] / 1e6 for i, n in enumerate(names)}}
 
 
 def clear_caches() -> None:

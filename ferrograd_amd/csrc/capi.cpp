@@ -329,6 +329,16 @@ int fg_stats(uint64_t* k, uint64_t* p, uint64_t* h) {
   return 0;
 }
 
+int fg_host_times(uint64_t out[5]) {
+  auto& s = fg::realize_stats();
+  out[0] = s.ns_schedule;
+  out[1] = s.ns_lower;
+  out[2] = s.ns_launch;
+  out[3] = s.ns_apply_map;
+  out[4] = s.ns_backward;
+  return 0;
+}
+
 int fg_clear_caches(void) {
   return guard([&] { fg::clear_kernel_caches(); });
 }

@@ -1296,6 +1296,7 @@ RenderedKernel render_hip_stable(const UOp& kernel) {
   };
   replace_all(rk.source);
   replace_all(rk.name);
+  for (auto& l : rk.launches) replace_all(l.func);
   return rk;
 }
 

@@ -272,6 +272,8 @@ UOp UOp::make(Op op, DType dtype, std::vector<UOp> srcs, Arg arg, bool has_tag, 
   inner->has_tag = has_tag;
   inner->tag = tag;
   inner->hash = h;
+  if (op == Op::Device) inner->device = static_cast<DeviceId>(inner->arg.a);
+  else if (!inner->srcs.empty()) inner->device = inner->srcs[0].get()->device;
   std::shared_ptr<const UOpInner> cp = inner;
   m.emplace(h, InternEntry{inner.get(), cp});
   return UOp(cp);
@@ -349,12 +351,8 @@ bool UOp::has_tag() const { return p_->has_tag; }
 uint64_t UOp::tag() const { return p_->tag; }
 
 DeviceId UOp::device() const {
-  const UOpInner* n = p_.get();
-  while (n->op != Op::Device) {
-    FG_CHECK(!n->srcs.empty(), "non-device UOps must derive device from sources");
-    n = n->srcs[0].get();
-  }
-  return static_cast<DeviceId>(n->arg.a);
+  FG_CHECK(p_->op == Op::Device || !p_->srcs.empty(), "non-device UOps must derive device from sources");
+  return p_->device;
 }
 
 bool UOp::is_const_float(double v) const {
@@ -362,8 +360,20 @@ bool UOp::is_const_float(double v) const {
 }
 bool UOp::is_const_int(int64_t v) const { return op() == Op::Const && arg() == Arg::integer(v); }
 
-// uop.rs:806-866
+// uop.rs:806-866 (memoised on the node)
 bool UOp::shape_opt(Shape* out) const {
+  if (p_->shape_state == -1) {
+    Shape s;
+    bool ok = compute_shape(&s);
+    p_->shape_state = ok ? 1 : 0;
+    if (ok) p_->shape_cache = std::move(s);
+  }
+  if (p_->shape_state == 0) return false;
+  *out = p_->shape_cache;
+  return true;
+}
+
+bool UOp::compute_shape(Shape* out) const {
   const Arg& a = arg();
   switch (op()) {
     case Op::Buffer:

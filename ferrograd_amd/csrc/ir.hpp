@@ -203,6 +203,7 @@ class UOp {
   const UOpInner* get() const { return p_.get(); }
 
  private:
+  bool compute_shape(Shape* out) const;
   std::shared_ptr<const UOpInner> p_;
 };
 
@@ -221,6 +222,10 @@ struct UOpInner {
   bool has_tag = false;
   uint64_t tag = 0;
   size_t hash = 0;
+  DeviceId device = DeviceId::Hip;  // derived from the first source at creation
+  // Lazily computed tensor shape (shape() is a pure function of the node).
+  mutable int8_t shape_state = -1;  // -1 unknown, 0 none, 1 cached
+  mutable Shape shape_cache;
   ~UOpInner();
 };
 

@@ -87,8 +87,28 @@ std::pair<UOp, std::vector<KernelArg>> parameterize_inputs(const UOp& root, size
         return UOp();
     }
   };
-  UOp out = graph_rewrite(root, fn);
-  return {out, inputs};
+  // One bottom-up pass in toposort order visits leaves in the same order as
+  // the first iteration of the reference's fixed-point rewrite (so slots
+  // match), and the rule never fires on its own output, so no second pass.
+  UOpMap<UOp> sub;
+  auto order = root.toposort();
+  sub.reserve(order.size() * 2);
+  for (auto& node : order) {
+    std::vector<UOp> ns;
+    ns.reserve(node.srcs().size());
+    bool changed = false;
+    for (auto& s : node.srcs()) {
+      const UOp& x = sub.at(s);
+      ns.push_back(x);
+      changed = changed || x != s;
+    }
+    UOp rebuilt = node;
+    if (changed)
+      rebuilt = node.op() == Op::Sink ? UOp::sink(ns) : UOp::make_new(node.op(), node.dtype(), ns, node.arg());
+    UOp r = fn(rebuilt);
+    sub[node] = r ? r : rebuilt;
+  }
+  return {sub.at(root), inputs};
 }
 
 // schedule.rs:131-151
@@ -200,11 +220,16 @@ bool assignment_effect(const UOp& root, UOp* store, UOp* value) {
   return true;
 }
 
-// schedule.rs:371-405
+// schedule.rs:371-405. Same result as the reference's full-graph walk, but
+// the walk stops at nodes already replaced by a buffer: nothing below them can
+// appear in this kernel.
 UOp substitute_materialized(const UOp& root, const UOpMap<UOp>& replacements) {
-  auto order = root.toposort();
   UOpMap<UOp> sub;
-  for (auto& node : order) {
+  std::vector<std::pair<UOp, bool>> stack{{root, false}};
+  while (!stack.empty()) {
+    auto [node, expanded] = stack.back();
+    stack.pop_back();
+    if (sub.count(node)) continue;
     if (node != root) {
       auto r = replacements.find(node);
       if (r != replacements.end()) {
@@ -212,19 +237,25 @@ UOp substitute_materialized(const UOp& root, const UOpMap<UOp>& replacements) {
         continue;
       }
     }
+    if (!expanded) {
+      stack.emplace_back(node, true);
+      for (auto& s : node.srcs())
+        if (!sub.count(s)) stack.emplace_back(s, false);
+      continue;
+    }
     std::vector<UOp> ns;
+    ns.reserve(node.srcs().size());
     bool changed = false;
     for (auto& s : node.srcs()) {
-      auto it = sub.find(s);
-      ns.push_back(it == sub.end() ? s : it->second);
-      changed = changed || ns.back() != s;
+      const UOp& x = sub.at(s);
+      ns.push_back(x);
+      changed = changed || x != s;
     }
     sub[node] = changed ? (node.op() == Op::Sink ? UOp::sink(ns)
                                                  : UOp::make_new(node.op(), node.dtype(), ns, node.arg()))
                         : node;
   }
-  auto it = sub.find(root);
-  return it == sub.end() ? root : it->second;
+  return sub.at(root);
 }
 
 // Marks the store destination's buffer as written (it no longer holds zeros).

@@ -21,6 +21,11 @@ std::vector<std::weak_ptr<TensorInner>>& live_list() {
 
 size_t g_kernel_count = 0;  // tensor.rs:71
 
+uint64_t now_ns() {
+  return static_cast<uint64_t>(
+      std::chrono::duration_cast<std::chrono::nanoseconds>(std::chrono::steady_clock::now().time_since_epoch()).count());
+}
+
 // Lowering cache: scheduled kernel sink -> compiled program, per device. The
 // sink is interned, and rangeify/optimize/render are pure functions of it, so a
 // hit skips the host passes as well as the compile (the reference caches by
@@ -81,12 +86,20 @@ void Tensor::set_uop(const UOp& u) const { p_->uop = u; }
 static void apply_map_to_tensors(const UOpMap<UOp>& replacements) {
   if (replacements.empty()) return;
   std::vector<std::pair<Tensor, UOp>> affected[2];
+  // Whether a graph reaches a replaced node, memoised across all live tensors
+  // (the reference toposorts every live tensor's whole graph separately).
+  std::unordered_map<const UOpInner*, bool> reaches;
+  std::function<bool(const UOp&)> uses = [&](const UOp& n) -> bool {
+    auto it = reaches.find(n.get());
+    if (it != reaches.end()) return it->second;
+    bool r = replacements.count(n) > 0;
+    for (size_t i = 0; !r && i < n.srcs().size(); i++) r = uses(n.src(i));
+    reaches.emplace(n.get(), r);
+    return r;
+  };
   for (auto& t : live_tensors()) {
     UOp cur = t.uop();
-    bool uses = false;
-    for (auto& n : cur.toposort())
-      if (replacements.count(n)) { uses = true; break; }
-    if (!uses) continue;
+    if (!uses(cur)) continue;
     affected[static_cast<int>(cur.device())].emplace_back(t, cur);
   }
   for (auto& group : affected) {
@@ -346,6 +359,7 @@ static void assert_kernel_ready(const UOp& root) {
 
 // tensor.rs:831-898
 static void execute_item(const ScheduleItem& item) {
+  const uint64_t start_ns = now_ns();
   Device& backend = get_device(item.sink.device());
   int debug = debug_level();
   size_t num_args = item.output_buffer ? item.inputs.size() + 1 : item.inputs.size();
@@ -406,7 +420,10 @@ static void execute_item(const ScheduleItem& item) {
     args.push_back(in);
   }
   auto t0 = std::chrono::steady_clock::now();
+  uint64_t l0 = now_ns();
+  realize_stats().ns_lower += l0 - start_ns;
   backend.execute(*program, args);
+  realize_stats().ns_launch += now_ns() - l0;
   realize_stats().kernels_launched++;
   if (debug >= 2) {
     backend.synchronize();
@@ -427,9 +444,14 @@ void Tensor::realize_many(const std::vector<Tensor>& tensors) {  // tensor.rs:78
   if (debug_level() >= 3) std::fprintf(stderr, "━━━ schedule [before] ━━━\n%s", UOp::sink(roots).dump().c_str());
   ScheduleOptions opt;
   opt.fuse = get_device(roots[0].device()).fuse_elementwise();
+  uint64_t t0 = now_ns();
   SchedulePlan plan = schedule_many(roots, opt);
+  uint64_t t1 = now_ns();
+  realize_stats().ns_schedule += t1 - t0;
   for (auto& item : plan.items) execute_item(item);
+  uint64_t t2 = now_ns();
   apply_map_to_tensors(plan.replacements);
+  realize_stats().ns_apply_map += now_ns() - t2;
 }
 
 Tensor Tensor::realize() const {
@@ -479,6 +501,10 @@ std::vector<Tensor> Tensor::gradient(const std::vector<Tensor>& targets) const {
 }
 
 void Tensor::backward() const {  // tensor.rs:971-998
+  struct Timer {
+    uint64_t t = now_ns();
+    ~Timer() { realize_stats().ns_backward += now_ns() - t; }
+  } timer;
   FG_CHECK(numel() == 1, "backward requires a scalar loss");
   UOpSet all;
   for (auto& n : uop().toposort()) all.insert(n);

@@ -130,6 +130,8 @@ struct RealizeStats {
   size_t kernels_launched = 0;
   size_t programs_compiled = 0;
   size_t lowering_cache_hits = 0;
+  // Host time (ns) spent in each stage of realize_many / backward.
+  uint64_t ns_schedule = 0, ns_lower = 0, ns_launch = 0, ns_apply_map = 0, ns_backward = 0;
 };
 RealizeStats& realize_stats();
 int debug_level();

@@ -92,6 +92,9 @@ int fg_sgd_free(fg_sgd* s);
 int fg_synchronize(int device);
 int fg_device_context(int device, void** ctx);
 int fg_stats(uint64_t* kernels_launched, uint64_t* programs_compiled, uint64_t* lowering_hits);
+/* Cumulative host nanoseconds in: schedule, lowering-cache/compile, launch,
+ * live-tensor rewrite after realisation, backward graph construction. */
+int fg_host_times(uint64_t out[5]);
 int fg_clear_caches(void);
 
 /* Inspection for tests and tooling: schedule the roots (without running
