@@ -1,5 +1,5 @@
 #!/usr/bin/env python3
-"""Benchmark of ferrograd's realize path on one MI355X.
+"""Benchmark of ferrograd's realize path on one MI355X (configs C1-C5).
 
 Primary line (the `value`): C2, the pure elementwise bandwidth config
 `(a*b + c).relu()` over 2^26 f32 elements, as HBM GB/s of algorithmic traffic
@@ -247,7 +247,7 @@ def main():
         return
     if args.gpus != 1:
         print(f"bench.py measures one MI355X; --gpus {args.gpus} is not supported in this build "
-              "(multi-GPU sharding is design-only, see DESIGN.md)", file=sys.stderr)
+              "(every config here runs on one GPU; sharding across GPUs is not built)", file=sys.stderr)
         sys.exit(2)
 
     import ferrograd_amd as fg

@@ -3,7 +3,7 @@
  * These entry points replace the reference's CPU backend primitives behind its
  * `Device` trait (src/device.rs:275-332) and its clang JIT
  * (src/device/cpu.rs:151-394). A Rust `HipDevice` implementing that trait binds
- * them one-to-one (binding stub in INTEGRATION.md):
+ * them one-to-one:
  *
  *   Device::allocate        (device.rs:283, cpu.rs:277-280)  -> fg_hip_alloc(zero=1)
  *   Buffer::ensure_allocated(device.rs:191-213)              -> fg_hip_alloc

@@ -142,31 +142,69 @@ def test_log_softmax_cross_entropy_float64(fg, cpu):
     assert abs(got - want) <= 1e-5 * max(1.0, abs(want))
 
 
-def test_kaiming_init_restatement(fg, cpu):
-    # nn.rs:16-47: LCG seed 42, u = (s>>33)/2^31, Box-Muller in f32, std sqrt(2/fan_in).
+_MASK64 = (1 << 64) - 1
+
+
+def _lcg_draw(n: int, seed: int = 42) -> float:
+    """The n-th (1-based) uniform of the init stream (nn.rs:17-27), computed
+    by jump-ahead instead of iteration: the step s -> a*s + 1 is an affine map
+    on Z/2^64, and its n-th power is found by repeated squaring."""
+    a, c = 6364136223846793005, 1
+    pa, pc = 1, 0          # accumulated map s -> pa*s + pc
+    while n:
+        if n & 1:
+            pa, pc = (a * pa) & _MASK64, (a * pc + c) & _MASK64
+        a, c = (a * a) & _MASK64, (a * c + c) & _MASK64
+        n >>= 1
+    s = (pa * seed + pc) & _MASK64
+    return float(np.float32(s >> 33)) / 2.0 ** 31
+
+
+def _check_box_muller_pairs(vals, first_draw, std):
+    """Invert Box-Muller on consecutive output pairs: x0^2 + x1^2 must equal
+    -2 std^2 ln(u1) and atan2(x1, x0) must equal 2 pi u2, with (u1, u2) the
+    draws `first_draw`, `first_draw + 1`, ... of the LCG stream."""
+    vals = np.asarray(vals, np.float64)
+    tiny = float(np.finfo(np.float32).tiny)
+    for k in range(0, len(vals), 2):
+        u1 = max(_lcg_draw(first_draw + k), tiny)
+        u2 = _lcg_draw(first_draw + k + 1)
+        r2 = -2.0 * std * std * math.log(u1)
+        if k + 1 < len(vals):
+            x0, x1 = vals[k], vals[k + 1]
+            assert abs(x0 * x0 + x1 * x1 - r2) <= 2e-5 * r2, (k, x0, x1, r2)
+            theta = math.atan2(x1, x0) % (2 * math.pi)
+            d = abs(theta - 2 * math.pi * u2)
+            assert min(d, 2 * math.pi - d) <= 2e-5 * 2 * math.pi + 1e-6 / math.sqrt(r2), (k, theta, u2)
+        else:  # odd count: the last value is the cosine half of a pair
+            assert abs(vals[k] - math.sqrt(r2) * math.cos(2 * math.pi * u2)) <= 2e-5 * math.sqrt(r2) + 1e-7
+
+
+def test_kaiming_init_inverts_to_the_lcg_stream(fg, cpu):
+    # nn.rs:16-47: draws u = (s>>33)/2^31 from s <- s*6364136223846793005 + 1
+    # (seed 42, one stream shared by every layer in construction order), pairs
+    # (u1, u2) -> sqrt(-2 ln u1) std (cos, sin)(2 pi u2), std = sqrt(2/fan_in).
     fg.reset_init_seed(42)
-    layer = fg.Linear(3, 2, cpu)
-    got = layer.weight.numpy().reshape(-1)
-    s = 42
-    mask = (1 << 64) - 1
+    l1 = fg.Linear(3, 2, cpu)   # 6 values: draws 1..6
+    l2 = fg.Linear(5, 3, cpu)   # 15 values: 8 pairs, draws 7..22, last sine dropped
+    l3 = fg.Linear(2, 2, cpu)   # draws 23..26
+    _check_box_muller_pairs(l1.weight.numpy().reshape(-1), 1, math.sqrt(2 / 3))
+    _check_box_muller_pairs(l2.weight.numpy().reshape(-1), 7, math.sqrt(2 / 5))
+    _check_box_muller_pairs(l3.weight.numpy().reshape(-1), 23, math.sqrt(2 / 2))
+    assert l1.bias.to_vec() == [0.0, 0.0] and l2.bias.to_vec() == [0.0] * 3
 
-    def unit():
-        nonlocal s
-        s = (s * 6364136223846793005 + 1) & mask
-        return np.float32(s >> 33) / np.float32(1 << 31)
 
-    std = np.float32(math.sqrt(np.float32(2.0) / np.float32(3)))
-    want = []
-    while len(want) < 6:
-        u1 = max(unit(), np.float32(1.17549435e-38))
-        u2 = unit()
-        radius = np.float32(math.sqrt(np.float32(-2.0) * np.float32(math.log(u1)))) * std
-        theta = np.float32(2.0 * np.float32(math.pi)) * u2
-        want.append(radius * np.float32(math.cos(theta)))
-        if len(want) < 6:
-            want.append(radius * np.float32(math.sin(theta)))
-    np.testing.assert_allclose(got, np.array(want, np.float32), rtol=2e-6, atol=1e-7)
-    assert layer.bias.to_vec() == [0.0, 0.0]
+def test_kaiming_init_distribution(fg, cpu):
+    # Over a C4-sized layer the values are N(0, 2/fan_in): checks the scale
+    # uses fan_in (not fan_out) and the transform is Gaussian.
+    from scipy import stats
+
+    fg.reset_init_seed(42)
+    w = fg.Linear(784, 128, cpu).weight.numpy().astype(np.float64).reshape(-1)
+    std = math.sqrt(2 / 784)
+    assert abs(w.mean()) < 5 * std / math.sqrt(w.size)
+    assert abs(w.std() / std - 1) < 0.01
+    assert stats.kstest(w / std, "norm").pvalue > 1e-3
 
 
 def test_renderer_text_matches_reference_shape(cpu, fg):  # clang.rs:449-460, 574-665
