@@ -72,6 +72,7 @@ def _declare(l: ctypes.CDLL) -> None:
         "fg_tensor_info": (c_int, [P] + [ctypes.POINTER(c_int)] * 4),
         "fg_tensor_set_requires_grad": (c_int, [P, c_int]),
         "fg_tensor_same": (c_int, [P, P, ctypes.POINTER(c_int)]),
+        "fg_tensor_data_ptr": (c_int, [P, PP, ctypes.POINTER(c_size)]),
         "fg_tensor_grad": (c_int, [P, PP]),
         "fg_tensor_backward": (c_int, [P]),
         "fg_tensor_gradient": (c_int, [P, PP, c_int, PP]),
@@ -89,6 +90,8 @@ def _declare(l: ctypes.CDLL) -> None:
         "fg_stats": (c_int, [ctypes.POINTER(ctypes.c_uint64)] * 3),
         "fg_clear_caches": (c_int, []),
         "fg_host_times": (c_int, [ctypes.POINTER(ctypes.c_uint64)]),
+        "fg_plan_cache_enable": (c_int, [c_int]),
+        "fg_plan_cache_stats": (c_int, [ctypes.POINTER(ctypes.c_uint64)] * 3),
         "fg_debug_plan": (c_int, [PP, c_int, c_int, c_int, ctypes.c_char_p, c_size, ctypes.POINTER(c_size)]),
     }
     for name, (res, args) in sigs.items():
@@ -233,6 +236,12 @@ class Tensor:
     def alias(self) -> "Tensor":
         """A second handle to the same tensor identity (a Rust `clone`)."""
         return Tensor._out(lib().fg_tensor_unary, self._h, 10)
+
+    def data_ptr(self) -> tuple:
+        """(device pointer, byte size) of a realised tensor's storage."""
+        p, n = ctypes.c_void_p(), ctypes.c_size_t()
+        _check(lib().fg_tensor_data_ptr(self._h, ctypes.byref(p), ctypes.byref(n)))
+        return p.value, n.value
 
     def same(self, other: "Tensor") -> bool:
         s = ctypes.c_int()
@@ -425,6 +434,17 @@ def stats() -> dict:
 
 def clear_caches() -> None:
     _check(lib().fg_clear_caches())
+
+
+def plan_cache(enabled: bool) -> None:
+    """Turn realisation-plan replay on or off (off also drops recorded plans)."""
+    _check(lib().fg_plan_cache_enable(int(enabled)))
+
+
+def plan_stats() -> dict:
+    h, m, e = ctypes.c_uint64(), ctypes.c_uint64(), ctypes.c_uint64()
+    _check(lib().fg_plan_cache_stats(ctypes.byref(h), ctypes.byref(m), ctypes.byref(e)))
+    return {"hits": h.value, "misses": m.value, "entries": e.value}
 
 
 def debug_plan(roots: Sequence[Tensor], fuse: bool = False, render_hip: bool = False) -> dict:

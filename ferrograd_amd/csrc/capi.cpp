@@ -228,6 +228,16 @@ int fg_tensor_info(fg_tensor* t, int* dtype, int* device, int* realized, int* rg
   });
 }
 
+int fg_tensor_data_ptr(fg_tensor* t, void** ptr, size_t* nbytes) {
+  return guard([&] {
+    FG_CHECK(t->t.is_realized(), "fg_tensor_data_ptr: tensor is not realized");
+    fg::Buffer b = t->t.realized_buffer();
+    b->ensure_allocated();
+    *ptr = b->storage;
+    if (nbytes) *nbytes = b->nbytes();
+  });
+}
+
 int fg_tensor_set_requires_grad(fg_tensor* t, int rg) {
   return guard([&] { t->t.with_requires_grad(rg != 0); });
 }
@@ -341,6 +351,14 @@ int fg_host_times(uint64_t out[5]) {
 
 int fg_clear_caches(void) {
   return guard([&] { fg::clear_kernel_caches(); });
+}
+
+int fg_plan_cache_enable(int on) {
+  return guard([&] { fg::set_plan_cache_enabled(on != 0); });
+}
+
+int fg_plan_cache_stats(uint64_t* hits, uint64_t* misses, uint64_t* entries) {
+  return guard([&] { fg::plan_cache_stats(hits, misses, entries); });
 }
 
 int fg_debug_plan(fg_tensor** roots, int n, int fuse, int render, char* buf, size_t len, size_t* needed) {

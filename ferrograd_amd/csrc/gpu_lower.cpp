@@ -161,6 +161,13 @@ UOp gpu_optimize(const UOp& rangeified) {
 // ── rendering helpers ───────────────────────────────────────────────────────
 namespace {
 
+// Elementwise outputs at least this large are written with non-temporal
+// stores: half of MI355X's 256 MB Infinity Cache, beyond which a consumer
+// kernel would find little of the output still cached anyway. Measured on a
+// 2^26-element (a*b+c).relu() writing a fresh buffer each launch: 6.28 TB/s
+// with non-temporal stores against 6.02 TB/s with plain ones.
+constexpr int64_t kStreamingStoreBytes = int64_t(128) << 20;
+
 const char* ctype(DType d) {
   switch (d.kind) {
     case DTypeKind::F32: return "float";
@@ -642,10 +649,19 @@ RenderedKernel render_elementwise(const KernelInfo& ki, const std::string& name)
     for (auto& t : a.terms)
       if (t.first != fast && t.second % 4 != 0) vstore = false;
     if (vstore) {
-      const char* vt = dt.kind == DTypeKind::F32 ? "float4" : "int4";
-      const char* mk = dt.kind == DTypeKind::F32 ? "make_float4" : "make_int4";
-      em.line(std::string("*(") + vt + "*)(" + out + "+" + em.idx(ki.out_index, 0) + ") = " + mk + "(" + vals[0] +
-              ", " + vals[1] + ", " + vals[2] + ", " + vals[3] + ");");
+      const std::string addr = out + "+" + em.idx(ki.out_index, 0);
+      const std::string four = vals[0] + ", " + vals[1] + ", " + vals[2] + ", " + vals[3];
+      if (static_cast<int64_t>(T) * static_cast<int64_t>(dt.size_bytes()) >= kStreamingStoreBytes) {
+        // Too large to stay in the Infinity Cache for a consumer: write it
+        // past the caches instead of evicting the inputs' lines.
+        const char* vt = dt.kind == DTypeKind::F32 ? "fg_f4" : "fg_i4";
+        em.line(std::string("const ") + vt + " vout = {" + four + "};");
+        em.line(std::string("__builtin_nontemporal_store(vout, (") + vt + "*)(" + addr + "));");
+      } else {
+        const char* vt = dt.kind == DTypeKind::F32 ? "float4" : "int4";
+        const char* mk = dt.kind == DTypeKind::F32 ? "make_float4" : "make_int4";
+        em.line(std::string("*(") + vt + "*)(" + addr + ") = " + mk + "(" + four + ");");
+      }
     }
   }
   if (!vstore)

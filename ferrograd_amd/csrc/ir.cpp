@@ -574,6 +574,47 @@ UOp substitute_with_map(const UOp& root, const UOpMap<UOp>& replacements) {
   return it == sub.end() ? root : it->second;
 }
 
+std::vector<UOp> substitute_many(const std::vector<UOp>& roots, const UOpMap<UOp>& replacements) {
+  // Memo: node -> index into `done` (its substituted value). The walk stops at
+  // replaced nodes, so the graph beneath them is never visited.
+  PtrIndexMap memo(1024);
+  std::vector<UOp> done;
+  done.reserve(1024);
+  std::vector<std::pair<const UOp*, bool>> stack;
+  std::vector<UOp> out;
+  out.reserve(roots.size());
+  for (const UOp& root : roots) {
+    stack.emplace_back(&root, false);
+    while (!stack.empty()) {
+      auto [np, expanded] = stack.back();
+      stack.pop_back();
+      const UOp& node = *np;
+      if (memo.get(node.get()) != PtrIndexMap::kAbsent) continue;
+      auto r = replacements.find(node);
+      if (r != replacements.end()) {
+        memo.set(node.get(), static_cast<uint32_t>(done.size()));
+        done.push_back(r->second);
+        continue;
+      }
+      const auto& srcs = node.srcs();
+      if (!expanded) {
+        stack.emplace_back(np, true);
+        for (size_t i = srcs.size(); i-- > 0;)
+          if (memo.get(srcs[i].get()) == PtrIndexMap::kAbsent) stack.emplace_back(&srcs[i], false);
+        continue;
+      }
+      std::vector<UOp> ns;
+      ns.reserve(srcs.size());
+      for (auto& s : srcs) ns.push_back(done[memo.get(s.get())]);
+      UOp v = rebuild(node, std::move(ns));
+      memo.set(node.get(), static_cast<uint32_t>(done.size()));
+      done.push_back(std::move(v));
+    }
+    out.push_back(done[memo.get(root.get())]);
+  }
+  return out;
+}
+
 UOp flatten_end_bodies(const UOp& node) {
   if (node.op() != Op::End || node.srcs().size() < 2) return UOp();
   bool changed = false;

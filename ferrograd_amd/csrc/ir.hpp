@@ -229,6 +229,65 @@ struct UOpInner {
   ~UOpInner();
 };
 
+// Open-addressing map from node (or buffer) address to a 32-bit value, for the
+// per-realize graph walks where std::unordered_map's node allocations dominate.
+class PtrIndexMap {
+ public:
+  static constexpr uint32_t kAbsent = 0xffffffffu;
+  explicit PtrIndexMap(size_t expected = 256) { rehash(expected * 2); }
+  uint32_t get(const void* k) const {
+    for (size_t i = slot(k);; i = (i + 1) & mask_) {
+      if (keys_[i] == k) return vals_[i];
+      if (!keys_[i]) return kAbsent;
+    }
+  }
+  // Inserts k -> v unless k is present; returns the stored value.
+  uint32_t put(const void* k, uint32_t v) {
+    if ((size_ + 1) * 2 > keys_.size()) rehash(keys_.size() * 2);
+    for (size_t i = slot(k);; i = (i + 1) & mask_) {
+      if (keys_[i] == k) return vals_[i];
+      if (!keys_[i]) {
+        keys_[i] = k;
+        vals_[i] = v;
+        size_++;
+        return v;
+      }
+    }
+  }
+  void set(const void* k, uint32_t v) {
+    if ((size_ + 1) * 2 > keys_.size()) rehash(keys_.size() * 2);
+    for (size_t i = slot(k);; i = (i + 1) & mask_) {
+      if (keys_[i] == k || !keys_[i]) {
+        if (!keys_[i]) size_++;
+        keys_[i] = k;
+        vals_[i] = v;
+        return;
+      }
+    }
+  }
+  size_t size() const { return size_; }
+
+ private:
+  size_t slot(const void* k) const {
+    return static_cast<size_t>((reinterpret_cast<uintptr_t>(k) >> 4) * 0x9E3779B97F4A7C15ULL >> 20) & mask_;
+  }
+  void rehash(size_t cap) {
+    size_t n = 16;
+    while (n < cap) n <<= 1;
+    std::vector<const void*> ok(n, nullptr);
+    std::vector<uint32_t> ov(n, 0);
+    ok.swap(keys_);
+    ov.swap(vals_);
+    mask_ = n - 1;
+    size_ = 0;
+    for (size_t i = 0; i < ok.size(); i++)
+      if (ok[i]) set(ok[i], ov[i]);
+  }
+  std::vector<const void*> keys_;
+  std::vector<uint32_t> vals_;
+  size_t mask_ = 0, size_ = 0;
+};
+
 size_t interner_size();
 void interner_clear_for_tests();
 
@@ -238,6 +297,9 @@ UOpMap<std::vector<UOp>> build_consumer_map(const std::vector<UOp>& order);
 using RewriteFn = std::function<UOp(const UOp&)>;  // returns null UOp for "no match"
 UOp graph_rewrite(const UOp& root, const RewriteFn& fn);
 UOp substitute_with_map(const UOp& root, const UOpMap<UOp>& replacements);
+// substitute_with_map over several roots with one shared memo; the walk does
+// not descend below replaced nodes (their subgraphs cannot survive).
+std::vector<UOp> substitute_many(const std::vector<UOp>& roots, const UOpMap<UOp>& replacements);
 UOp flatten_end_bodies(const UOp& node);
 UOp flatten_nested_sinks(const UOp& node);
 

@@ -51,6 +51,7 @@ int debug_level() {  // tensor.rs:62-67
 }
 
 void clear_kernel_caches() {
+  clear_plan_cache();
   for (int d = 0; d < 2; d++) {
     lowering_cache(static_cast<DeviceId>(d)).clear();
     if (has_device(static_cast<DeviceId>(d))) get_device(static_cast<DeviceId>(d)).clear_for_tests();
@@ -83,35 +84,19 @@ UOp Tensor::uop() const { return p_->uop; }
 void Tensor::set_uop(const UOp& u) const { p_->uop = u; }
 
 // tensor.rs:222-252
+// Every live tensor whose graph reaches a replaced node is repointed at the
+// substituted graph. One memoised walk serves all live tensors and stops at
+// replaced nodes (the reference toposorts each live tensor's whole graph and
+// substitutes over the full graphs; the resulting graphs are the same).
 static void apply_map_to_tensors(const UOpMap<UOp>& replacements) {
   if (replacements.empty()) return;
-  std::vector<std::pair<Tensor, UOp>> affected[2];
-  // Whether a graph reaches a replaced node, memoised across all live tensors
-  // (the reference toposorts every live tensor's whole graph separately).
-  std::unordered_map<const UOpInner*, bool> reaches;
-  std::function<bool(const UOp&)> uses = [&](const UOp& n) -> bool {
-    auto it = reaches.find(n.get());
-    if (it != reaches.end()) return it->second;
-    bool r = replacements.count(n) > 0;
-    for (size_t i = 0; !r && i < n.srcs().size(); i++) r = uses(n.src(i));
-    reaches.emplace(n.get(), r);
-    return r;
-  };
-  for (auto& t : live_tensors()) {
-    UOp cur = t.uop();
-    if (!uses(cur)) continue;
-    affected[static_cast<int>(cur.device())].emplace_back(t, cur);
-  }
-  for (auto& group : affected) {
-    if (group.empty()) continue;
-    std::vector<UOp> roots;
-    for (auto& [t, r] : group) roots.push_back(r);
-    UOp s = substitute_with_map(UOp::sink(roots), replacements);
-    for (size_t i = 0; i < group.size(); i++) {
-      const UOp& nr = s.src(i);
-      if (nr != group[i].second) group[i].first.set_uop(nr);
-    }
-  }
+  std::vector<Tensor> live = live_tensors();
+  std::vector<UOp> roots;
+  roots.reserve(live.size());
+  for (auto& t : live) roots.push_back(t.uop());
+  std::vector<UOp> subst = substitute_many(roots, replacements);
+  for (size_t i = 0; i < live.size(); i++)
+    if (subst[i] != roots[i]) live[i].set_uop(subst[i]);
 }
 
 Tensor Tensor::from_bytes(const void* data, size_t nbytes, const Shape& shape, DType dtype, DeviceId dev) {
@@ -358,7 +343,7 @@ static void assert_kernel_ready(const UOp& root) {
 }
 
 // tensor.rs:831-898
-static void execute_item(const ScheduleItem& item) {
+static std::shared_ptr<Program> execute_item(const ScheduleItem& item) {
   const uint64_t start_ns = now_ns();
   Device& backend = get_device(item.sink.device());
   int debug = debug_level();
@@ -430,6 +415,291 @@ static void execute_item(const ScheduleItem& item) {
     double ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
     std::fprintf(stderr, "              exec time=%.3fms\n", ms);
   }
+  return program;
+}
+
+// ── plan cache ──────────────────────────────────────────────────────────────
+// schedule_many is a pure function of the lazy graph's structure, of which
+// buffers are shared between leaves, and of which leaf buffers still hold
+// allocate()'s zeros (zero-folding). A train loop rebuilds the same structure
+// over the same parameter buffers every step, so the whole realisation (kernel
+// partition, parameter slots, programs, argument wiring, replacement map) is
+// recorded once per structure and replayed: no rewrites, no interning beyond
+// the replacement buffers. The key is an exact serialisation, compared in full
+// on a hash match.
+namespace {
+
+struct GraphKey {
+  std::vector<UOp> order;            // toposort of Sink(roots)
+  std::vector<Buffer> leaves;        // distinct buffers, first-visit order
+  std::vector<uint64_t> code;        // exact structural serialisation
+  uint64_t hash = 0;
+};
+
+void key_word(GraphKey& k, uint64_t w) { k.code.push_back(w); }
+
+// One depth-first walk yields the toposort (the order UOp::toposort produces:
+// sources first, left to right, except After which walks its effect first)
+// and the serialisation, with one open-addressing map for both the visited
+// set and node positions.
+GraphKey graph_key(const std::vector<UOp>& roots, bool fuse) {
+  GraphKey k;
+  const UOp sink = UOp::sink(roots);
+  PtrIndexMap pos(1024);
+  PtrIndexMap leaf(64);
+  k.order.reserve(1024);
+  k.code.reserve(8192);
+  key_word(k, fuse ? 1 : 0);
+  std::vector<std::pair<const UOp*, bool>> stack;
+  stack.reserve(256);
+  stack.emplace_back(&sink, false);
+  while (!stack.empty()) {
+    auto [np, processed] = stack.back();
+    stack.pop_back();
+    const UOpInner* raw = np->get();
+    if (pos.get(raw) != PtrIndexMap::kAbsent) continue;
+    const auto& srcs = raw->srcs;
+    if (!processed) {
+      stack.emplace_back(np, true);
+      if (raw->op == Op::After) {
+        for (size_t i = 0; i < srcs.size(); i++)
+          if (pos.get(srcs[i].get()) == PtrIndexMap::kAbsent) stack.emplace_back(&srcs[i], false);
+      } else {
+        for (size_t i = srcs.size(); i-- > 0;)
+          if (pos.get(srcs[i].get()) == PtrIndexMap::kAbsent) stack.emplace_back(&srcs[i], false);
+      }
+      continue;
+    }
+    pos.set(raw, static_cast<uint32_t>(k.order.size()));
+    k.order.push_back(*np);
+    const Arg& a = raw->arg;
+    key_word(k, static_cast<uint64_t>(raw->op) | (static_cast<uint64_t>(raw->dtype.kind) << 8) |
+                    (static_cast<uint64_t>(raw->dtype.vcount) << 16) | (static_cast<uint64_t>(raw->has_tag) << 32) |
+                    (static_cast<uint64_t>(a.kind) << 40) | (static_cast<uint64_t>(a.rop) << 48));
+    if (raw->has_tag) key_word(k, raw->tag);
+    key_word(k, srcs.size());
+    for (auto& s : srcs) key_word(k, pos.get(s.get()));
+    if (a.kind == Arg::Kind::Buffer) {
+      const Buffer& b = a.buf;
+      if (!b) {
+        key_word(k, ~uint64_t(0));
+        continue;
+      }
+      uint32_t li = leaf.put(b.get(), static_cast<uint32_t>(k.leaves.size()));
+      if (li == k.leaves.size()) k.leaves.push_back(b);
+      key_word(k, li);
+      key_word(k, static_cast<uint64_t>(b->dtype.kind) | (static_cast<uint64_t>(b->known_zero) << 8) |
+                      (static_cast<uint64_t>(b->device) << 16));
+      key_word(k, b->numel);
+      continue;
+    }
+    uint64_t fbits;
+    std::memcpy(&fbits, &a.f, sizeof(fbits));
+    key_word(k, static_cast<uint64_t>(a.a));
+    key_word(k, static_cast<uint64_t>(a.b));
+    key_word(k, static_cast<uint64_t>(a.c));
+    key_word(k, fbits);
+    key_word(k, a.v.size());
+    for (auto x : a.v) key_word(k, static_cast<uint64_t>(x));
+    key_word(k, a.name.size());
+    for (size_t c = 0; c < a.name.size(); c += 8) {
+      uint64_t w = 0;
+      std::memcpy(&w, a.name.data() + c, std::min<size_t>(8, a.name.size() - c));
+      key_word(k, w);
+    }
+  }
+  uint64_t h = 1469598103934665603ULL;
+  for (uint64_t w : k.code) h = (h ^ w) * 1099511628211ULL;
+  k.hash = h;
+  return k;
+}
+
+struct PlanArg {
+  enum Kind : uint8_t { Leaf, Output, Value } kind = Value;
+  uint32_t index = 0;
+  KernelArg value;
+};
+
+struct PlanKernel {
+  std::shared_ptr<Program> program;
+  bool has_output = false;
+  DType out_dtype;
+  size_t out_numel = 0;
+  Shape out_shape;
+  std::vector<PlanArg> args;
+};
+
+struct PlanReplacement {
+  uint32_t node = 0;       // position of the replaced node in the key's order
+  int32_t kernel = -1;     // its kernel's output buffer, or
+  uint32_t value = 0;      // (kernel < 0) another node of the graph
+};
+
+struct CachedPlan {
+  std::vector<uint64_t> code;
+  std::vector<PlanKernel> kernels;
+  std::vector<PlanReplacement> replacements;
+  std::vector<uint32_t> written_leaves;  // leaves scheduling marked as overwritten
+};
+
+struct PlanCache {
+  std::unordered_map<uint64_t, std::vector<std::shared_ptr<CachedPlan>>> map;
+  size_t entries = 0;
+  bool enabled = true;
+  uint64_t hits = 0, misses = 0;
+};
+
+PlanCache& plan_cache() {
+  static PlanCache* c = new PlanCache();
+  return *c;
+}
+
+constexpr size_t kMaxCachedPlans = 512;
+
+std::shared_ptr<CachedPlan> find_plan(const GraphKey& k) {
+  auto it = plan_cache().map.find(k.hash);
+  if (it == plan_cache().map.end()) return nullptr;
+  for (auto& p : it->second)
+    if (p->code == k.code) return p;
+  return nullptr;
+}
+
+// Builds a replayable record of a realisation that just ran, or null when some
+// part of it is not expressible in terms of the key (then it is not cached).
+std::shared_ptr<CachedPlan> record_plan(const GraphKey& k, const SchedulePlan& plan,
+                                        const std::vector<std::shared_ptr<Program>>& programs,
+                                        const std::vector<uint8_t>& zero_before) {
+  auto rec = std::make_shared<CachedPlan>();
+  std::unordered_map<const BufferInner*, uint32_t> leaf_of, out_of;
+  for (uint32_t i = 0; i < k.leaves.size(); i++) leaf_of.emplace(k.leaves[i].get(), i);
+  for (size_t j = 0; j < plan.items.size(); j++) {
+    const ScheduleItem& item = plan.items[j];
+    PlanKernel pk;
+    pk.program = programs[j];
+    if (item.output_buffer) {
+      pk.has_output = true;
+      pk.out_dtype = item.output_buffer->dtype;
+      pk.out_numel = item.output_buffer->numel;
+      pk.out_shape = item.out_shape;
+      out_of.emplace(item.output_buffer.get(), static_cast<uint32_t>(j));
+    }
+    for (auto& in : item.inputs) {
+      PlanArg pa;
+      if (in.kind == KernelArg::Kind::Buffer) {
+        auto l = leaf_of.find(in.buffer.get());
+        auto o = out_of.find(in.buffer.get());
+        if (l != leaf_of.end()) {
+          pa.kind = PlanArg::Leaf;
+          pa.index = l->second;
+        } else if (o != out_of.end()) {
+          pa.kind = PlanArg::Output;
+          pa.index = o->second;
+        } else {
+          return nullptr;
+        }
+      } else {
+        pa.value = in;
+      }
+      pk.args.push_back(std::move(pa));
+    }
+    rec->kernels.push_back(std::move(pk));
+  }
+  std::unordered_map<const UOpInner*, uint32_t> pos;
+  for (uint32_t i = 0; i < k.order.size(); i++) pos.emplace(k.order[i].get(), i);
+  for (auto& [node, repl] : plan.replacements) {
+    auto np = pos.find(node.get());
+    if (np == pos.end()) return nullptr;
+    PlanReplacement pr;
+    pr.node = np->second;
+    if (repl.op() == Op::Reshape && repl.src(0).op() == Op::Buffer && repl.src(0).arg().buf &&
+        out_of.count(repl.src(0).arg().buf.get())) {
+      pr.kernel = static_cast<int32_t>(out_of.at(repl.src(0).arg().buf.get()));
+      if (rec->kernels[pr.kernel].out_shape != repl.arg().usizes()) return nullptr;
+    } else {
+      auto vp = pos.find(repl.get());
+      if (vp == pos.end()) return nullptr;
+      pr.value = vp->second;
+    }
+    rec->replacements.push_back(pr);
+  }
+  for (uint32_t i = 0; i < k.leaves.size(); i++)
+    if (zero_before[i] && !k.leaves[i]->known_zero) rec->written_leaves.push_back(i);
+  rec->code = k.code;
+  return rec;
+}
+
+void replay_plan(Device& backend, const GraphKey& k, const CachedPlan& plan) {
+  for (uint32_t i : plan.written_leaves) k.leaves[i]->known_zero = false;
+  std::vector<Buffer> outs(plan.kernels.size());
+  std::vector<KernelArg> args;
+  int debug = debug_level();
+  for (size_t j = 0; j < plan.kernels.size(); j++) {
+    const PlanKernel& pk = plan.kernels[j];
+    uint64_t l0 = now_ns();
+    args.clear();
+    if (pk.has_output) {
+      Buffer out = backend.reserve_buffer(pk.out_dtype, pk.out_numel);
+      backend.realize_storage(*out, false);
+      out->known_zero = false;
+      outs[j] = out;
+      args.push_back(KernelArg::buf(out));
+    }
+    for (auto& pa : pk.args) {
+      if (pa.kind == PlanArg::Value) {
+        args.push_back(pa.value);
+        continue;
+      }
+      const Buffer& b = pa.kind == PlanArg::Leaf ? k.leaves[pa.index] : outs[pa.index];
+      if (!b->is_realized()) {
+        FG_CHECK(b->zero_init, "scheduled input buffer missing");
+        backend.realize_storage(*b, true);
+      }
+      args.push_back(KernelArg::buf(b));
+    }
+    uint64_t l1 = now_ns();
+    realize_stats().ns_lower += l1 - l0;
+    realize_stats().lowering_cache_hits++;
+    if (debug >= 1) {
+      size_t kid = g_kernel_count++;
+      std::fprintf(stderr, "*** %s %4zu  (plan)           arg %2zu\n", backend.id() == DeviceId::Hip ? "HIP" : "CPU",
+                   kid, args.size());
+    }
+    backend.execute(*pk.program, args);
+    realize_stats().ns_launch += now_ns() - l1;
+    realize_stats().kernels_launched++;
+  }
+  uint64_t t2 = now_ns();
+  UOpMap<UOp> repl;
+  repl.reserve(plan.replacements.size() * 2);
+  for (auto& pr : plan.replacements) {
+    const UOp& node = k.order[pr.node];
+    if (pr.kernel >= 0) {
+      const PlanKernel& pk = plan.kernels[pr.kernel];
+      repl[node] = UOp::reshape(UOp::buffer(outs[pr.kernel], pk.out_dtype, node.device()), pk.out_shape);
+    } else {
+      repl[node] = k.order[pr.value];
+    }
+  }
+  apply_map_to_tensors(repl);
+  realize_stats().ns_apply_map += now_ns() - t2;
+}
+
+}  // namespace
+
+void set_plan_cache_enabled(bool on) {
+  plan_cache().enabled = on;
+  if (!on) clear_plan_cache();
+}
+
+void clear_plan_cache() {
+  plan_cache().map.clear();
+  plan_cache().entries = 0;
+}
+
+void plan_cache_stats(uint64_t* hits, uint64_t* misses, uint64_t* entries) {
+  *hits = plan_cache().hits;
+  *misses = plan_cache().misses;
+  *entries = plan_cache().entries;
 }
 
 void Tensor::realize_many(const std::vector<Tensor>& tensors) {  // tensor.rs:781-821
@@ -445,10 +715,33 @@ void Tensor::realize_many(const std::vector<Tensor>& tensors) {  // tensor.rs:78
   ScheduleOptions opt;
   opt.fuse = get_device(roots[0].device()).fuse_elementwise();
   uint64_t t0 = now_ns();
+  PlanCache& pc = plan_cache();
+  GraphKey key;
+  std::vector<uint8_t> zero_before;
+  if (pc.enabled) {
+    key = graph_key(roots, opt.fuse);
+    if (auto hit = find_plan(key)) {
+      pc.hits++;
+      realize_stats().ns_schedule += now_ns() - t0;
+      replay_plan(get_device(roots[0].device()), key, *hit);
+      return;
+    }
+    pc.misses++;
+    for (auto& b : key.leaves) zero_before.push_back(b->known_zero ? 1 : 0);
+  }
   SchedulePlan plan = schedule_many(roots, opt);
   uint64_t t1 = now_ns();
   realize_stats().ns_schedule += t1 - t0;
-  for (auto& item : plan.items) execute_item(item);
+  std::vector<std::shared_ptr<Program>> programs;
+  programs.reserve(plan.items.size());
+  for (auto& item : plan.items) programs.push_back(execute_item(item));
+  if (pc.enabled) {
+    if (auto rec = record_plan(key, plan, programs, zero_before)) {
+      if (pc.entries >= kMaxCachedPlans) clear_plan_cache();
+      pc.map[key.hash].push_back(std::move(rec));
+      pc.entries++;
+    }
+  }
   uint64_t t2 = now_ns();
   apply_map_to_tensors(plan.replacements);
   realize_stats().ns_apply_map += now_ns() - t2;

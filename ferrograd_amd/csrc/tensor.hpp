@@ -135,7 +135,12 @@ struct RealizeStats {
 };
 RealizeStats& realize_stats();
 int debug_level();
-// Drops every cached program and lowering on all registered devices.
+// Drops every cached program, lowering and realisation plan on all devices.
 void clear_kernel_caches();
+// Realisation plan cache (structure of the lazy graph -> recorded kernel
+// launches and replacements). On by default.
+void set_plan_cache_enabled(bool on);
+void clear_plan_cache();
+void plan_cache_stats(uint64_t* hits, uint64_t* misses, uint64_t* entries);
 
 }  // namespace fg

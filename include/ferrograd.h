@@ -65,6 +65,12 @@ int fg_tensor_read(fg_tensor* t, void* dst, size_t nbytes);
 int fg_tensor_shape(fg_tensor* t, int64_t* shape, int* ndim);
 int fg_tensor_info(fg_tensor* t, int* dtype, int* device, int* realized, int* requires_grad);
 int fg_tensor_set_requires_grad(fg_tensor* t, int requires_grad);
+/* Storage of a realised tensor: the device pointer (HIP) or host pointer
+ * (cpu) and its byte size, for zero-copy interop. The pointer stays valid while
+ * the tensor's buffer is alive and may change when the tensor is realised
+ * again; lazily zero-filled storage is materialised first. No reference
+ * counterpart (the reference keeps Storage opaque, device.rs:60-70). */
+int fg_tensor_data_ptr(fg_tensor* t, void** ptr, size_t* nbytes);
 int fg_tensor_same(fg_tensor* a, fg_tensor* b, int* same);
 
 /* Autograd (tensor.rs:938-998). fg_tensor_grad sets *out to NULL if none. */
@@ -96,6 +102,14 @@ int fg_stats(uint64_t* kernels_launched, uint64_t* programs_compiled, uint64_t* 
  * live-tensor rewrite after realisation, backward graph construction. */
 int fg_host_times(uint64_t out[5]);
 int fg_clear_caches(void);
+/* Realisation plans: realize_many records each distinct lazy-graph structure
+ * (with its buffer sharing and which leaves still hold zeros) together with
+ * its kernel launches, and replays that record when the structure recurs, as
+ * in a training loop. Replays produce the same kernels, arguments and results;
+ * disabling the cache (on = 0) also drops it. No reference counterpart (the
+ * reference reschedules every realize, tensor.rs:781-821). */
+int fg_plan_cache_enable(int on);
+int fg_plan_cache_stats(uint64_t* hits, uint64_t* misses, uint64_t* entries);
 
 /* Inspection for tests and tooling: schedule the roots (without running
  * anything) and describe the plan as JSON; optionally render each kernel with

@@ -28,6 +28,17 @@ def test_c2_is_one_vectorised_elementwise_kernel(fg, cpu):
     compile_only(fg, src, items[0]["name"])
 
 
+def test_large_elementwise_output_uses_streaming_stores(fg, cpu):
+    # >= 128 MiB of output (2^25 f32) is written past the caches; smaller outputs are not.
+    n = 1 << 25
+    a = fg.Tensor.new(np.ones(n, np.float32), [n], cpu)
+    src = hip_plan(fg, [a.mul(a).relu()])[0]["source"]
+    assert "__builtin_nontemporal_store(vout, (fg_f4*)" in src and "*(float4*)" not in src
+    compile_only(fg, src, hip_plan(fg, [a.mul(a).relu()])[0]["name"])
+    small = fg.Tensor.new(np.ones(n // 2, np.float32), [n // 2], cpu)
+    assert "__builtin_nontemporal_store" not in hip_plan(fg, [small.mul(small).relu()])[0]["source"]
+
+
 def test_c1_is_one_row_reduce_with_dpp_tree(fg, cpu):
     x = fg.Tensor.new(np.ones((64, 4096), np.float32), [64, 4096], cpu)
     y = x.mul(fg.Tensor.scalar(0.5, cpu)).add(fg.Tensor.scalar(1.0, cpu)).relu().sum([1])

@@ -1,0 +1,101 @@
+"""Realisation-plan replay: a recurring lazy-graph structure replays its
+recorded kernels instead of being rescheduled. Replays must be
+indistinguishable from scheduling afresh: same results bit for bit, and every
+input that changes the schedule (buffer sharing, leaves still holding zeros,
+literal values) must select a different plan."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from conftest import seeded
+
+
+@pytest.fixture
+def fresh_plans(fg):
+    fg.plan_cache(False)
+    fg.plan_cache(True)
+    yield
+    fg.plan_cache(True)
+
+
+def train(fg, dev, steps, enabled):
+    fg.plan_cache(enabled)
+    r = seeded(7)
+    x = r.uniform(0, 1, (16, 784)).astype(np.float32)
+    t = np.eye(10, dtype=np.float32)[np.floor(r.uniform(0, 1, 16) * 10).astype(int)]
+    fg.reset_init_seed(42)
+    l1, l2 = fg.Linear(784, 32, dev), fg.Linear(32, 10, dev)
+    params = l1.parameters() + l2.parameters()
+    opt = fg.Sgd(params, 0.01)
+    tx, tt = fg.Tensor.new(x, [16, 784], dev), fg.Tensor.new(t, [16, 10], dev)
+    losses = []
+    for _ in range(steps):
+        loss = l2(l1(tx).relu()).cross_entropy(tt)
+        opt.zero_grad()
+        loss.backward()
+        opt.step()
+        losses.append(loss.to_vec()[0])
+    return losses, [p.numpy() for p in params]
+
+
+def check_replay_matches_fresh(fg, dev):
+    before = fg.plan_stats()["hits"]
+    l_on, p_on = train(fg, dev, 4, True)
+    hits = fg.plan_stats()["hits"] - before
+    l_off, p_off = train(fg, dev, 4, False)
+    fg.plan_cache(True)
+    assert hits >= 4  # steps 2..4 replay both realisations of the step
+    assert l_on == l_off
+    for a, b in zip(p_on, p_off):
+        assert np.array_equal(a, b)
+
+
+def test_replayed_train_steps_match_fresh_scheduling(fg, cpu, fresh_plans):
+    check_replay_matches_fresh(fg, cpu)
+
+
+@pytest.mark.gpu
+def test_replayed_train_steps_match_fresh_scheduling_hip(fg, hip, fresh_plans):
+    check_replay_matches_fresh(fg, hip)
+
+
+def test_zero_leaf_then_written_selects_new_plan(fg, cpu, fresh_plans):
+    x = fg.Tensor.new([1.0, 2.0, 3.0, 4.0], [4], cpu)
+    z = fg.Tensor.zeros([4], cpu)
+    assert x.add(z).relu().to_vec() == [1.0, 2.0, 3.0, 4.0]  # z folded to a literal 0
+    z.assign(fg.Tensor.new([10.0, 20.0, 30.0, 40.0], [4], cpu))
+    fg.Tensor.realize_many([z])
+    # Same structure over the same buffers, but z no longer holds zeros.
+    assert x.add(z).relu().to_vec() == [11.0, 22.0, 33.0, 44.0]
+
+
+def test_buffer_sharing_is_part_of_the_key(fg, cpu, fresh_plans):
+    a = fg.Tensor.new([1.0, 2.0], [2], cpu)
+    b = fg.Tensor.new([5.0, 7.0], [2], cpu)
+    assert a.mul(a).add(b).to_vec() == [6.0, 11.0]
+    assert a.mul(b).add(b).to_vec() == [10.0, 21.0]
+    assert b.mul(b).add(a).to_vec() == [26.0, 51.0]  # same sharing as the first: replay, new buffers
+
+
+def test_new_leaf_values_replay_with_new_buffers(fg, cpu, fresh_plans):
+    x = fg.Tensor.new(np.arange(8, dtype=np.float32), [8], cpu)
+    outs = []
+    for s in (0.5, 2.0, -1.0):
+        outs.append(x.mul(fg.Tensor.scalar(s, cpu)).sum([0]).to_vec()[0])
+    assert outs == [14.0, 56.0, -28.0]
+    assert fg.plan_stats()["hits"] >= 2
+
+
+def test_literal_values_are_part_of_the_key(fg, cpu, fresh_plans):
+    x = fg.Tensor.new(np.arange(6, dtype=np.float32), [6], cpu)
+    assert x.narrow(0, 1, 2).contiguous().to_vec() == [1.0, 2.0]
+    assert x.narrow(0, 3, 2).contiguous().to_vec() == [3.0, 4.0]
+
+
+def test_disabling_drops_recorded_plans(fg, cpu, fresh_plans):
+    x = fg.Tensor.new([1.0], [1], cpu)
+    x.add(x).to_vec()
+    assert fg.plan_stats()["entries"] >= 1
+    fg.plan_cache(False)
+    assert fg.plan_stats()["entries"] == 0
