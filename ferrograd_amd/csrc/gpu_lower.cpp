@@ -343,6 +343,19 @@ class Emitter {
   }
   void set_lane_base_aligned(bool b) { lane_base_aligned_ = b; }
   void set_nontemporal_loads(bool b) { nt_loads_ = b; }
+  // Non-temporal loads only for addresses that depend on every one of these
+  // ranges (the kernel's output ranges): such an element is read by one
+  // output only. Loads shared by several outputs stay cacheable.
+  void set_streaming_ranges(const std::vector<UOp>& rs) {
+    nt_ranges_.clear();
+    for (auto& r : rs) nt_ranges_.push_back(r.get());
+  }
+  bool streams(const UOp& index) {
+    if (!nt_loads_) return false;
+    for (auto* r : nt_ranges_)
+      if (!depends_on(index, r)) return false;
+    return true;
+  }
 
   std::string val(const UOp& n, int lane) {
     bool lane_dep = lane_range_ && depends_on(n, lane_range_);
@@ -368,7 +381,7 @@ class Emitter {
         const char* vt = n.dtype().kind == DTypeKind::F32 ? "fg_f4" : "fg_i4";
         std::string addr = std::string("(const ") + vt + "*)(" + pname(ix.src(0)) + "+" + idx(ix.src(1), 0) + ")";
         // Streaming kernels read each element once: non-temporal 16-byte loads.
-        std::string rhs = nt_loads_ ? "__builtin_nontemporal_load(" + addr + ")" : "*" + addr;
+        std::string rhs = streams(ix.src(1)) ? "__builtin_nontemporal_load(" + addr + ")" : "*" + addr;
         emit_at(si, std::string("const ") + vt + " " + v + " = " + rhs + ";");
         static const char* comp[4] = {".x", ".y", ".z", ".w"};
         for (int u = 0; u < 4; u++) remember(si, std::make_pair(n.get(), u), v + comp[u]);
@@ -441,6 +454,7 @@ class Emitter {
   int lanes_ = 1;
   bool lane_base_aligned_ = true;
   bool nt_loads_ = false;
+  std::vector<const UOpInner*> nt_ranges_;
   int counter_ = 0;
 };
 
@@ -615,6 +629,7 @@ RenderedKernel render_serial(const KernelInfo& ki, const std::string& name) {
 RenderedKernel render_elementwise(const KernelInfo& ki, const std::string& name) {
   Emitter em;
   em.set_nontemporal_loads(true);
+  em.set_streaming_ranges(ki.out_ranges);
   UOp fast = pick_fast_output(ki);
   int64_t T = total_outputs(ki);
   int V = 1;
@@ -710,9 +725,30 @@ RenderedKernel render_row_reduce(const KernelInfo& ki, const std::string& name) 
   }
   Emitter em;
   em.set_nontemporal_loads(true);
+  em.set_streaming_ranges(ki.out_ranges);
+  const int64_t grid = (NOUT + OPW - 1) / OPW;
   em.line("const int tid = threadIdx.x;");
   em.line("const int rlane = tid % " + std::to_string(T) + ";");
-  em.line("const long oid = (long)blockIdx.x * " + std::to_string(OPW) + " + tid / " + std::to_string(T) + ";");
+  // Whether some streamed operand (one that varies along the reduce axis) is
+  // read by several outputs: the same row for every output column of a
+  // narrow matmul.
+  bool shared_rows = false;
+  for (auto& ld : loads_in(R.src(0))) {
+    const UOp& ix = ld.src(0).src(1);
+    if (!em.depends_on(ix, r_in.get())) continue;
+    for (auto& o : ki.out_ranges)
+      if (!em.depends_on(ix, o.get())) shared_rows = true;
+  }
+  if (shared_rows && grid % 8 == 0) {
+    // Workgroups are dispatched round-robin over the 8 XCDs: give each XCD a
+    // contiguous run of outputs, so the outputs that share an input row read
+    // it through one L2. (Outputs that each stream their own rows keep the
+    // interleaved order, which spreads the 8 XCDs' reads over HBM better.)
+    em.line("const long bid = (long)(blockIdx.x % 8) * " + std::to_string(grid / 8) + " + blockIdx.x / 8;");
+  } else {
+    em.line("const long bid = blockIdx.x;");
+  }
+  em.line("const long oid = bid * " + std::to_string(OPW) + " + tid / " + std::to_string(T) + ";");
   em.line("const bool active = oid < " + std::to_string(NOUT) + "L;");
   em.line("const long ocl = active ? oid : 0;");
   decode_outputs(em, ki, "ocl", UOp());
@@ -803,6 +839,7 @@ RenderedKernel render_column_reduce_split(const KernelInfo& ki, const std::strin
   // Pass 1: partial sums.
   Emitter p1;
   p1.set_nontemporal_loads(true);
+  p1.set_streaming_ranges(ki.out_ranges);
   p1.line("const int tid = threadIdx.x;");
   p1.line("const int tx = tid % " + std::to_string(TX) + ", tr = tid / " + std::to_string(TX) + ";");
   p1.line("const long cb = blockIdx.x % " + std::to_string(per_f * other) + ";");
@@ -916,6 +953,7 @@ RenderedKernel render_column_reduce(const KernelInfo& ki, const std::string& nam
   if (nchunks > 1) return render_column_reduce_split(ki, name, V, TX, TR, per_f, other, fext, nchunks);
   Emitter em;
   em.set_nontemporal_loads(true);
+  em.set_streaming_ranges(ki.out_ranges);
   em.line("const int tid = threadIdx.x;");
   em.line("const int tx = tid % " + std::to_string(TX) + ", tr = tid / " + std::to_string(TX) + ";");
   em.line("const int fbase = (int)(blockIdx.x % " + std::to_string(per_f) + ") * " + std::to_string(TX * V) + " + tx * " +

@@ -178,10 +178,65 @@ bool reconverges(const UOp& node, const UOpMap<std::vector<UOp>>& consumers, con
   return true;
 }
 
+// What a kernel reading `src` loads: a literal, one buffer, or something that
+// needs computing. Movement views of constants, of allocate()'s still-zero
+// buffers (read as literals when fusing) and of buffers are leaves, as are
+// nodes already materialised.
+enum class LeafKind { Literal, Buffer, Computed };
+LeafKind leaf_kind(const UOp& src, const UOpMap<UOp>& materialized) {
+  UOp b = src;
+  while (true) {
+    if (materialized.count(b)) return LeafKind::Buffer;
+    if (!is_movement(b.op()) || b.op() == Op::Contiguous) break;
+    b = b.src(0);
+  }
+  if (b.op() == Op::Const) return LeafKind::Literal;
+  if (b.op() == Op::Buffer) {
+    const Buffer& h = b.arg().buf;
+    if (h && h->known_zero && b.dtype() == DType::F32()) return LeafKind::Literal;
+    return LeafKind::Buffer;
+  }
+  return LeafKind::Computed;
+}
+
+// A multi-consumer node cheap enough to recompute in each consumer: one
+// comparison or arithmetic op over literals and at most one loaded value
+// (relu's mask `0 < x` is the case that matters). Recomputing it reads x where
+// the materialised node would have been read, and gives the same bits.
+bool cheap_to_recompute(const UOp& node, const UOpMap<UOp>& materialized) {
+  switch (node.op()) {
+    case Op::CmpLt: case Op::Neg: case Op::Add: case Op::Mul: case Op::Max: case Op::Where: break;
+    default: return false;
+  }
+  int loads = 0;
+  for (auto& s : node.srcs()) {
+    LeafKind k = leaf_kind(s, materialized);
+    if (k == LeafKind::Computed) return false;
+    if (k == LeafKind::Buffer) loads++;
+  }
+  return loads <= 1;
+}
+
+// Whether `expr` (a kernel value under construction) computes a reduction
+// that is not yet materialised.
+bool has_unmaterialized_reduce(const UOp& expr, const UOpMap<UOp>& materialized, const UOp& except) {
+  std::vector<UOp> stack{expr};
+  UOpSet seen;
+  while (!stack.empty()) {
+    UOp n = stack.back();
+    stack.pop_back();
+    if (n == except || materialized.count(n) || !seen.insert(n).second) continue;
+    if (n.op() == Op::ReduceAxis) return true;
+    for (auto& s : n.srcs()) stack.push_back(s);
+  }
+  return false;
+}
+
 // schedule.rs:289-335
 bool should_materialize(const UOp& node, const UOpSet& roots,
                         const UOpMap<std::vector<UOp>>& consumers, const UOpSet& nested,
-                        const ScheduleOptions& opt, const UOpMap<size_t>& topo_idx) {
+                        const ScheduleOptions& opt, const UOpMap<size_t>& topo_idx,
+                        const UOpMap<UOp>& materialized) {
   if (roots.count(node) || !node.has_shape()) return false;
   switch (node.op()) {
     case Op::Sink: case Op::Store: case Op::After: case Op::Assign: case Op::DefineAcc:
@@ -194,7 +249,8 @@ bool should_materialize(const UOp& node, const UOpSet& roots,
   if (node.has_buffer_identity()) return false;
   auto it = consumers.find(node);
   if (it != consumers.end() && it->second.size() > 1) {
-    if (opt.fuse && reconverges(node, consumers, roots, topo_idx)) return false;
+    if (opt.fuse && (reconverges(node, consumers, roots, topo_idx) || cheap_to_recompute(node, materialized)))
+      return false;
     return true;
   }
   if (node.op() == Op::ReduceAxis && it != consumers.end()) {
@@ -202,6 +258,25 @@ bool should_materialize(const UOp& node, const UOpSet& roots,
       if (is_alu(c.op())) return true;
   }
   return node.op() == Op::ReduceAxis && nested.count(node);
+}
+
+// The elementwise node a reduce feeds through a chain of single-consumer
+// reshapes/permutes (views that read each reduced value once), or null. When
+// fusing, the reduce can run as that node's epilogue instead of writing its
+// own buffer.
+UOp epilogue_consumer(const UOp& reduce, const UOpMap<std::vector<UOp>>& consumers, const UOpSet& roots) {
+  UOp cur = reduce;
+  while (true) {
+    if (roots.count(cur)) return UOp();
+    auto it = consumers.find(cur);
+    if (it == consumers.end() || it->second.size() != 1) return UOp();
+    const UOp& c = it->second[0];
+    if (c.op() == Op::Reshape || c.op() == Op::Permute) {
+      cur = c;
+      continue;
+    }
+    return is_alu(c.op()) ? c : UOp();
+  }
 }
 
 // schedule.rs:340-353
@@ -295,12 +370,40 @@ SchedulePlan schedule_many(const std::vector<UOp>& exprs, const ScheduleOptions&
   for (size_t i = 0; i < order.size(); i++) topo_idx[order[i]] = i;
 
   SchedulePlan plan;
-  for (auto& node : order) {
-    if (!should_materialize(node, roots, consumers, nested, opt, topo_idx)) continue;
+  auto materialize = [&](const UOp& node) {
     UOp kexpr = substitute_materialized(node, plan.replacements);
     ScheduleItem item = parameterize(kexpr, opt);
     plan.replacements[node] = buffer_replacement(item);
     plan.items.push_back(std::move(item));
+  };
+  // Reduces held back to run as the epilogue of the elementwise node they
+  // feed (fusing only), keyed by that node. Value-preserving: the kernel
+  // applies the same elementwise ops to the same reduced values.
+  UOpMap<UOp> deferred;
+  for (auto& node : order) {
+    auto d = deferred.find(node);
+    if (d != deferred.end()) {
+      // The reduce stays fused only if this node gets a kernel of its own and
+      // that kernel computes no other reduction.
+      bool own_kernel = roots.count(node) ||
+                        should_materialize(node, roots, consumers, nested, opt, topo_idx, plan.replacements);
+      if (!own_kernel || has_unmaterialized_reduce(node, plan.replacements, d->second)) materialize(d->second);
+      deferred.erase(d);
+    }
+    if (!should_materialize(node, roots, consumers, nested, opt, topo_idx, plan.replacements)) continue;
+    if (opt.fuse && node.op() == Op::ReduceAxis) {
+      UOp c = epilogue_consumer(node, consumers, roots);
+      // One reduce per consumer; and not into a root that other nodes read
+      // (roots are computed inline by their readers until the end).
+      bool root_read = false;
+      if (c && roots.count(c) && consumers.count(c))
+        for (auto& r : consumers.at(c)) root_read = root_read || r != uni;
+      if (c && !root_read && !deferred.count(c)) {
+        deferred[c] = node;
+        continue;
+      }
+    }
+    materialize(node);
   }
   for (auto& expr : exprs) {
     UOp fin = substitute_materialized(expr, plan.replacements);

@@ -130,3 +130,53 @@ def test_assign_in_same_schedule_disables_folding_for_later_kernels(fg, cpu):
     y = z.add(fg.Tensor.new([1.0] * 4, [4], cpu))
     items = plan(fg, [z, y], fuse=True)
     assert len(items) == 2 and len(items[1]["inputs"]) == 2
+
+
+def mlp_forward(fg, dev, dims=(32, 64, 48, 10), batch=16):
+    fg.reset_init_seed(42)
+    layers = [fg.Linear(dims[i], dims[i + 1], dev) for i in range(len(dims) - 1)]
+    x = fg.Tensor.new(np.full((batch, dims[0]), 0.5, np.float32), [batch, dims[0]], dev)
+    t = fg.Tensor.new(np.eye(dims[-1], dtype=np.float32)[np.arange(batch) % dims[-1]], [batch, dims[-1]], dev)
+    h = x
+    for i, l in enumerate(layers):
+        h = l(h)
+        if i + 1 < len(layers):
+            h = h.relu()
+    return layers, h.cross_entropy(t)
+
+
+def test_fusion_runs_linear_bias_as_reduce_epilogue_and_recomputes_relu_mask(fg, cpu):
+    # Reference partition: the matmul reduce and `mm + b` are separate kernels
+    # (nested-reduce rule), and relu's mask `0 < pre` is a bool buffer shared by
+    # forward and backward. Fused: `mm + b` is the reduce's epilogue and the
+    # mask is recomputed from pre by its readers.
+    layers, loss = mlp_forward(fg, cpu)
+    loss.backward()
+    params = [p for l in layers for p in l.parameters()]
+    for p in params:
+        p.assign(p.detach().sub(p.grad().mul(fg.Tensor.scalar(0.01, cpu))))
+    ref = plan(fg, params + [loss])
+    fused = plan(fg, params + [loss], fuse=True, render=True)
+    assert len(fused) < len(ref)
+    assert not any("bool* __restrict__ data0" in it["source"] for it in fused)  # no mask buffer
+    # Every [16, 64] / [16, 48] pre-activation is written by a reduction kernel.
+    pre = [it for it in fused if it.get("out_shape") in ([16, 64], [16, 48])]
+    assert pre and all(it["class"] != "elementwise" for it in pre)
+
+
+def test_reduce_read_through_broadcast_stays_materialised(fg, cpu):
+    # y = 2 * x.sum(1) feeds a broadcast: fusing it into the consumer would
+    # recompute the sum for every broadcast element, so it keeps its kernel.
+    x = fg.Tensor.new(np.ones((4, 8), np.float32), [4, 8], cpu)
+    y = x.sum([1]).mul(fg.Tensor.scalar(2.0, cpu))
+    z = y.expand([4, 8]).add(x)
+    items = plan(fg, [z], fuse=True, render=True)
+    assert [it["class"] for it in items] == ["row_reduce", "elementwise"]
+
+
+def test_two_reduces_into_one_consumer_keep_one_per_kernel(fg, cpu):
+    x = fg.Tensor.new(np.ones((4, 8), np.float32), [4, 8], cpu)
+    w = fg.Tensor.new(np.ones((4, 8), np.float32), [4, 8], cpu)
+    z = x.sum([1]).add(w.max([1]))
+    items = plan(fg, [z], fuse=True, render=True)
+    assert len(items) == 2 and all(it["class"] == "row_reduce" for it in items)
