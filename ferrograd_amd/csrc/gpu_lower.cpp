@@ -1085,22 +1085,34 @@ bool match_gemm(const KernelInfo& ki, GemmMatch* g) {
 
 RenderedKernel render_gemm(const KernelInfo& ki, const GemmMatch& g, const std::string& name) {
   const int64_t M = g.M, N = g.N, K = g.K;
-  // Tile: 128x128 when that still gives a few hundred tiles, else 64-wide.
-  int BM = 128, BN = 128;
-  if ((M + 127) / 128 * ((N + 127) / 128) < 256) {
+  // Tile shape (measured on MI355X, fp32 4096^3: 256x256/BK16/8 waves 131
+  // TFLOP/s, 256x128/BK8/4 waves 128, 128x128/BK16/4 waves 114): the largest
+  // tile that still gives every CU a tile, else the previous 128/64 shapes.
+  auto tiles = [&](int64_t bm, int64_t bn) { return ((M + bm - 1) / bm) * ((N + bn - 1) / bn); };
+  int BM = 128, BN = 128, BK = 16, WGM = 2, WGN = 2;
+  if (M >= 256 && N >= 256 && tiles(256, 256) >= 256) {
+    BM = 256; BN = 256; BK = 16; WGM = 4; WGN = 2;
+  } else if (M >= 256 && N >= 128 && tiles(256, 128) >= 256) {
+    BM = 256; BN = 128; BK = 8;
+  } else if (M >= 128 && N >= 256 && tiles(128, 256) >= 256) {
+    BM = 128; BN = 256; BK = 8;
+  } else if (tiles(128, 128) < 256) {
     BM = M >= 128 && (M + 63) / 64 * ((N + 63) / 64) < 128 ? 128 : 64;
     BN = 64;
   }
   if (N <= 64) BN = 64;
   if (M <= 64) BM = 64;
-  const int BK = 16;
-  const int PAD = 4;
+  const int NT = 64 * WGM * WGN;
+  const int PAD = 4;  // keeps LDS rows 16-byte aligned for float4 stores
+  FG_CHECK(BM % (32 * WGM) == 0 && BN % (32 * WGN) == 0 && BM * BK % (4 * NT) == 0 && BN * BK % (4 * NT) == 0,
+           "gemm tile shape does not fit the wave grid");
 
   std::ostringstream s;
   s << kPrelude;
   s << "#define M_ " << M << "\n#define N_ " << N << "\n#define K_ " << K << "\n";
   s << "#define BM " << BM << "\n#define BN " << BN << "\n#define BK " << BK << "\n#define PAD " << PAD << "\n";
-  s << signature(ki, name, 256) << " {\n";
+  s << "#define NT " << NT << "\n#define WGN " << WGN << "\n";
+  s << signature(ki, name, NT) << " {\n";
   s << R"(  __shared__ float As[2][BK][BM + PAD];
   __shared__ float Bs[2][BK][BN + PAD];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -1114,9 +1126,9 @@ RenderedKernel render_gemm(const KernelInfo& ki, const GemmMatch& g, const std::
   const int gsz = (nbm - first_m) < GM ? (nbm - first_m) : GM;
   const int tm = first_m + (bid % (GM * nbn)) % gsz, tn = (bid % (GM * nbn)) / gsz;
   const int m0 = tm * BM, n0 = tn * BN;
-  // 2x2 waves; each wave owns a (BM/2)x(BN/2) block of 32x32 MFMA tiles.
-  constexpr int WM = BM / 2, WN = BN / 2, TM = WM / 32, TN = WN / 32;
-  const int wm = (wave >> 1) * WM, wn = (wave & 1) * WN;
+  // A grid of waves; each wave owns a WM x WN block of 32x32 MFMA tiles.
+  constexpr int WM = BM / (NT / 64 / WGN), WN = BN / WGN, TM = WM / 32, TN = WN / 32;
+  const int wm = (wave / WGN) * WM, wn = (wave % WGN) * WN;
   floatx16 acc[TM][TN];
   #pragma unroll
   for (int i = 0; i < TM; i++)
@@ -1124,7 +1136,7 @@ RenderedKernel render_gemm(const KernelInfo& ki, const GemmMatch& g, const std::
     for (int j = 0; j < TN; j++)
       #pragma unroll
       for (int e = 0; e < 16; e++) acc[i][j][e] = 0.0f;
-  constexpr int AE = BM * BK / 256, BE = BN * BK / 256;  // elements per thread per stage
+  constexpr int AE = BM * BK / NT, BE = BN * BK / NT;  // elements per thread per stage
   float ra[AE], rb[BE];
 )";
   // Global -> register loaders. Staging modes: 0 = 4 consecutive k per thread
@@ -1161,22 +1173,22 @@ RenderedKernel render_gemm(const KernelInfo& ki, const GemmMatch& g, const std::
     std::ostringstream l;
     l << "  auto load_" << X << " = [&](int k0) {\n";
     if (md == 0 || md == 1) {
-      l << "    #pragma unroll\n    for (int j = 0; j < " << BX << " * BK / 1024; j++) {\n";
+      l << "    #pragma unroll\n    for (int j = 0; j < " << BX << " * BK / (4 * NT); j++) {\n";
+      l << "      const int idx = tid + NT * j;\n";
       if (md == 0) {
-        l << "      const int r = tid / 4 + 64 * j, kq = (tid % 4) * 4;\n";
+        l << "      const int r = idx / (BK / 4), kq = (idx % (BK / 4)) * 4;\n";
         l << "      const int gr = " << dim << "0 + r, gk = k0 + kq;\n";
       } else {
-        l << "      const int kk = tid / (" << BX << " / 4) + (256 / (" << BX << " / 4)) * j, r = (tid % (" << BX
-          << " / 4)) * 4;\n";
+        l << "      const int kk = idx / (" << BX << " / 4), r = (idx % (" << BX << " / 4)) * 4;\n";
         l << "      const int gr = " << dim << "0 + r, gk = k0 + kk;\n";
       }
       l << "      float* dst = &r" << X << "[4*j];\n";
       l << "      if (gr < " << ext << " && gk < K_) {\n" << body("dst", md == 0, md == 1) << "      } else {\n";
       l << "        dst[0] = 0.0f; dst[1] = 0.0f; dst[2] = 0.0f; dst[3] = 0.0f;\n      }\n    }\n";
     } else {
-      l << "    #pragma unroll\n    for (int e = 0; e < " << BX << " * BK / 256; e++) {\n";
-      if (k_fast) l << "      const int i = tid + 256 * e, r = i / BK, kk = i % BK;\n";
-      else l << "      const int i = tid + 256 * e, kk = i / " << BX << ", r = i % " << BX << ";\n";
+      l << "    #pragma unroll\n    for (int e = 0; e < " << BX << " * BK / NT; e++) {\n";
+      if (k_fast) l << "      const int i = tid + NT * e, r = i / BK, kk = i % BK;\n";
+      else l << "      const int i = tid + NT * e, kk = i / " << BX << ", r = i % " << BX << ";\n";
       l << "      const int gr = " << dim << "0 + r, gk = k0 + kk;\n";
       l << "      if (gr < " << ext << " && gk < K_) {\n" << body("r" + std::string(X) + "[e]", 0, 0)
         << "      } else {\n        r" << X << "[e] = 0.0f;\n      }\n    }\n";
@@ -1185,19 +1197,18 @@ RenderedKernel render_gemm(const KernelInfo& ki, const GemmMatch& g, const std::
     l << "  auto store_" << X << " = [&](int buf) {\n";
     const char* S = X[0] == 'a' ? "As" : "Bs";
     if (md == 0) {
-      l << "    #pragma unroll\n    for (int j = 0; j < " << BX << " * BK / 1024; j++) {\n";
-      l << "      const int r = tid / 4 + 64 * j, kq = (tid % 4) * 4;\n";
+      l << "    #pragma unroll\n    for (int j = 0; j < " << BX << " * BK / (4 * NT); j++) {\n";
+      l << "      const int idx = tid + NT * j, r = idx / (BK / 4), kq = (idx % (BK / 4)) * 4;\n";
       l << "      #pragma unroll\n      for (int q = 0; q < 4; q++) " << S << "[buf][kq + q][r] = r" << X << "[4*j+q];\n    }\n";
     } else if (md == 1) {
-      l << "    #pragma unroll\n    for (int j = 0; j < " << BX << " * BK / 1024; j++) {\n";
-      l << "      const int kk = tid / (" << BX << " / 4) + (256 / (" << BX << " / 4)) * j, r = (tid % (" << BX
-        << " / 4)) * 4;\n";
+      l << "    #pragma unroll\n    for (int j = 0; j < " << BX << " * BK / (4 * NT); j++) {\n";
+      l << "      const int idx = tid + NT * j, kk = idx / (" << BX << " / 4), r = (idx % (" << BX << " / 4)) * 4;\n";
       l << "      *(float4*)(&" << S << "[buf][kk][r]) = make_float4(r" << X << "[4*j], r" << X << "[4*j+1], r" << X
         << "[4*j+2], r" << X << "[4*j+3]);\n    }\n";
     } else {
-      l << "    #pragma unroll\n    for (int e = 0; e < " << BX << " * BK / 256; e++) {\n";
-      if (k_fast) l << "      const int i = tid + 256 * e, r = i / BK, kk = i % BK;\n";
-      else l << "      const int i = tid + 256 * e, kk = i / " << BX << ", r = i % " << BX << ";\n";
+      l << "    #pragma unroll\n    for (int e = 0; e < " << BX << " * BK / NT; e++) {\n";
+      if (k_fast) l << "      const int i = tid + NT * e, r = i / BK, kk = i % BK;\n";
+      else l << "      const int i = tid + NT * e, kk = i / " << BX << ", r = i % " << BX << ";\n";
       l << "      " << S << "[buf][kk][r] = r" << X << "[e];\n    }\n";
     }
     l << "  };\n";
@@ -1260,7 +1271,7 @@ RenderedKernel render_gemm(const KernelInfo& ki, const GemmMatch& g, const std::
   rk.name = name;
   rk.kind = kernel_class_name(KernelClass::Gemm);
   rk.source = s.str();
-  rk.block[0] = 256;
+  rk.block[0] = static_cast<unsigned>(NT);
   rk.grid[0] = static_cast<unsigned>(((M + BM - 1) / BM) * ((N + BN - 1) / BN));
   return rk;
 }

@@ -149,7 +149,11 @@ def test_c1_row_reduce(fg, cpu, shape):
     assert rel_err_bound(got, want, scale, 1e-4) <= 1.0
 
 
-@pytest.mark.parametrize("mnk", [(64, 64, 64), (256, 128, 784), (128, 10, 128), (512, 512, 512), (100, 70, 30)])
+# Shapes cover each GEMM tile path: 64/128-wide tiles, 256x128 and 128x256
+# (BK 8) and 256x256 (BK 16, 8 waves), with ragged M/N edges and K not a
+# multiple of the k-tile.
+@pytest.mark.parametrize("mnk", [(64, 64, 64), (256, 128, 784), (128, 10, 128), (512, 512, 512), (100, 70, 30),
+                                 (4100, 4000, 100), (4096, 2100, 72), (2100, 4096, 40)])
 def test_c3_linear_forward(fg, cpu, mnk):
     m, n, k = mnk
     r = seeded(5)
