@@ -58,6 +58,8 @@ def _declare(l: ctypes.CDLL) -> None:
         "fg_tensor_zeros": (c_int, [c_int, c_int, i64p, c_int, PP]),
         "fg_tensor_ones": (c_int, [c_int, c_int, i64p, c_int, PP]),
         "fg_tensor_free": (c_int, [P]),
+        "fg_idx_images": (c_int, [ctypes.c_char_p, c_int, PP]),
+        "fg_idx_labels": (c_int, [ctypes.c_char_p, P, c_size, ctypes.POINTER(c_size)]),
         "fg_tensor_unary": (c_int, [P, c_int, PP]),
         "fg_tensor_binary": (c_int, [P, P, c_int, PP]),
         "fg_tensor_reduce": (c_int, [P, c_int, i64p, c_int, PP]),

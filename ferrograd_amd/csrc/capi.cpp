@@ -113,6 +113,22 @@ int fg_tensor_ones(int device, int dtype, const int64_t* shape, int ndim, fg_ten
   return guard([&] { *out = wrap(fg::Tensor::ones(to_shape(shape, ndim), to_dev(device), to_dtype(dtype))); });
 }
 
+int fg_idx_images(const char* path, int device, fg_tensor** out) {
+  return guard([&] { *out = wrap(fg::idx_images(path, to_dev(device))); });
+}
+
+int fg_idx_labels(const char* path, uint8_t* out, size_t capacity, size_t* count) {
+  return guard([&] {
+    std::vector<uint8_t> labels = fg::idx_labels(path);
+    *count = labels.size();
+    if (out) {
+      FG_CHECK(capacity >= labels.size(), "fg_idx_labels: buffer holds " + std::to_string(capacity) + " labels, file has " +
+                                              std::to_string(labels.size()));
+      std::memcpy(out, labels.data(), labels.size());
+    }
+  });
+}
+
 int fg_tensor_free(fg_tensor* t) {
   delete t;
   return 0;

@@ -433,26 +433,31 @@ struct GraphKey {
   std::vector<UOp> order;            // toposort of Sink(roots)
   std::vector<Buffer> leaves;        // distinct buffers, first-visit order
   std::vector<uint64_t> code;        // exact structural serialisation
+  std::vector<uint32_t> scalar_nodes;  // positions of parameterised Shrink starts
   uint64_t hash = 0;
 };
 
 void key_word(GraphKey& k, uint64_t w) { k.code.push_back(w); }
 
-// One depth-first walk yields the toposort (the order UOp::toposort produces:
-// sources first, left to right, except After which walks its effect first)
-// and the serialisation, with one open-addressing map for both the visited
-// set and node positions.
+// A depth-first walk yields the toposort (the order UOp::toposort produces:
+// sources first, left to right, except After which walks its effect first),
+// using one open-addressing map for the visited set and node positions; a
+// second pass serialises it.
+//
+// Integer constants used only as Shrink starts that parameterize turns into
+// ParamScalar kernel arguments (schedule.rs:217-239) are serialised without
+// their value: narrow(0, start, len) over successive batches is then one plan,
+// and replays read the start from the current graph (scalar_nodes).
 GraphKey graph_key(const std::vector<UOp>& roots, bool fuse) {
   GraphKey k;
   const UOp sink = UOp::sink(roots);
   PtrIndexMap pos(1024);
   PtrIndexMap leaf(64);
   k.order.reserve(1024);
-  k.code.reserve(8192);
-  key_word(k, fuse ? 1 : 0);
   std::vector<std::pair<const UOp*, bool>> stack;
   stack.reserve(256);
   stack.emplace_back(&sink, false);
+  bool has_bind = false;
   while (!stack.empty()) {
     auto [np, processed] = stack.back();
     stack.pop_back();
@@ -472,6 +477,30 @@ GraphKey graph_key(const std::vector<UOp>& roots, bool fuse) {
     }
     pos.set(raw, static_cast<uint32_t>(k.order.size()));
     k.order.push_back(*np);
+    has_bind = has_bind || raw->op == Op::Bind;
+  }
+  // Which integer constants are parameterised Shrink starts and nothing else
+  // (1 = such a use seen, 2 = another use seen).
+  std::vector<uint8_t> use(k.order.size(), 0);
+  if (!has_bind) {
+    for (auto& n : k.order) {
+      const auto& srcs = n.srcs();
+      Shape src_shape;
+      bool shrink = n.op() == Op::Shrink && srcs[0].shape_opt(&src_shape);
+      for (size_t j = 0; j < srcs.size(); j++) {
+        if (srcs[j].op() != Op::Const || srcs[j].dtype() != DType::I32()) continue;
+        uint32_t sp = pos.get(srcs[j].get());
+        bool param = shrink && j >= 1 && j - 1 < n.arg().v.size() &&
+                     static_cast<size_t>(n.arg().v[j - 1]) != src_shape[j - 1];
+        use[sp] |= param ? 1 : 2;
+      }
+    }
+  }
+  k.code.reserve(k.order.size() * 8 + 4);
+  key_word(k, fuse ? 1 : 0);
+  for (uint32_t i = 0; i < k.order.size(); i++) {
+    const UOpInner* raw = k.order[i].get();
+    const auto& srcs = raw->srcs;
     const Arg& a = raw->arg;
     key_word(k, static_cast<uint64_t>(raw->op) | (static_cast<uint64_t>(raw->dtype.kind) << 8) |
                     (static_cast<uint64_t>(raw->dtype.vcount) << 16) | (static_cast<uint64_t>(raw->has_tag) << 32) |
@@ -479,6 +508,11 @@ GraphKey graph_key(const std::vector<UOp>& roots, bool fuse) {
     if (raw->has_tag) key_word(k, raw->tag);
     key_word(k, srcs.size());
     for (auto& s : srcs) key_word(k, pos.get(s.get()));
+    if (use[i] == 1) {
+      key_word(k, 0x5354415254ULL);  // a start value supplied per replay
+      k.scalar_nodes.push_back(i);
+      continue;
+    }
     if (a.kind == Arg::Kind::Buffer) {
       const Buffer& b = a.buf;
       if (!b) {
@@ -515,7 +549,7 @@ GraphKey graph_key(const std::vector<UOp>& roots, bool fuse) {
 }
 
 struct PlanArg {
-  enum Kind : uint8_t { Leaf, Output, Value } kind = Value;
+  enum Kind : uint8_t { Leaf, Output, Value, Start } kind = Value;
   uint32_t index = 0;
   KernelArg value;
 };
@@ -599,6 +633,15 @@ std::shared_ptr<CachedPlan> record_plan(const GraphKey& k, const SchedulePlan& p
         }
       } else {
         pa.value = in;
+        if (in.kind == KernelArg::Kind::I32) {
+          // A Shrink start: bind it to the start node (interning makes the
+          // constant node of a value unique) so replays read the new value.
+          for (uint32_t p : k.scalar_nodes)
+            if (k.order[p].arg().a == in.i) {
+              pa.kind = PlanArg::Start;
+              pa.index = p;
+            }
+        }
       }
       pk.args.push_back(std::move(pa));
     }
@@ -647,6 +690,10 @@ void replay_plan(Device& backend, const GraphKey& k, const CachedPlan& plan) {
     for (auto& pa : pk.args) {
       if (pa.kind == PlanArg::Value) {
         args.push_back(pa.value);
+        continue;
+      }
+      if (pa.kind == PlanArg::Start) {
+        args.push_back(KernelArg::i32(static_cast<int32_t>(k.order[pa.index].arg().a)));
         continue;
       }
       const Buffer& b = pa.kind == PlanArg::Leaf ? k.leaves[pa.index] : outs[pa.index];

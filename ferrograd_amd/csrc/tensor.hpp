@@ -4,6 +4,7 @@
 
 #include <memory>
 #include <optional>
+#include <string>
 #include <vector>
 
 #include "device.hpp"
@@ -124,6 +125,11 @@ struct Sgd {
   void zero_grad() const;
   void step() const;
 };
+
+// Offline MNIST IDX files (dataset.rs:116-161): images as f32 [count, 784]
+// scaled by 1/255 on `dev`, labels as bytes.
+Tensor idx_images(const std::string& path, DeviceId dev);
+std::vector<uint8_t> idx_labels(const std::string& path);
 
 // Per-process statistics used by tests and the benchmark.
 struct RealizeStats {

@@ -69,3 +69,66 @@ def mlp_setup(fg, device, batch: int, dims: Sequence[int], lr: float = 0.01, see
         return loss.to_vec()[0]
 
     return step, model
+
+
+def predictions(logits: np.ndarray) -> np.ndarray:
+    """Index of the largest logit per row; among equal maxima the last one, as
+    Iterator::max_by in examples/mnist.rs:108-114 returns."""
+    flipped = logits[:, ::-1]
+    return logits.shape[1] - 1 - np.argmax(flipped, axis=1)
+
+
+def train_mnist(dataset, device="hip", epochs: int = 5, batch_size: int = 256, lr: float = 0.01,
+                max_batches: int | None = None, log=print) -> dict:
+    """examples/mnist.rs:59-126 on `device`: Linear(784,128) -> ReLU ->
+    Linear(128,10), cross-entropy, SGD; batches are narrow()ed views of the
+    resident training set. Returns per-batch losses and per-epoch average loss
+    and test accuracy (percent)."""
+    train_targets = Tensor.new(one_hot(dataset.train_labels, dataset.num_classes),
+                               [dataset.train_len(), dataset.num_classes], device)
+    model = Mlp((784, 128, 10), device)
+    opt = Sgd(model.parameters(), lr)
+    num_batches = dataset.train_len() // batch_size
+    if max_batches is None:
+        import os
+
+        max_batches = int(os.environ.get("MAX_BATCHES", num_batches))
+    runs = min(max_batches, num_batches)
+    history = {"batch_loss": [], "epoch_loss": [], "accuracy": []}
+    for epoch in range(epochs):
+        epoch_loss = np.float32(0.0)
+        for b in range(runs):
+            start = b * batch_size
+            x = dataset.train_images.narrow(0, start, batch_size)
+            t = train_targets.narrow(0, start, batch_size)
+            loss = model.forward(x).cross_entropy(t)
+            opt.zero_grad()
+            loss.backward()
+            opt.step()
+            v = loss.to_vec()[0]
+            epoch_loss = np.float32(epoch_loss + np.float32(v))
+            history["batch_loss"].append(v)
+            if log:
+                log(f"  epoch {epoch} batch {b:>4}/{num_batches}  loss={v:.4f}")
+        avg = float(epoch_loss / np.float32(runs))
+        logits = model.forward(dataset.test_images).numpy().reshape(dataset.test_len(), dataset.num_classes)
+        acc = float(np.float32(np.sum(predictions(logits) == dataset.test_labels)) / np.float32(dataset.test_len())
+                    * np.float32(100.0))
+        history["epoch_loss"].append(avg)
+        history["accuracy"].append(acc)
+        if log:
+            log(f"Epoch {epoch}: avg_loss={avg:.4f}, test_accuracy={acc:.1f}%")
+    return history
+
+
+if __name__ == "__main__":
+    import argparse
+
+    from .dataset import MNISTDataset
+
+    ap = argparse.ArgumentParser(description="Train the examples/mnist.rs MLP on local IDX files")
+    ap.add_argument("--data", default="data/mnist")
+    ap.add_argument("--device", default="hip")
+    ap.add_argument("--epochs", type=int, default=5)
+    a = ap.parse_args()
+    train_mnist(MNISTDataset.load(a.data, a.device), a.device, epochs=a.epochs)

@@ -44,6 +44,15 @@ int fg_tensor_zeros(int device, int dtype, const int64_t* shape, int ndim, fg_te
 int fg_tensor_ones(int device, int dtype, const int64_t* shape, int ndim, fg_tensor** out);
 int fg_tensor_free(fg_tensor* t);
 
+/* Offline MNIST IDX files (dataset.rs:116-161; no download). Images: magic
+ * 2051, big-endian u32 count/rows/cols (28x28 required), u8 pixels -> f32
+ * [count, 784] scaled by 1/255 on `device`. Labels: magic 2049, u32 count, u8
+ * labels; call with out == NULL to get the count, then with a buffer of at
+ * least that many bytes. Errors carry the reference's messages ("bad IDX
+ * format: expected IDX image magic 2051, got N", "io: ..."). */
+int fg_idx_images(const char* path, int device, fg_tensor** out);
+int fg_idx_labels(const char* path, uint8_t* out, size_t capacity, size_t* count);
+
 /* Lazy ops (tensor.rs:442-778). */
 int fg_tensor_unary(fg_tensor* t, int op, fg_tensor** out);
 int fg_tensor_binary(fg_tensor* a, fg_tensor* b, int op, fg_tensor** out);

@@ -87,10 +87,20 @@ def test_new_leaf_values_replay_with_new_buffers(fg, cpu, fresh_plans):
     assert fg.plan_stats()["hits"] >= 2
 
 
-def test_literal_values_are_part_of_the_key(fg, cpu, fresh_plans):
-    x = fg.Tensor.new(np.arange(6, dtype=np.float32), [6], cpu)
-    assert x.narrow(0, 1, 2).contiguous().to_vec() == [1.0, 2.0]
-    assert x.narrow(0, 3, 2).contiguous().to_vec() == [3.0, 4.0]
+def test_narrow_starts_replay_as_kernel_scalars(fg, cpu, fresh_plans):
+    # Shrink starts become ParamScalar arguments (schedule.rs:217-239): one
+    # plan serves every batch offset and each replay passes the new start.
+    x = fg.Tensor.new(np.arange(12, dtype=np.float32).reshape(6, 2), [6, 2], cpu)
+    before = fg.plan_stats()["hits"]
+    got = [x.narrow(0, s, 2).mul(fg.Tensor.scalar(2.0, cpu)).to_vec() for s in (0, 1, 3, 4)]
+    assert got == [[0.0, 2.0, 4.0, 6.0], [4.0, 6.0, 8.0, 10.0], [12.0, 14.0, 16.0, 18.0], [16.0, 18.0, 20.0, 22.0]]
+    assert fg.plan_stats()["hits"] - before >= 2
+
+
+def test_same_inputs_different_ops_select_different_plans(fg, cpu, fresh_plans):
+    x = fg.Tensor.new(np.arange(4, dtype=np.float32), [4], cpu)
+    assert x.add(x).exp2().to_vec() == [1.0, 4.0, 16.0, 64.0]
+    assert x.add(x).log2().to_vec()[1:] == [1.0, 2.0, np.log2(6.0).astype(np.float32)]
 
 
 def test_disabling_drops_recorded_plans(fg, cpu, fresh_plans):
