@@ -1134,8 +1134,12 @@ RenderedKernel render_gemm(const KernelInfo& ki, const GemmMatch& g, const std::
   s << "#define BM " << BM << "\n#define BN " << BN << "\n#define BK " << BK << "\n#define PAD " << PAD << "\n";
   s << "#define NT " << NT << "\n#define WGN " << WGN << "\n";
   s << signature(ki, name, NT) << " {\n";
-  s << R"(  __shared__ float As[2][BK][BM + PAD];
-  __shared__ float Bs[2][BK][BN + PAD];
+  s << R"(  // One LDS block: the double-buffered operand stages during the K loop,
+  // then per-wave 32x32 staging tiles for the epilogue.
+  constexpr int SA = 2 * BK * (BM + PAD), SB = 2 * BK * (BN + PAD), EPS = 36, SE = (NT / 64) * 32 * EPS;
+  __shared__ __attribute__((aligned(16))) float smem[(SA + SB) > SE ? (SA + SB) : SE];
+  float (*As)[BK][BM + PAD] = reinterpret_cast<float (*)[BK][BM + PAD]>(smem);
+  float (*Bs)[BK][BN + PAD] = reinterpret_cast<float (*)[BK][BN + PAD]>(smem + SA);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int nbm = (M_ + BM - 1) / BM, nbn = (N_ + BN - 1) / BN, nb = nbm * nbn;
   int bid = blockIdx.x;
@@ -1261,33 +1265,70 @@ RenderedKernel render_gemm(const KernelInfo& ki, const GemmMatch& g, const std::
     if (kt + 1 < KT) { store_a(cur ^ 1); store_b(cur ^ 1); }
     __syncthreads();
   }
-  // 32x32 accumulator layout: element e of lane l is row 8*(e/4) + 4*(l/32) + e%4, column l%32.
+  // Epilogue: each wave stages one 32x32 accumulator tile at a time in its own
+  // LDS tile (32x32 layout: element e of lane l is row 8*(e/4) + 4*(l/32) +
+  // e%4, column l%32), then reads it back as rows of float4, 8 lanes per row,
+  // so epilogue operands load and outputs store 16 bytes per lane.
+  float* wst = smem + wave * (32 * EPS);
   #pragma unroll
   for (int i = 0; i < TM; i++)
     #pragma unroll
-    for (int j = 0; j < TN; j++)
+    for (int j = 0; j < TN; j++) {
       #pragma unroll
-      for (int e = 0; e < 16; e++) {
-        const int grow = m0 + wm + i * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
-        const int gcol = n0 + wn + j * 32 + (lane & 31);
+      for (int e = 0; e < 16; e++) wst[(8 * (e >> 2) + 4 * (lane >> 5) + (e & 3)) * EPS + (lane & 31)] = acc[i][j][e];
+      __syncthreads();
+      #pragma unroll
+      for (int q = 0; q < 4; q++) {
+        const int rr = (lane >> 3) + 8 * q, cc = (lane & 7) * 4;
+        const fg_f4 gv = *(const fg_f4*)(wst + rr * EPS + cc);
+        const int grow = m0 + wm + i * 32 + rr, gcol = n0 + wn + j * 32 + cc;
         if (grow < M_ && gcol < N_) {
-          const float gacc = acc[i][j][e];
 )";
-  // Epilogue: everything outside the reduction, per output element.
+  // Everything outside the reduction, for the four columns gcol..gcol+3.
+  static const char* kComp[4] = {"gv.x", "gv.y", "gv.z", "gv.w"};
   Emitter em;
   em.define_range(g.rm, "grow");
-  em.define_range(g.rn, "gcol");
-  em.reduce_cb_ = [&](const UOp& RR, int lane) -> std::string {
-    FG_CHECK(RR == g.R, "gemm epilogue sees one reduction");
-    (void)lane;
-    return "gacc";
-  };
-  std::string v = em.val(ki.value, 0);
-  em.line(pname(ki.out_param) + "[" + em.idx(ki.out_index, 0) + "] = " + v + ";");
+  const std::string out = pname(ki.out_param);
+  if (N % 4 == 0) {
+    // Every column group lies inside the tile: lanes along the columns.
+    em.define_range(g.rn, "gcol");
+    em.set_lane_range(g.rn, 4);
+    em.reduce_cb_ = [&](const UOp& RR, int lane) -> std::string {
+      FG_CHECK(RR == g.R, "gemm epilogue sees one reduction");
+      return kComp[lane];
+    };
+    std::vector<std::string> vals;
+    for (int u = 0; u < 4; u++) vals.push_back(em.val(ki.value, u));
+    Affine ao = affine_of(ki.out_index);
+    bool vstore = ao.ok && !ao.has_scalar_terms() && ao.coef(g.rn) == 1 && ao.c0 % 4 == 0 &&
+                  ki.out_param.dtype().kind == DTypeKind::F32;
+    for (auto& t : ao.terms)
+      if (t.first != g.rn && t.second % 4 != 0) vstore = false;
+    if (vstore) {
+      em.line("*(float4*)(" + out + "+" + em.idx(ki.out_index, 0) + ") = make_float4(" + vals[0] + ", " + vals[1] +
+              ", " + vals[2] + ", " + vals[3] + ");");
+    } else {
+      for (int u = 0; u < 4; u++) em.line(out + "[" + em.idx(ki.out_index, u) + "] = " + vals[u] + ";");
+    }
+  } else {
+    // Ragged last column group: one guarded column at a time.
+    for (int u = 0; u < 4; u++) {
+      const std::string col = "(gcol+" + std::to_string(u) + ")";
+      em.open_scope("if (" + col + " < N_) {", "}");
+      em.define_range(g.rn, col);
+      em.reduce_cb_ = [&, u](const UOp& RR, int) -> std::string {
+        FG_CHECK(RR == g.R, "gemm epilogue sees one reduction");
+        return kComp[u];
+      };
+      std::string v = em.val(ki.value, 0);
+      em.line(out + "[" + em.idx(ki.out_index, 0) + "] = " + v + ";");
+      em.close_scope();
+    }
+  }
   std::istringstream is(em.code());
   std::string l;
   while (std::getline(is, l)) s << "        " << l << "\n";
-  s << "        }\n      }\n}\n";
+  s << "        }\n      }\n      __syncthreads();\n    }\n}\n";
   RenderedKernel rk;
   rk.name = name;
   rk.kind = kernel_class_name(KernelClass::Gemm);
