@@ -373,6 +373,14 @@ class Emitter {
       default: break;
     }
     size_t si = scope_of(n);
+    if (n.op() == Op::Load && load_cb_) {
+      // A load whose value the caller already holds (e.g. in a register).
+      std::string held = load_cb_(n, lane);
+      if (!held.empty()) {
+        remember(si, key, held);
+        return held;
+      }
+    }
     if (n.op() == Op::Load) {
       const UOp& ix = n.src(0);
       FG_CHECK(ix.op() == Op::Index, "Load must read through Index");
@@ -438,6 +446,8 @@ class Emitter {
   size_t depth() const { return scopes_.size(); }
 
   std::function<std::string(const UOp&, int)> reduce_cb_;
+  // Optional: returns the expression holding a load's value (empty: emit the load).
+  std::function<std::string(const UOp&, int)> load_cb_;
 
  private:
   static bool is_index_expr(const UOp& n) {
@@ -1075,6 +1085,66 @@ bool gemm_operand(const UOp& e, const UOp& rk, const KernelInfo& ki, GemmOperand
   return true;
 }
 
+// Workgroup tile of the fp32 MFMA GEMM and the number of K splits.
+struct GemmTile {
+  int BM = 128, BN = 128, BK = 16, WGM = 2, WGN = 2;
+  int64_t S = 1;   // K splits (partials summed by a second pass)
+  int64_t KC = 0;  // K per split, a multiple of BK
+  int nt() const { return 64 * WGM * WGN; }
+};
+
+constexpr int64_t kComputeUnits = 256;  // MI355X
+constexpr int64_t kMinSplitK = 64;      // shortest K range a split workgroup runs
+
+// Tile shape (measured on MI355X, fp32 4096^3: 256x256/BK16/8 waves 131
+// TFLOP/s, 256x128/BK8/4 waves 128, 128x128/BK16/4 waves 114): the largest
+// tile that still gives every CU a tile. When no shape does, the largest tile
+// that wastes at most 15% of its area on padding and can fill half the chip
+// once K is split, else 64-wide tiles; a side of at most 32 gets a 32-wide
+// tile. The K range is then split over workgroups until the grid fills the
+// resident slots (one 8-wave or two 4-wave workgroups per CU).
+GemmTile choose_gemm_tile(int64_t M, int64_t N, int64_t K) {
+  auto tiles = [&](int64_t bm, int64_t bn) { return ((M + bm - 1) / bm) * ((N + bn - 1) / bn); };
+  auto waste = [&](int64_t bm, int64_t bn) {
+    return static_cast<double>((M + bm - 1) / bm * bm) * static_cast<double>((N + bn - 1) / bn * bn) /
+           (static_cast<double>(M) * static_cast<double>(N));
+  };
+  auto slots = [](const GemmTile& t) { return kComputeUnits * (t.nt() <= 256 ? 2 : 1); };
+  const int64_t smax = std::max<int64_t>(1, K / kMinSplitK);
+  const GemmTile big[4] = {{256, 256, 16, 4, 2}, {256, 128, 8, 2, 2}, {128, 256, 8, 2, 2}, {128, 128, 16, 2, 2}};
+  GemmTile t;
+  bool chosen = false;
+  if (M <= 32 || N <= 32) {
+    auto side = [](int64_t ext, int* b, int* w) {
+      if (ext <= 32) { *b = 32; *w = 1; }
+      else if (ext >= 256) { *b = 256; *w = 4; }
+      else if (ext >= 128) { *b = 128; *w = 2; }
+      else { *b = 64; *w = 1; }
+    };
+    side(M, &t.BM, &t.WGM);
+    side(N, &t.BN, &t.WGN);
+    t.BK = 16;
+    chosen = true;
+  }
+  for (int i = 0; i < 4 && !chosen; i++)
+    if (M >= big[i].BM && N >= big[i].BN && tiles(big[i].BM, big[i].BN) >= kComputeUnits) {
+      t = big[i];
+      chosen = true;
+    }
+  for (int i = 0; i < 4 && !chosen; i++)
+    if (M >= big[i].BM && N >= big[i].BN && waste(big[i].BM, big[i].BN) <= 1.15 &&
+        tiles(big[i].BM, big[i].BN) * smax * 2 >= slots(big[i])) {
+      t = big[i];
+      chosen = true;
+    }
+  if (!chosen) t = {64, 64, 16, 2, 2};
+  const int64_t nt = tiles(t.BM, t.BN);
+  if (nt < kComputeUnits) t.S = std::max<int64_t>(1, std::min(slots(t) / nt, smax));
+  t.KC = ((K + t.S - 1) / t.S + t.BK - 1) / t.BK * t.BK;
+  t.S = (K + t.KC - 1) / t.KC;
+  return t;
+}
+
 bool match_gemm(const KernelInfo& ki, GemmMatch* g) {
   if (ki.reduces.size() != 1 || ki.out_ranges.size() != 2) return false;
   const UOp& R = ki.reduces[0];
@@ -1100,40 +1170,38 @@ bool match_gemm(const KernelInfo& ki, GemmMatch* g) {
   g->M = range_extent(g->rm);
   g->N = range_extent(g->rn);
   g->K = range_extent(rk);
-  if (g->M < 16 || g->N < 16 || g->M * g->N * g->K < (1LL << 18)) return false;
+  if (std::min(g->M, g->N) < 8 || g->M * g->N * g->K < (1LL << 18)) return false;
+  if (g->M <= 32 || g->N <= 32) {
+    // A narrow product pays for a 32-wide MFMA tile only when the grid fills
+    // the chip; otherwise the row and column reductions serve it better.
+    GemmTile t = choose_gemm_tile(g->M, g->N, g->K);
+    if (((g->M + t.BM - 1) / t.BM) * ((g->N + t.BN - 1) / t.BN) * t.S < 128) return false;
+  }
   return true;
 }
 
 RenderedKernel render_gemm(const KernelInfo& ki, const GemmMatch& g, const std::string& name) {
   const int64_t M = g.M, N = g.N, K = g.K;
-  // Tile shape (measured on MI355X, fp32 4096^3: 256x256/BK16/8 waves 131
-  // TFLOP/s, 256x128/BK8/4 waves 128, 128x128/BK16/4 waves 114): the largest
-  // tile that still gives every CU a tile, else the previous 128/64 shapes.
-  auto tiles = [&](int64_t bm, int64_t bn) { return ((M + bm - 1) / bm) * ((N + bn - 1) / bn); };
-  int BM = 128, BN = 128, BK = 16, WGM = 2, WGN = 2;
-  if (M >= 256 && N >= 256 && tiles(256, 256) >= 256) {
-    BM = 256; BN = 256; BK = 16; WGM = 4; WGN = 2;
-  } else if (M >= 256 && N >= 128 && tiles(256, 128) >= 256) {
-    BM = 256; BN = 128; BK = 8;
-  } else if (M >= 128 && N >= 256 && tiles(128, 256) >= 256) {
-    BM = 128; BN = 256; BK = 8;
-  } else if (tiles(128, 128) < 256) {
-    BM = M >= 128 && (M + 63) / 64 * ((N + 63) / 64) < 128 ? 128 : 64;
-    BN = 64;
-  }
-  if (N <= 64) BN = 64;
-  if (M <= 64) BM = 64;
-  const int NT = 64 * WGM * WGN;
+  const GemmTile tile = choose_gemm_tile(M, N, K);
+  const int BM = tile.BM, BN = tile.BN, BK = tile.BK, WGM = tile.WGM, WGN = tile.WGN, NT = tile.nt();
+  const int64_t S = tile.S, KC = tile.KC, NP = (N + 3) / 4 * 4;
+  const int64_t ntiles = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
   const int PAD = 4;  // keeps LDS rows 16-byte aligned for float4 stores
-  FG_CHECK(BM % (32 * WGM) == 0 && BN % (32 * WGN) == 0 && BM * BK % (4 * NT) == 0 && BN * BK % (4 * NT) == 0,
-           "gemm tile shape does not fit the wave grid");
+  FG_CHECK(BM % (32 * WGM) == 0 && BN % (32 * WGN) == 0, "gemm tile shape does not fit the wave grid");
+  const std::string scratch_param = S > 1 ? ", float* __restrict__ fg_scratch" : "";
+  auto sig = [&](const std::string& fn, int block) {
+    std::string s = signature(ki, fn, block);
+    return s.substr(0, s.size() - 1) + scratch_param + ")";
+  };
+  const std::string main_name = S > 1 ? name + "_part" : name;
 
   std::ostringstream s;
   s << kPrelude;
-  s << "#define M_ " << M << "\n#define N_ " << N << "\n#define K_ " << K << "\n";
+  s << "#define M_ " << M << "\n#define N_ " << N << "\n#define K_ " << K << "\n#define NP_ " << NP << "\n";
+  s << "#define S_ " << S << "\n#define KC_ " << KC << "\n#define NTILES_ " << ntiles << "\n";
   s << "#define BM " << BM << "\n#define BN " << BN << "\n#define BK " << BK << "\n#define PAD " << PAD << "\n";
   s << "#define NT " << NT << "\n#define WGN " << WGN << "\n";
-  s << signature(ki, name, NT) << " {\n";
+  s << sig(main_name, NT) << " {\n";
   s << R"(  // One LDS block: the double-buffered operand stages during the K loop,
   // then per-wave 32x32 staging tiles for the epilogue.
   constexpr int SA = 2 * BK * (BM + PAD), SB = 2 * BK * (BN + PAD), EPS = 36, SE = (NT / 64) * 32 * EPS;
@@ -1141,11 +1209,19 @@ RenderedKernel render_gemm(const KernelInfo& ki, const GemmMatch& g, const std::
   float (*As)[BK][BM + PAD] = reinterpret_cast<float (*)[BK][BM + PAD]>(smem);
   float (*Bs)[BK][BN + PAD] = reinterpret_cast<float (*)[BK][BN + PAD]>(smem + SA);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int nbm = (M_ + BM - 1) / BM, nbn = (N_ + BN - 1) / BN, nb = nbm * nbn;
+  const int nbm = (M_ + BM - 1) / BM, nbn = (N_ + BN - 1) / BN;
   int bid = blockIdx.x;
   // Blocks are dispatched round-robin over the 8 XCDs; give each XCD a
-  // contiguous run of tiles so neighbouring tiles share its L2.
-  if (nb % 8 == 0) bid = (bid % 8) * (nb / 8) + bid / 8;
+  // contiguous run of (split, tile) pairs so neighbouring tiles of one K
+  // range share its L2.
+  if ((NTILES_ * S_) % 8 == 0) bid = (bid % 8) * (NTILES_ * S_ / 8) + bid / 8;
+#if S_ > 1
+  const int ks = bid / NTILES_;
+  bid = bid % NTILES_;
+  const int kbeg = ks * KC_, kend = (kbeg + KC_ < K_) ? kbeg + KC_ : K_;
+#else
+  constexpr int kbeg = 0, kend = K_;
+#endif
   const int GM = 8;
   const int group = bid / (GM * nbn), first_m = group * GM;
   const int gsz = (nbm - first_m) < GM ? (nbm - first_m) : GM;
@@ -1161,93 +1237,118 @@ RenderedKernel render_gemm(const KernelInfo& ki, const GemmMatch& g, const std::
     for (int j = 0; j < TN; j++)
       #pragma unroll
       for (int e = 0; e < 16; e++) acc[i][j][e] = 0.0f;
-  constexpr int AE = BM * BK / NT, BE = BN * BK / NT;  // elements per thread per stage
-  float ra[AE], rb[BE];
 )";
   // Global -> register loaders. Staging modes: 0 = 4 consecutive k per thread
   // (unit stride along k: 16-byte loads), 1 = 4 consecutive rows per thread
-  // (unit stride along m/n), 2 = one element at a time. The operand expression
-  // is rendered per element group by the emitter, vectorising unit-stride loads.
+  // (unit stride along m/n), 2 = one element at a time. A stage holds BX*BK
+  // elements; when the threads outnumber its groups the extra threads idle.
+  // load_X only issues the operand's raw loads into registers; store_X
+  // evaluates the operand expression (relu recompute, masks) on them when it
+  // writes the stage to LDS, after the MFMAs of the current stage, so the loads
+  // stay in flight under the MFMAs.
   auto loader = [&](const char* X, const GemmOperand& op, int BX, int64_t ext, const char* dim) {
     int64_t so = op.lead.coef(op.rout), sk = op.lead.coef(g.rk);
     int md = 2;
     if (sk == 1 && K % 4 == 0) md = 0;
     else if (so == 1 && ext % 4 == 0) md = 1;
     bool k_fast = std::llabs(sk) <= std::llabs(so);  // mode 2 mapping
-    auto body = [&](const std::string& dst, int lanes_along_k, int lanes_along_r) {
-      Emitter em;
+    const int groups = md == 2 ? BX * BK : BX * BK / 4;
+    const int per = (groups + NT - 1) / NT;
+    const int V = md == 2 ? 1 : 4;
+    const std::string guard = groups % NT == 0 ? "" : "idx < " + std::to_string(groups) + " && ";
+    const std::vector<UOp> lds = loads_in(op.expr);
+    auto reg = [&](size_t i, const std::string& slot) { return "r" + std::string(X) + std::to_string(i) + "[" + slot + "]"; };
+    auto slot = [&](int u) { return V == 1 ? std::string("j") : "4*j+" + std::to_string(u); };
+    auto coords = [&]() {
+      std::ostringstream c;
+      c << "      const int idx = tid + NT * j;\n";
+      if (md == 0) c << "      const int r = idx / (BK / 4), kk = (idx % (BK / 4)) * 4;\n";
+      else if (md == 1) c << "      const int kk = idx / (" << BX << " / 4), r = (idx % (" << BX << " / 4)) * 4;\n";
+      else if (k_fast) c << "      const int r = idx / BK, kk = idx % BK;\n";
+      else c << "      const int kk = idx / " << BX << ", r = idx % " << BX << ";\n";
+      c << "      const int gr = " << dim << "0 + r, gk = k0 + kk;\n";
+      c << "      const bool in = " << guard << "gr < " << ext << " && gk < kend;\n";
+      return c.str();
+    };
+    auto setup = [&](Emitter& em) {
       em.define_range(op.rout, "gr");
       em.define_range(g.rk, "gk");
-      int V = 1;
-      if (lanes_along_k) {
-        em.set_lane_range(g.rk, 4);
-        V = 4;
-      } else if (lanes_along_r) {
-        em.set_lane_range(op.rout, 4);
-        V = 4;
-      }
-      std::vector<std::string> vals;
-      for (int u = 0; u < V; u++) vals.push_back(em.val(op.expr, u));
-      std::ostringstream b;
-      std::istringstream is(em.code());
+      if (md == 0) em.set_lane_range(g.rk, 4);
+      else if (md == 1) em.set_lane_range(op.rout, 4);
+    };
+    auto indent = [](const std::string& code, const char* pre) {
+      std::ostringstream o;
+      std::istringstream is(code);
       std::string ln;
-      while (std::getline(is, ln)) b << "        " << ln << "\n";
-      for (int u = 0; u < V; u++) b << "        " << dst << (V > 1 ? "[" + std::to_string(u) + "]" : "") << " = " << vals[u] << ";\n";
-      return b.str();
+      while (std::getline(is, ln)) o << pre << ln << "\n";
+      return o.str();
     };
     std::ostringstream l;
+    for (size_t i = 0; i < lds.size(); i++)
+      l << "  " << ctype(lds[i].dtype()) << " r" << X << i << "[" << per * V << "];\n";
     l << "  auto load_" << X << " = [&](int k0) {\n";
-    if (md == 0 || md == 1) {
-      l << "    #pragma unroll\n    for (int j = 0; j < " << BX << " * BK / (4 * NT); j++) {\n";
-      l << "      const int idx = tid + NT * j;\n";
-      if (md == 0) {
-        l << "      const int r = idx / (BK / 4), kq = (idx % (BK / 4)) * 4;\n";
-        l << "      const int gr = " << dim << "0 + r, gk = k0 + kq;\n";
+    l << "    #pragma unroll\n    for (int j = 0; j < " << per << "; j++) {\n" << coords();
+    {
+      Emitter em;
+      setup(em);
+      std::ostringstream body;
+      for (size_t i = 0; i < lds.size(); i++)
+        for (int u = 0; u < V; u++) {
+          std::string v = em.val(lds[i], u);
+          body << reg(i, slot(u)) << " = " << v << ";\n";
+        }
+      // Defined on both paths: no register carries a value across stages.
+      for (size_t i = 0; i < lds.size(); i++)
+        for (int u = 0; u < V; u++) l << "      " << reg(i, slot(u)) << " = 0;\n";
+      l << "      if (in) {\n" << indent(em.code() + body.str(), "        ") << "      }\n";
+    }
+    l << "    }\n  };\n";
+    const char* SX = X[0] == 'a' ? "As" : "Bs";
+    l << "  auto store_" << X << " = [&](int buf, int k0) {\n";
+    l << "    #pragma unroll\n    for (int j = 0; j < " << per << "; j++) {\n" << coords();
+    {
+      Emitter em;
+      setup(em);
+      em.load_cb_ = [&](const UOp& ld, int u) -> std::string {
+        for (size_t i = 0; i < lds.size(); i++)
+          if (lds[i] == ld) return reg(i, slot(u));
+        return std::string();
+      };
+      std::vector<std::string> vals;
+      for (int u = 0; u < V; u++) vals.push_back(em.val(op.expr, u));
+      std::ostringstream body;
+      for (int u = 0; u < V; u++) body << "v[" << u << "] = " << vals[u] << ";\n";
+      l << "      float v[" << V << "];\n";
+      if (op.expr.op() == Op::Load && op.expr.dtype() == DType::F32()) {
+        // A bare f32 load: its registers already hold 0 outside the operand.
+        l << indent(em.code() + body.str(), "      ");
       } else {
-        l << "      const int kk = idx / (" << BX << " / 4), r = (idx % (" << BX << " / 4)) * 4;\n";
-        l << "      const int gr = " << dim << "0 + r, gk = k0 + kk;\n";
+        l << "      if (in) {\n" << indent(em.code() + body.str(), "        ") << "      } else {\n";
+        for (int u = 0; u < V; u++) l << "        v[" << u << "] = 0.0f;\n";
+        l << "      }\n";
       }
-      l << "      float* dst = &r" << X << "[4*j];\n";
-      l << "      if (gr < " << ext << " && gk < K_) {\n" << body("dst", md == 0, md == 1) << "      } else {\n";
-      l << "        dst[0] = 0.0f; dst[1] = 0.0f; dst[2] = 0.0f; dst[3] = 0.0f;\n      }\n    }\n";
-    } else {
-      l << "    #pragma unroll\n    for (int e = 0; e < " << BX << " * BK / NT; e++) {\n";
-      if (k_fast) l << "      const int i = tid + NT * e, r = i / BK, kk = i % BK;\n";
-      else l << "      const int i = tid + NT * e, kk = i / " << BX << ", r = i % " << BX << ";\n";
-      l << "      const int gr = " << dim << "0 + r, gk = k0 + kk;\n";
-      l << "      if (gr < " << ext << " && gk < K_) {\n" << body("r" + std::string(X) + "[e]", 0, 0)
-        << "      } else {\n        r" << X << "[e] = 0.0f;\n      }\n    }\n";
     }
-    l << "  };\n";
-    l << "  auto store_" << X << " = [&](int buf) {\n";
-    const char* S = X[0] == 'a' ? "As" : "Bs";
+    const std::string sguard = groups % NT == 0 ? "" : "if (idx < " + std::to_string(groups) + ") ";
     if (md == 0) {
-      l << "    #pragma unroll\n    for (int j = 0; j < " << BX << " * BK / (4 * NT); j++) {\n";
-      l << "      const int idx = tid + NT * j, r = idx / (BK / 4), kq = (idx % (BK / 4)) * 4;\n";
-      l << "      #pragma unroll\n      for (int q = 0; q < 4; q++) " << S << "[buf][kq + q][r] = r" << X << "[4*j+q];\n    }\n";
+      l << "      " << sguard << "{\n        #pragma unroll\n        for (int q = 0; q < 4; q++) " << SX
+        << "[buf][kk + q][r] = v[q];\n      }\n";
     } else if (md == 1) {
-      l << "    #pragma unroll\n    for (int j = 0; j < " << BX << " * BK / (4 * NT); j++) {\n";
-      l << "      const int idx = tid + NT * j, kk = idx / (" << BX << " / 4), r = (idx % (" << BX << " / 4)) * 4;\n";
-      l << "      *(float4*)(&" << S << "[buf][kk][r]) = make_float4(r" << X << "[4*j], r" << X << "[4*j+1], r" << X
-        << "[4*j+2], r" << X << "[4*j+3]);\n    }\n";
+      l << "      " << sguard << "*(float4*)(&" << SX << "[buf][kk][r]) = make_float4(v[0], v[1], v[2], v[3]);\n";
     } else {
-      l << "    #pragma unroll\n    for (int e = 0; e < " << BX << " * BK / NT; e++) {\n";
-      if (k_fast) l << "      const int i = tid + NT * e, r = i / BK, kk = i % BK;\n";
-      else l << "      const int i = tid + NT * e, kk = i / " << BX << ", r = i % " << BX << ";\n";
-      l << "      " << S << "[buf][kk][r] = r" << X << "[e];\n    }\n";
+      l << "      " << sguard << SX << "[buf][kk][r] = v[0];\n";
     }
-    l << "  };\n";
+    l << "    }\n  };\n";
     return l.str();
   };
   s << loader("a", g.a, BM, M, "m");
   s << loader("b", g.b, BN, N, "n");
-  s << R"(  const int KT = (K_ + BK - 1) / BK;
-  load_a(0); load_b(0);
-  store_a(0); store_b(0);
+  s << R"(  const int KT = (kend - kbeg + BK - 1) / BK;
+  load_a(kbeg); load_b(kbeg);
+  store_a(0, kbeg); store_b(0, kbeg);
   __syncthreads();
   for (int kt = 0; kt < KT; kt++) {
-    const int cur = kt & 1;
-    if (kt + 1 < KT) { load_a((kt + 1) * BK); load_b((kt + 1) * BK); }
+    const int cur = kt & 1, knext = kbeg + (kt + 1) * BK;
+    if (kt + 1 < KT) { load_a(knext); load_b(knext); }
     #pragma unroll
     for (int kk = 0; kk < BK; kk += 2) {
       const int kr = kk + (lane >> 5);
@@ -1262,7 +1363,7 @@ RenderedKernel render_gemm(const KernelInfo& ki, const GemmMatch& g, const std::
         for (int j = 0; j < TN; j++)
           acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[i], bf[j], acc[i][j], 0, 0, 0);
     }
-    if (kt + 1 < KT) { store_a(cur ^ 1); store_b(cur ^ 1); }
+    if (kt + 1 < KT) { store_a(cur ^ 1, knext); store_b(cur ^ 1, knext); }
     __syncthreads();
   }
   // Epilogue: each wave stages one 32x32 accumulator tile at a time in its own
@@ -1284,57 +1385,99 @@ RenderedKernel render_gemm(const KernelInfo& ki, const GemmMatch& g, const std::
         const int grow = m0 + wm + i * 32 + rr, gcol = n0 + wn + j * 32 + cc;
         if (grow < M_ && gcol < N_) {
 )";
-  // Everything outside the reduction, for the four columns gcol..gcol+3.
-  static const char* kComp[4] = {"gv.x", "gv.y", "gv.z", "gv.w"};
-  Emitter em;
-  em.define_range(g.rm, "grow");
-  const std::string out = pname(ki.out_param);
-  if (N % 4 == 0) {
-    // Every column group lies inside the tile: lanes along the columns.
-    em.define_range(g.rn, "gcol");
-    em.set_lane_range(g.rn, 4);
-    em.reduce_cb_ = [&](const UOp& RR, int lane) -> std::string {
-      FG_CHECK(RR == g.R, "gemm epilogue sees one reduction");
-      return kComp[lane];
-    };
-    std::vector<std::string> vals;
-    for (int u = 0; u < 4; u++) vals.push_back(em.val(ki.value, u));
-    Affine ao = affine_of(ki.out_index);
-    bool vstore = ao.ok && !ao.has_scalar_terms() && ao.coef(g.rn) == 1 && ao.c0 % 4 == 0 &&
-                  ki.out_param.dtype().kind == DTypeKind::F32;
-    for (auto& t : ao.terms)
-      if (t.first != g.rn && t.second % 4 != 0) vstore = false;
-    if (vstore) {
-      em.line("*(float4*)(" + out + "+" + em.idx(ki.out_index, 0) + ") = make_float4(" + vals[0] + ", " + vals[1] +
-              ", " + vals[2] + ", " + vals[3] + ");");
-    } else {
-      for (int u = 0; u < 4; u++) em.line(out + "[" + em.idx(ki.out_index, u) + "] = " + vals[u] + ";");
-    }
-  } else {
-    // Ragged last column group: one guarded column at a time.
-    for (int u = 0; u < 4; u++) {
-      const std::string col = "(gcol+" + std::to_string(u) + ")";
-      em.open_scope("if (" + col + " < N_) {", "}");
-      em.define_range(g.rn, col);
-      em.reduce_cb_ = [&, u](const UOp& RR, int) -> std::string {
+  // Everything outside the reduction, for the four columns gcol..gcol+3 of
+  // row grow whose sums are in gv.
+  auto epilogue = [&]() {
+    static const char* kComp[4] = {"gv.x", "gv.y", "gv.z", "gv.w"};
+    Emitter em;
+    em.define_range(g.rm, "grow");
+    const std::string out = pname(ki.out_param);
+    if (N % 4 == 0) {
+      // Every column group lies inside the tile: lanes along the columns.
+      em.define_range(g.rn, "gcol");
+      em.set_lane_range(g.rn, 4);
+      em.reduce_cb_ = [&](const UOp& RR, int lane) -> std::string {
         FG_CHECK(RR == g.R, "gemm epilogue sees one reduction");
-        return kComp[u];
+        return kComp[lane];
       };
-      std::string v = em.val(ki.value, 0);
-      em.line(out + "[" + em.idx(ki.out_index, 0) + "] = " + v + ";");
-      em.close_scope();
+      std::vector<std::string> vals;
+      for (int u = 0; u < 4; u++) vals.push_back(em.val(ki.value, u));
+      Affine ao = affine_of(ki.out_index);
+      bool vstore = ao.ok && !ao.has_scalar_terms() && ao.coef(g.rn) == 1 && ao.c0 % 4 == 0 &&
+                    ki.out_param.dtype().kind == DTypeKind::F32;
+      for (auto& t : ao.terms)
+        if (t.first != g.rn && t.second % 4 != 0) vstore = false;
+      if (vstore) {
+        em.line("*(float4*)(" + out + "+" + em.idx(ki.out_index, 0) + ") = make_float4(" + vals[0] + ", " + vals[1] +
+                ", " + vals[2] + ", " + vals[3] + ");");
+      } else {
+        for (int u = 0; u < 4; u++) em.line(out + "[" + em.idx(ki.out_index, u) + "] = " + vals[u] + ";");
+      }
+    } else {
+      // Ragged last column group: one guarded column at a time.
+      for (int u = 0; u < 4; u++) {
+        const std::string col = "(gcol+" + std::to_string(u) + ")";
+        em.open_scope("if (" + col + " < N_) {", "}");
+        em.define_range(g.rn, col);
+        em.reduce_cb_ = [&, u](const UOp& RR, int) -> std::string {
+          FG_CHECK(RR == g.R, "gemm epilogue sees one reduction");
+          return kComp[u];
+        };
+        std::string v = em.val(ki.value, 0);
+        em.line(out + "[" + em.idx(ki.out_index, 0) + "] = " + v + ";");
+        em.close_scope();
+      }
     }
+    return em.code();
+  };
+  auto indent = [](const std::string& code, const std::string& pre) {
+    std::ostringstream o;
+    std::istringstream is(code);
+    std::string l;
+    while (std::getline(is, l)) o << pre << l << "\n";
+    return o.str();
+  };
+  if (S == 1) {
+    s << indent(epilogue(), "        ");
+  } else {
+    // Raw partial sums of this K range; the epilogue runs after they are summed.
+    s << "          *(fg_f4*)(fg_scratch + ((long)ks * M_ + grow) * NP_ + gcol) = gv;\n";
   }
-  std::istringstream is(em.code());
-  std::string l;
-  while (std::getline(is, l)) s << "        " << l << "\n";
   s << "        }\n      }\n      __syncthreads();\n    }\n}\n";
+  if (S > 1) {
+    // Second pass: one thread per 4 columns of a row sums the S partials in
+    // split order, then runs the epilogue.
+    s << sig(name + "_fin", 256) << " {\n";
+    s << R"(  const long gid = (long)blockIdx.x * 256 + threadIdx.x;
+  if (gid >= (long)M_ * (NP_ / 4)) return;
+  const int grow = (int)(gid / (NP_ / 4)), gcol = (int)(gid % (NP_ / 4)) * 4;
+  fg_f4 gv = *(const fg_f4*)(fg_scratch + (long)grow * NP_ + gcol);
+  for (int ks = 1; ks < S_; ks++) {
+    const fg_f4 p = *(const fg_f4*)(fg_scratch + ((long)ks * M_ + grow) * NP_ + gcol);
+    gv.x = gv.x + p.x; gv.y = gv.y + p.y; gv.z = gv.z + p.z; gv.w = gv.w + p.w;
+  }
+  if (gcol < N_) {
+)";
+    s << indent(epilogue(), "    ");
+    s << "  }\n}\n";
+  }
   RenderedKernel rk;
   rk.name = name;
   rk.kind = kernel_class_name(KernelClass::Gemm);
   rk.source = s.str();
   rk.block[0] = static_cast<unsigned>(NT);
-  rk.grid[0] = static_cast<unsigned>(((M + BM - 1) / BM) * ((N + BN - 1) / BN));
+  rk.grid[0] = static_cast<unsigned>(ntiles * S);
+  if (S > 1) {
+    LaunchSpec a, b;
+    a.func = name + "_part";
+    a.grid[0] = rk.grid[0];
+    a.block[0] = static_cast<unsigned>(NT);
+    b.func = name + "_fin";
+    b.grid[0] = static_cast<unsigned>((M * (NP / 4) + 255) / 256);
+    b.block[0] = 256;
+    rk.launches = {a, b};
+    rk.scratch_bytes = static_cast<size_t>(S * M * NP) * sizeof(float);
+  }
   return rk;
 }
 

@@ -61,6 +61,24 @@ def test_c3_is_copy_plus_mfma_gemm(fg, cpu):
         compile_only(fg, it["source"], it["name"])
 
 
+@pytest.mark.parametrize("mnk,split", [((256, 128, 784), True), ((4096, 10, 2048), True), ((10, 4096, 2048), True),
+                                       ((4096, 4096, 64), False), ((256, 10, 128), False)])
+def test_short_grid_and_narrow_gemms_split_k(fg, cpu, mnk, split):
+    m, n, k = mnk
+    x = fg.Tensor.new(np.ones((m, k), np.float32), [m, k], cpu)
+    w = fg.Tensor.new(np.ones((n, k), np.float32), [n, k], cpu)
+    items = hip_plan(fg, [x.matmul(w.permute([1, 0]))])
+    gemm = [it for it in items if it["class"] == "gemm_mfma_f32"]
+    if (m, n, k) == (256, 10, 128):
+        # Too small a grid for a 32-wide tile: stays a row reduction.
+        assert not gemm and items[-1]["class"] == "row_reduce"
+        return
+    assert len(gemm) == 1
+    src = gemm[0]["source"]
+    assert ("_part(" in src and "_fin(" in src and "fg_scratch" in src) == split
+    compile_only(fg, src, gemm[0]["name"] + ("_part" if split else ""))
+
+
 @pytest.mark.parametrize("batch,dims", [(256, (784, 128, 10)), (512, (784, 256, 256, 10))])
 def test_train_step_kernels_compile_and_use_mfma(fg, cpu, batch, dims):
     from ferrograd_amd.mlp import Mlp, synthetic_batch
