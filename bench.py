@@ -177,7 +177,8 @@ def bench_c1(fg, ctx, steps, warmup):
     ach = alg / (dk["avg_ms"] / 1e3) / 1e9
     return {"ms_per_step": ms, "gbs": alg / (ms / 1e3) / 1e9, "kernels": kern,
             "roofline": {"bound": "hbm", "achieved": ach, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                         "frac": ach / HBM_PEAK_GBS, "kernel": name, "kernel_avg_ms": dk["avg_ms"]}}
+                         "frac": ach / HBM_PEAK_GBS, "traffic": pmc_traffic(name), "kernel": name,
+                         "algorithmic_bytes": alg, "kernel_avg_ms": dk["avg_ms"]}}
 
 
 def bench_c3(fg, ctx, steps, warmup):
@@ -195,13 +196,14 @@ def bench_c3(fg, ctx, steps, warmup):
 
     ms, prof = timed(fg, ctx, step, steps, warmup)
     kern = by_kernel(prof, steps)
-    gemm = [k for k in kern if k.endswith("_gemm")]
+    gemm = [k for k in kern if k.endswith("_gemm")]  # 4096^3 fills the chip: no K split
     flops = 2 * 4096 ** 3
     g = kern[gemm[0]] if gemm else dominant(kern)[1]
     tf = flops / (g["avg_ms"] / 1e3) / 1e12
     return {"ms_per_step": ms, "tflops_step": flops / (ms / 1e3) / 1e12, "kernels": kern,
             "roofline": {"bound": "mfma", "achieved": tf, "peak": FP32_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
                          "frac": tf / FP32_MFMA_PEAK_TFLOPS, "kernel": gemm[0] if gemm else None,
+                         "traffic": pmc_traffic(gemm[0]) if gemm else None, "algorithmic_flops": flops,
                          "kernel_avg_ms": g["avg_ms"]}}
 
 
@@ -222,15 +224,26 @@ def bench_mlp(fg, ctx, steps, warmup, batch, dims):
 
     step, _ = mlp_setup(fg, "hip", batch=batch, dims=dims)
     losses = []
-    ms, prof = timed(fg, ctx, lambda: losses.append(step()), steps, warmup)
+    for _ in range(warmup):  # the first step compiles (hiprtc or the code-object cache)
+        losses.append(step())
+    h0 = fg.stats()["host_ms"]
+    ms, prof = timed(fg, ctx, lambda: losses.append(step()), steps, 0)
+    h1 = fg.stats()["host_ms"]
+    # Host pipeline phases per step, over the timed and the profiled steps.
+    host = {k: (h1[k] - h0[k]) / (2 * steps) for k in h1}
     kern = by_kernel(prof, steps)
-    gemm_ms = sum(v["total_ms_per_step"] for k, v in kern.items() if k.endswith("_gemm"))
+    # MFMA kernels: `_gemm`, or the `_gemm_part` / `_gemm_fin` pair of a split-K GEMM.
+    gemm_ms = sum(v["total_ms_per_step"] for k, v in kern.items() if "_gemm" in k)
     dev_ms = sum(v["total_ms_per_step"] for v in kern.values())
     flops = mlp_gemm_flops(batch, dims)
-    return {"ms_per_step": ms, "steps_per_s": 1e3 / ms, "device_ms_per_step": dev_ms,
+    tf = lambda t: flops / (t / 1e3) / 1e12 / FP32_MFMA_PEAK_TFLOPS if t else None  # noqa: E731
+    return {"ms_per_step": ms, "steps_per_s": 1e3 / ms, "device_ms_per_step": dev_ms, "host_ms_per_step": host,
             "kernels_per_step": sum(v["calls_per_step"] for v in kern.values()),
             "gemm_flops_per_step": flops, "gemm_ms_per_step": gemm_ms,
-            "mfma_frac_of_gemm_kernels": (flops / (gemm_ms / 1e3) / 1e12 / FP32_MFMA_PEAK_TFLOPS) if gemm_ms else None,
+            # All of the step's GEMM FLOPs over the MFMA kernels' time (the narrow
+            # N=10 products, 0.2% of C5's FLOPs, run as row/column reductions and
+            # are counted in the numerator only), and over all device time.
+            "mfma_frac_of_gemm_kernels": tf(gemm_ms), "mfma_frac_of_device_time": tf(dev_ms),
             "loss_first_last": [losses[0], losses[-1]] if losses else None, "kernels": kern}
 
 
@@ -257,6 +270,35 @@ def copy_probe(nbytes: int = 1 << 30, reps: int = 5) -> None:
     print(json.dumps({"copy_probe_bytes_read": nbytes, "copy_probe_bytes_written": nbytes, "launches": reps}))
 
 
+def library_compare() -> None:
+    """Reference points from the vendor libraries on the same GPU: torch's fp32
+    matmul (hipBLASLt / rocBLAS, TF32 off) at C3's 4096^3, and torch's add over
+    2^26 f32 elements (2 reads + 1 write). Not part of the ferrograd path."""
+    import torch
+
+    torch.backends.cuda.matmul.allow_tf32 = False
+    x, w = torch.randn(4096, 4096, device="cuda"), torch.randn(4096, 4096, device="cuda")
+    a, b = torch.rand(1 << 26, device="cuda"), torch.rand(1 << 26, device="cuda")
+    o = torch.empty_like(a)
+
+    def time_ms(fn, reps=20):
+        for _ in range(5):
+            fn()
+        torch.cuda.synchronize()
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        for _ in range(reps):
+            fn()
+        e.record()
+        torch.cuda.synchronize()
+        return s.elapsed_time(e) / reps
+
+    mm = time_ms(lambda: torch.mm(x, w.t()))
+    add = time_ms(lambda: torch.add(a, b, out=o))
+    print(json.dumps({"torch_fp32_mm_4096_ms": mm, "torch_fp32_mm_tflops": 2 * 4096 ** 3 / mm / 1e9,
+                      "torch_add_2^26_ms": add, "torch_add_gbs": 3 * 4 * (1 << 26) / add / 1e6}))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -266,9 +308,13 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--kernels", action="store_true", help="include per-kernel tables")
     ap.add_argument("--copy-probe", action="store_true", help="only run the 1 GiB copy calibration kernel")
+    ap.add_argument("--library-compare", action="store_true", help="only time torch's fp32 mm and add for reference")
     args = ap.parse_args()
     if args.copy_probe:
         copy_probe()
+        return
+    if args.library_compare:
+        library_compare()
         return
     if args.gpus != 1:
         print(f"bench.py measures one MI355X; --gpus {args.gpus} is not supported in this build "
