@@ -1085,45 +1085,62 @@ bool gemm_operand(const UOp& e, const UOp& rk, const KernelInfo& ki, GemmOperand
   return true;
 }
 
-// Workgroup tile of the fp32 MFMA GEMM and the number of K splits.
+// Workgroup tile of the fp32 MFMA GEMM and the number of K splits. Each wave
+// owns a (BM/WGM) x (BN/WGN) block of 32x32 MFMA tiles: TM x TN of them.
 struct GemmTile {
-  int BM = 128, BN = 128, BK = 16, WGM = 2, WGN = 2;
+  int BM = 256, BN = 256, BK = 32, WGM = 2, WGN = 2;
   int64_t S = 1;   // K splits (partials summed by a second pass)
   int64_t KC = 0;  // K per split, a multiple of BK
   int nt() const { return 64 * WGM * WGN; }
+  int tm() const { return BM / WGM / 32; }
+  int tn() const { return BN / WGN / 32; }
 };
 
 constexpr int64_t kComputeUnits = 256;  // MI355X
+constexpr int64_t kLdsPerCu = 163840;   // gfx950 LDS bytes per CU
 constexpr int64_t kMinSplitK = 64;      // shortest K range a split workgroup runs
 
-// Tile shape (measured on MI355X, fp32 4096^3: 256x256/BK16/8 waves 131
-// TFLOP/s, 256x128/BK8/4 waves 128, 128x128/BK16/4 waves 114): the largest
-// tile that still gives every CU a tile. When no shape does, the largest tile
-// that wastes at most 15% of its area on padding and can fill half the chip
-// once K is split, else 64-wide tiles; a side of at most 32 gets a 32-wide
-// tile. The K range is then split over workgroups until the grid fills the
-// resident slots (one 8-wave or two 4-wave workgroups per CU).
+// Workgroups of a tile one CU holds at once: bounded by the LDS of the two
+// double-buffered operand stages (rows padded by 4 floats) and by the
+// accumulators (16 VGPRs per 32x32 tile, about 128 more for staging and
+// addresses, 512 per SIMD lane).
+int64_t gemm_tile_residency(const GemmTile& t) {
+  const int64_t lds = 2 * 4 * static_cast<int64_t>(t.BM + t.BN + 8) * (t.BK + 4);
+  const int64_t waves_per_simd = std::max<int64_t>(1, 512 / (16 * t.tm() * t.tn() + 128));
+  const int64_t by_waves = std::max<int64_t>(1, waves_per_simd * 4 / (t.WGM * t.WGN));
+  return std::max<int64_t>(1, std::min(kLdsPerCu / lds, by_waves));
+}
+
+// Tile shape, measured on MI355X at fp32 4096^3 (same box, same run):
+// 256x256 with four 128x128 waves and BK 32 ran at 134.8-137.6 TFLOP/s
+// (hipBLASLt 138.9-142.8); 256x128 / 128x256 with BK 16 at 129; 128x128 at
+// 127. The largest tile that still gives every CU a tile; when no shape does,
+// the largest that wastes at most 15% of its area on padding and can fill half
+// the chip once K is split, else 64x64; a side of at most 32 gets a 32-wide
+// tile on one wave. The K range is then split over workgroups until the grid
+// fills the resident slots.
 GemmTile choose_gemm_tile(int64_t M, int64_t N, int64_t K) {
   auto tiles = [&](int64_t bm, int64_t bn) { return ((M + bm - 1) / bm) * ((N + bn - 1) / bn); };
   auto waste = [&](int64_t bm, int64_t bn) {
     return static_cast<double>((M + bm - 1) / bm * bm) * static_cast<double>((N + bn - 1) / bn * bn) /
            (static_cast<double>(M) * static_cast<double>(N));
   };
-  auto slots = [](const GemmTile& t) { return kComputeUnits * (t.nt() <= 256 ? 2 : 1); };
+  auto slots = [](const GemmTile& t) { return kComputeUnits * gemm_tile_residency(t); };
   const int64_t smax = std::max<int64_t>(1, K / kMinSplitK);
-  const GemmTile big[4] = {{256, 256, 16, 4, 2}, {256, 128, 8, 2, 2}, {128, 256, 8, 2, 2}, {128, 128, 16, 2, 2}};
+  const int bk = K <= 16 ? 16 : 32;
+  const GemmTile big[4] = {{256, 256, bk, 2, 2}, {256, 128, bk, 2, 2}, {128, 256, bk, 2, 2}, {128, 128, bk, 2, 2}};
   GemmTile t;
   bool chosen = false;
   if (M <= 32 || N <= 32) {
     auto side = [](int64_t ext, int* b, int* w) {
       if (ext <= 32) { *b = 32; *w = 1; }
       else if (ext >= 256) { *b = 256; *w = 4; }
-      else if (ext >= 128) { *b = 128; *w = 2; }
-      else { *b = 64; *w = 1; }
+      else if (ext >= 128) { *b = 128; *w = 4; }
+      else { *b = 64; *w = 2; }
     };
     side(M, &t.BM, &t.WGM);
     side(N, &t.BN, &t.WGN);
-    t.BK = 16;
+    t.BK = bk;
     chosen = true;
   }
   for (int i = 0; i < 4 && !chosen; i++)
@@ -1137,7 +1154,7 @@ GemmTile choose_gemm_tile(int64_t M, int64_t N, int64_t K) {
       t = big[i];
       chosen = true;
     }
-  if (!chosen) t = {64, 64, 16, 2, 2};
+  if (!chosen) t = {64, 64, bk, 2, 2};
   const int64_t nt = tiles(t.BM, t.BN);
   if (nt < kComputeUnits) t.S = std::max<int64_t>(1, std::min(slots(t) / nt, smax));
   t.KC = ((K + t.S - 1) / t.S + t.BK - 1) / t.BK * t.BK;
@@ -1180,35 +1197,118 @@ bool match_gemm(const KernelInfo& ki, GemmMatch* g) {
   return true;
 }
 
+// Helpers of the generated GEMM: vector types for 1/2/4 operands per LDS read
+// and the instruction interleave of one k-tile (sched_group_barrier masks:
+// 0x008 MFMA, 0x020 VMEM read, 0x100 DS read, 0x200 DS write). Group g's MFMAs
+// are paired one to one with the global loads of the next stage (group 0), the
+// LDS reads of group g+1, and the LDS writes of the next stage (last group), so
+// those instructions issue while the MFMA pipe is busy.
+const char* kGemmPrelude = R"(typedef float fg_f2 __attribute__((ext_vector_type(2)));
+template <int V> struct fg_vt;
+template <> struct fg_vt<1> { typedef float t; };
+template <> struct fg_vt<2> { typedef fg_f2 t; };
+template <> struct fg_vt<4> { typedef fg_f4 t; };
+template <int mask, int n>
+__device__ __forceinline__ void fg_sched_pairs() {
+  if constexpr (n > 0) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    __builtin_amdgcn_sched_group_barrier(mask, 1, 0);
+    fg_sched_pairs<mask, n - 1>();
+  }
+}
+template <int G, int g, int NV, int ND, int NW, int MF>
+__device__ __forceinline__ void fg_sched_k_tile() {
+  constexpr int nv = g == 0 ? NV : 0, nd = g + 1 < G ? ND : 0, nw = g == G - 1 ? NW : 0;
+  constexpr int rest = MF - nv - nd - nw;
+  fg_sched_pairs<0x020, nv>();
+  fg_sched_pairs<0x100, nd>();
+  fg_sched_pairs<0x200, nw>();
+  if constexpr (rest > 0) __builtin_amdgcn_sched_group_barrier(0x008, rest, 0);
+  if constexpr (g + 1 < G) fg_sched_k_tile<G, g + 1, NV, ND, NW, MF>();
+}
+)";
+
 RenderedKernel render_gemm(const KernelInfo& ki, const GemmMatch& g, const std::string& name) {
   const int64_t M = g.M, N = g.N, K = g.K;
   const GemmTile tile = choose_gemm_tile(M, N, K);
   const int BM = tile.BM, BN = tile.BN, BK = tile.BK, WGM = tile.WGM, WGN = tile.WGN, NT = tile.nt();
+  const int TM = tile.tm(), TN = tile.tn();
   const int64_t S = tile.S, KC = tile.KC, NP = (N + 3) / 4 * 4;
   const int64_t ntiles = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
-  const int PAD = 4;  // keeps LDS rows 16-byte aligned for float4 stores
-  FG_CHECK(BM % (32 * WGM) == 0 && BN % (32 * WGN) == 0, "gemm tile shape does not fit the wave grid");
+  FG_CHECK(BM % (32 * WGM) == 0 && BN % (32 * WGN) == 0 && BK % 8 == 0, "gemm tile shape does not fit the wave grid");
+  FG_CHECK((TM == 1 || TM == 2 || TM == 4) && (TN == 1 || TN == 2 || TN == 4), "gemm wave tile must be 32, 64 or 128 wide");
   const std::string scratch_param = S > 1 ? ", float* __restrict__ fg_scratch" : "";
-  auto sig = [&](const std::string& fn, int block) {
+  const int waves_per_eu = static_cast<int>(std::max<int64_t>(1, gemm_tile_residency(tile) * NT / 256));
+  auto sig = [&](const std::string& fn, int block, bool main) {
     std::string s = signature(ki, fn, block);
-    return s.substr(0, s.size() - 1) + scratch_param + ")";
+    s = s.substr(0, s.size() - 1) + scratch_param + ")";
+    if (main) {
+      const std::string lb = "__launch_bounds__(" + std::to_string(block) + ") ";
+      s.replace(s.find(lb), lb.size(),
+                lb + "__attribute__((amdgpu_waves_per_eu(" + std::to_string(waves_per_eu) + "))) ");
+    }
+    return s;
   };
   const std::string main_name = S > 1 ? name + "_part" : name;
 
+  // How each operand reaches LDS. Mode 0: 4 consecutive k per thread (unit
+  // stride along k: 16-byte loads), staged [row][k]. Mode 1: 4 consecutive rows
+  // per thread (unit stride along m/n), staged [k][row] with the rows of tile i
+  // interleaved (tile i row r is wave row T*r+i), so one LDS read gives a lane
+  // its operand for all T tiles. Mode 2: one element per load, staged along
+  // whichever index moves faster in memory.
+  struct Stage {
+    int md = 2;
+    bool km = false;
+    int groups = 0, per = 0, V = 1;
+    bool k_fast = true;
+    std::vector<UOp> lds;
+  };
+  auto plan = [&](const GemmOperand& op, int BX, int64_t ext) {
+    Stage st;
+    const int64_t so = op.lead.coef(op.rout), sk = op.lead.coef(g.rk);
+    if (sk == 1 && K % 4 == 0) st.md = 0;
+    else if (so == 1 && ext % 4 == 0) st.md = 1;
+    st.k_fast = std::llabs(sk) <= std::llabs(so);
+    st.km = st.md == 1 || (st.md == 2 && !st.k_fast);
+    st.V = st.md == 2 ? 1 : 4;
+    st.groups = st.md == 2 ? BX * BK : BX * BK / 4;
+    st.per = (st.groups + NT - 1) / NT;
+    st.lds = loads_in(op.expr);
+    return st;
+  };
+  const Stage sa = plan(g.a, BM, M), sb = plan(g.b, BN, N);
+  const int NV = sa.per * static_cast<int>(sa.lds.size()) + sb.per * static_cast<int>(sb.lds.size());
+  const int ND = (sa.km ? 4 : TM) + (sb.km ? 4 : TN);
+  const int NW = sa.per + sb.per;
+
   std::ostringstream s;
-  s << kPrelude;
+  s << kPrelude << kGemmPrelude;
   s << "#define M_ " << M << "\n#define N_ " << N << "\n#define K_ " << K << "\n#define NP_ " << NP << "\n";
   s << "#define S_ " << S << "\n#define KC_ " << KC << "\n#define NTILES_ " << ntiles << "\n";
-  s << "#define BM " << BM << "\n#define BN " << BN << "\n#define BK " << BK << "\n#define PAD " << PAD << "\n";
-  s << "#define NT " << NT << "\n#define WGN " << WGN << "\n";
-  s << sig(main_name, NT) << " {\n";
-  s << R"(  // One LDS block: the double-buffered operand stages during the K loop,
-  // then per-wave 32x32 staging tiles for the epilogue.
-  constexpr int SA = 2 * BK * (BM + PAD), SB = 2 * BK * (BN + PAD), EPS = 36, SE = (NT / 64) * 32 * EPS;
+  s << "#define BM " << BM << "\n#define BN " << BN << "\n#define BK " << BK << "\n";
+  s << "#define NT " << NT << "\n#define WGN " << WGN << "\n#define TM " << TM << "\n#define TN " << TN << "\n";
+  s << "#define A_KM " << (sa.km ? 1 : 0) << "\n#define B_KM " << (sb.km ? 1 : 0) << "\n";
+  s << "#define NV_ " << NV << "\n#define ND_ " << ND << "\n#define NW_ " << NW << "\n";
+  s << sig(main_name, NT, true) << " {\n";
+  s << R"(  // Operand stages, double-buffered, rows padded by 4 floats; then per-wave
+  // 32 x WN staging tiles for the epilogue.
+  constexpr int WM = BM / (NT / 64 / WGN), WN = BN / WGN;
+#if A_KM
+  constexpr int SA_R = BK, SA_C = BM + 4;
+#else
+  constexpr int SA_R = BM, SA_C = BK + 4;
+#endif
+#if B_KM
+  constexpr int SB_R = BK, SB_C = BN + 4;
+#else
+  constexpr int SB_R = BN, SB_C = BK + 4;
+#endif
+  constexpr int SA = 2 * SA_R * SA_C, SB = 2 * SB_R * SB_C, EPS = WN + 4, SE = (NT / 64) * 32 * EPS;
   __shared__ __attribute__((aligned(16))) float smem[(SA + SB) > SE ? (SA + SB) : SE];
-  float (*As)[BK][BM + PAD] = reinterpret_cast<float (*)[BK][BM + PAD]>(smem);
-  float (*Bs)[BK][BN + PAD] = reinterpret_cast<float (*)[BK][BN + PAD]>(smem + SA);
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  float (*As)[SA_R][SA_C] = reinterpret_cast<float (*)[SA_R][SA_C]>(smem);
+  float (*Bs)[SB_R][SB_C] = reinterpret_cast<float (*)[SB_R][SB_C]>(smem + SA);
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, h = lane >> 5, r32 = lane & 31;
   const int nbm = (M_ + BM - 1) / BM, nbn = (N_ + BN - 1) / BN;
   int bid = blockIdx.x;
   // Blocks are dispatched round-robin over the 8 XCDs; give each XCD a
@@ -1227,8 +1327,6 @@ RenderedKernel render_gemm(const KernelInfo& ki, const GemmMatch& g, const std::
   const int gsz = (nbm - first_m) < GM ? (nbm - first_m) : GM;
   const int tm = first_m + (bid % (GM * nbn)) % gsz, tn = (bid % (GM * nbn)) / gsz;
   const int m0 = tm * BM, n0 = tn * BN;
-  // A grid of waves; each wave owns a WM x WN block of 32x32 MFMA tiles.
-  constexpr int WM = BM / (NT / 64 / WGN), WN = BN / WGN, TM = WM / 32, TN = WN / 32;
   const int wm = (wave / WGN) * WM, wn = (wave % WGN) * WN;
   floatx16 acc[TM][TN];
   #pragma unroll
@@ -1238,43 +1336,51 @@ RenderedKernel render_gemm(const KernelInfo& ki, const GemmMatch& g, const std::
       #pragma unroll
       for (int e = 0; e < 16; e++) acc[i][j][e] = 0.0f;
 )";
-  // Global -> register loaders. Staging modes: 0 = 4 consecutive k per thread
-  // (unit stride along k: 16-byte loads), 1 = 4 consecutive rows per thread
-  // (unit stride along m/n), 2 = one element at a time. A stage holds BX*BK
-  // elements; when the threads outnumber its groups the extra threads idle.
-  // load_X only issues the operand's raw loads into registers; store_X
+  // Global -> register loaders. load_X issues the operand's raw loads; store_X
   // evaluates the operand expression (relu recompute, masks) on them when it
-  // writes the stage to LDS, after the MFMAs of the current stage, so the loads
-  // stay in flight under the MFMAs.
-  auto loader = [&](const char* X, const GemmOperand& op, int BX, int64_t ext, const char* dim) {
-    int64_t so = op.lead.coef(op.rout), sk = op.lead.coef(g.rk);
-    int md = 2;
-    if (sk == 1 && K % 4 == 0) md = 0;
-    else if (so == 1 && ext % 4 == 0) md = 1;
-    bool k_fast = std::llabs(sk) <= std::llabs(so);  // mode 2 mapping
-    const int groups = md == 2 ? BX * BK : BX * BK / 4;
-    const int per = (groups + NT - 1) / NT;
-    const int V = md == 2 ? 1 : 4;
-    const std::string guard = groups % NT == 0 ? "" : "idx < " + std::to_string(groups) + " && ";
-    const std::vector<UOp> lds = loads_in(op.expr);
+  // writes the next stage to LDS, late in the k-tile, so the loads stay in
+  // flight under the MFMAs. Out-of-range elements load from a clamped, valid
+  // address and are replaced by 0 with a select: the k-tile body has no
+  // branches, so its instructions can be interleaved as one region.
+  auto loader = [&](const char* X, const GemmOperand& op, const Stage& st, int BX, int64_t ext, const char* dim) {
+    const int V = st.V, per = st.per;
+    const bool guard = st.groups % NT != 0;
+    // Bounds checks only where a tile can overhang: rows when the extent is not
+    // a multiple of the tile, k when K is not a multiple of BK (the K splits
+    // are multiples of BK). Statically in-range loads keep their plain
+    // addresses, which saves registers in the large tiles.
+    const bool row_check = ext % BX != 0, k_check = K % BK != 0;
     auto reg = [&](size_t i, const std::string& slot) { return "r" + std::string(X) + std::to_string(i) + "[" + slot + "]"; };
     auto slot = [&](int u) { return V == 1 ? std::string("j") : "4*j+" + std::to_string(u); };
     auto coords = [&]() {
       std::ostringstream c;
       c << "      const int idx = tid + NT * j;\n";
-      if (md == 0) c << "      const int r = idx / (BK / 4), kk = (idx % (BK / 4)) * 4;\n";
-      else if (md == 1) c << "      const int kk = idx / (" << BX << " / 4), r = (idx % (" << BX << " / 4)) * 4;\n";
-      else if (k_fast) c << "      const int r = idx / BK, kk = idx % BK;\n";
+      if (st.md == 0) c << "      const int r = idx / (BK / 4), kk = (idx % (BK / 4)) * 4;\n";
+      else if (st.md == 1) c << "      const int kk = idx / (" << BX << " / 4), r = (idx % (" << BX << " / 4)) * 4;\n";
+      else if (st.k_fast) c << "      const int r = idx / BK, kk = idx % BK;\n";
       else c << "      const int kk = idx / " << BX << ", r = idx % " << BX << ";\n";
       c << "      const int gr = " << dim << "0 + r, gk = k0 + kk;\n";
-      c << "      const bool in = " << guard << "gr < " << ext << " && gk < kend;\n";
+      std::string cond;
+      if (guard) cond += "idx < " + std::to_string(st.groups);
+      if (row_check) cond += (cond.empty() ? "" : " && ") + std::string("gr < ") + std::to_string(ext);
+      if (k_check) cond += (cond.empty() ? "" : " && ") + std::string("gk < kend");
+      if (cond.empty()) {
+        c << "      constexpr bool in = true;\n      const int grc = gr, gkc = gk;\n";
+      } else {
+        c << "      const bool in = " << cond << ";\n";
+        c << "      const int grc = in ? gr : 0, gkc = in ? gk : 0;\n";
+      }
       return c.str();
     };
     auto setup = [&](Emitter& em) {
-      em.define_range(op.rout, "gr");
-      em.define_range(g.rk, "gk");
-      if (md == 0) em.set_lane_range(g.rk, 4);
-      else if (md == 1) em.set_lane_range(op.rout, 4);
+      // 64-bit index arithmetic: the per-j address offsets are then constants
+      // the compiler folds into the loads, instead of 32-bit sums it must
+      // recompute and sign-extend (which alone cost 80+ spilled VGPRs in the
+      // 256x256 tile).
+      em.define_range(op.rout, "(long)grc");
+      em.define_range(g.rk, "(long)gkc");
+      if (st.md == 0) em.set_lane_range(g.rk, 4);
+      else if (st.md == 1) em.set_lane_range(op.rout, 4);
     };
     auto indent = [](const std::string& code, const char* pre) {
       std::ostringstream o;
@@ -1284,23 +1390,17 @@ RenderedKernel render_gemm(const KernelInfo& ki, const GemmMatch& g, const std::
       return o.str();
     };
     std::ostringstream l;
-    for (size_t i = 0; i < lds.size(); i++)
-      l << "  " << ctype(lds[i].dtype()) << " r" << X << i << "[" << per * V << "];\n";
+    for (size_t i = 0; i < st.lds.size(); i++)
+      l << "  " << ctype(st.lds[i].dtype()) << " r" << X << i << "[" << per * V << "];\n";
     l << "  auto load_" << X << " = [&](int k0) {\n";
     l << "    #pragma unroll\n    for (int j = 0; j < " << per << "; j++) {\n" << coords();
     {
       Emitter em;
       setup(em);
       std::ostringstream body;
-      for (size_t i = 0; i < lds.size(); i++)
-        for (int u = 0; u < V; u++) {
-          std::string v = em.val(lds[i], u);
-          body << reg(i, slot(u)) << " = " << v << ";\n";
-        }
-      // Defined on both paths: no register carries a value across stages.
-      for (size_t i = 0; i < lds.size(); i++)
-        for (int u = 0; u < V; u++) l << "      " << reg(i, slot(u)) << " = 0;\n";
-      l << "      if (in) {\n" << indent(em.code() + body.str(), "        ") << "      }\n";
+      for (size_t i = 0; i < st.lds.size(); i++)
+        for (int u = 0; u < V; u++) body << reg(i, slot(u)) << " = " << em.val(st.lds[i], u) << ";\n";
+      l << indent(em.code() + body.str(), "      ");
     }
     l << "    }\n  };\n";
     const char* SX = X[0] == 'a' ? "As" : "Bs";
@@ -1310,80 +1410,123 @@ RenderedKernel render_gemm(const KernelInfo& ki, const GemmMatch& g, const std::
       Emitter em;
       setup(em);
       em.load_cb_ = [&](const UOp& ld, int u) -> std::string {
-        for (size_t i = 0; i < lds.size(); i++)
-          if (lds[i] == ld) return reg(i, slot(u));
+        for (size_t i = 0; i < st.lds.size(); i++)
+          if (st.lds[i] == ld) return reg(i, slot(u));
         return std::string();
       };
       std::vector<std::string> vals;
       for (int u = 0; u < V; u++) vals.push_back(em.val(op.expr, u));
       std::ostringstream body;
-      for (int u = 0; u < V; u++) body << "v[" << u << "] = " << vals[u] << ";\n";
-      l << "      float v[" << V << "];\n";
-      if (op.expr.op() == Op::Load && op.expr.dtype() == DType::F32()) {
-        // A bare f32 load: its registers already hold 0 outside the operand.
-        l << indent(em.code() + body.str(), "      ");
-      } else {
-        l << "      if (in) {\n" << indent(em.code() + body.str(), "        ") << "      } else {\n";
-        for (int u = 0; u < V; u++) l << "        v[" << u << "] = 0.0f;\n";
-        l << "      }\n";
-      }
+      for (int u = 0; u < V; u++) body << "v[" << u << "] = in ? " << vals[u] << " : 0.0f;\n";
+      l << "      float v[" << V << "];\n" << indent(em.code() + body.str(), "      ");
     }
-    const std::string sguard = groups % NT == 0 ? "" : "if (idx < " + std::to_string(groups) + ") ";
-    if (md == 0) {
-      l << "      " << sguard << "{\n        #pragma unroll\n        for (int q = 0; q < 4; q++) " << SX
-        << "[buf][kk + q][r] = v[q];\n      }\n";
-    } else if (md == 1) {
-      l << "      " << sguard << "*(float4*)(&" << SX << "[buf][kk][r]) = make_float4(v[0], v[1], v[2], v[3]);\n";
-    } else {
+    const std::string sguard = guard ? "if (idx < " + std::to_string(st.groups) + ") " : "";
+    if (st.md == 0) {
+      l << "      " << sguard << "*(fg_f4*)(&" << SX << "[buf][r][kk]) = fg_f4{v[0], v[1], v[2], v[3]};\n";
+    } else if (st.md == 1) {
+      l << "      " << sguard << "*(fg_f4*)(&" << SX << "[buf][kk][r]) = fg_f4{v[0], v[1], v[2], v[3]};\n";
+    } else if (st.km) {
       l << "      " << sguard << SX << "[buf][kk][r] = v[0];\n";
+    } else {
+      l << "      " << sguard << SX << "[buf][r][kk] = v[0];\n";
     }
     l << "    }\n  };\n";
     return l.str();
   };
-  s << loader("a", g.a, BM, M, "m");
-  s << loader("b", g.b, BN, N, "n");
-  s << R"(  const int KT = (kend - kbeg + BK - 1) / BK;
+  s << loader("a", g.a, sa, BM, M, "m");
+  s << loader("b", g.b, sb, BN, N, "n");
+  s << R"(  // K schedule: in group g (8 k), MFMA step t, lane half h uses k = 8g + 4h + t.
+  float fa[2][TM][4], fb[2][TN][4];
+  auto frag = [&](int buf, int g, float (&fra)[TM][4], float (&frb)[TN][4]) {
+#if A_KM
+    #pragma unroll
+    for (int t = 0; t < 4; t++) {
+      const typename fg_vt<TM>::t v = *(const typename fg_vt<TM>::t*)&As[buf][8 * g + 4 * h + t][wm + TM * r32];
+      #pragma unroll
+      for (int i = 0; i < TM; i++) fra[i][t] = ((const float*)&v)[i];
+    }
+#else
+    #pragma unroll
+    for (int i = 0; i < TM; i++) {
+      const fg_f4 v = *(const fg_f4*)&As[buf][wm + 32 * i + r32][8 * g + 4 * h];
+      fra[i][0] = v.x; fra[i][1] = v.y; fra[i][2] = v.z; fra[i][3] = v.w;
+    }
+#endif
+#if B_KM
+    #pragma unroll
+    for (int t = 0; t < 4; t++) {
+      const typename fg_vt<TN>::t v = *(const typename fg_vt<TN>::t*)&Bs[buf][8 * g + 4 * h + t][wn + TN * r32];
+      #pragma unroll
+      for (int j = 0; j < TN; j++) frb[j][t] = ((const float*)&v)[j];
+    }
+#else
+    #pragma unroll
+    for (int j = 0; j < TN; j++) {
+      const fg_f4 v = *(const fg_f4*)&Bs[buf][wn + 32 * j + r32][8 * g + 4 * h];
+      frb[j][0] = v.x; frb[j][1] = v.y; frb[j][2] = v.z; frb[j][3] = v.w;
+    }
+#endif
+  };
+  const int KT = (kend - kbeg + BK - 1) / BK;
   load_a(kbeg); load_b(kbeg);
   store_a(0, kbeg); store_b(0, kbeg);
   __syncthreads();
+  frag(0, 0, fa[0], fb[0]);
   for (int kt = 0; kt < KT; kt++) {
-    const int cur = kt & 1, knext = kbeg + (kt + 1) * BK;
-    if (kt + 1 < KT) { load_a(knext); load_b(knext); }
+    const int cur = kt & 1;
+    // The last k-tile reloads itself, so the body is the same every time.
+    const int knext = kbeg + (kt + 1 < KT ? kt + 1 : kt) * BK;
+    load_a(knext); load_b(knext);
     #pragma unroll
-    for (int kk = 0; kk < BK; kk += 2) {
-      const int kr = kk + (lane >> 5);
-      float af[TM], bf[TN];
+    for (int g = 0; g < BK / 8; g++) {
+      if (g + 1 < BK / 8) frag(cur, g + 1, fa[(g + 1) & 1], fb[(g + 1) & 1]);
       #pragma unroll
-      for (int i = 0; i < TM; i++) af[i] = As[cur][kr][wm + i * 32 + (lane & 31)];
-      #pragma unroll
-      for (int j = 0; j < TN; j++) bf[j] = Bs[cur][kr][wn + j * 32 + (lane & 31)];
-      #pragma unroll
-      for (int i = 0; i < TM; i++)
+      for (int t = 0; t < 4; t++)
         #pragma unroll
-        for (int j = 0; j < TN; j++)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[i], bf[j], acc[i][j], 0, 0, 0);
+        for (int i = 0; i < TM; i++)
+          #pragma unroll
+          for (int j = 0; j < TN; j++)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[g & 1][i][t], fb[g & 1][j][t], acc[i][j], 0, 0, 0);
+      if (g == BK / 8 - 1) { store_a(cur ^ 1, knext); store_b(cur ^ 1, knext); }
     }
-    if (kt + 1 < KT) { store_a(cur ^ 1, knext); store_b(cur ^ 1, knext); }
+    fg_sched_k_tile<BK / 8, 0, NV_, ND_, NW_, 4 * TM * TN>();
     __syncthreads();
+    frag(cur ^ 1, 0, fa[0], fb[0]);
   }
-  // Epilogue: each wave stages one 32x32 accumulator tile at a time in its own
-  // LDS tile (32x32 layout: element e of lane l is row 8*(e/4) + 4*(l/32) +
-  // e%4, column l%32), then reads it back as rows of float4, 8 lanes per row,
-  // so epilogue operands load and outputs store 16 bytes per lane.
+  // Epilogue: each wave stages the 32 x WN accumulators of tile row i in its
+  // own LDS tile (32x32 MFMA layout: element e of lane l is row
+  // 8*(e/4) + 4*(l/32) + e%4, column l%32 of its tile), then reads them back as
+  // rows of float4, so epilogue operands load and outputs store 16 bytes per
+  // lane.
+  __syncthreads();
   float* wst = smem + wave * (32 * EPS);
   #pragma unroll
-  for (int i = 0; i < TM; i++)
+  for (int i = 0; i < TM; i++) {
     #pragma unroll
-    for (int j = 0; j < TN; j++) {
+    for (int e = 0; e < 16; e++) {
+      const int rr = 8 * (e >> 2) + 4 * h + (e & 3);
+#if B_KM
+      typename fg_vt<TN>::t v;
       #pragma unroll
-      for (int e = 0; e < 16; e++) wst[(8 * (e >> 2) + 4 * (lane >> 5) + (e & 3)) * EPS + (lane & 31)] = acc[i][j][e];
-      __syncthreads();
+      for (int j = 0; j < TN; j++) ((float*)&v)[j] = acc[i][j][e];
+      *(typename fg_vt<TN>::t*)(wst + rr * EPS + TN * r32) = v;
+#else
       #pragma unroll
-      for (int q = 0; q < 4; q++) {
-        const int rr = (lane >> 3) + 8 * q, cc = (lane & 7) * 4;
-        const fg_f4 gv = *(const fg_f4*)(wst + rr * EPS + cc);
-        const int grow = m0 + wm + i * 32 + rr, gcol = n0 + wn + j * 32 + cc;
-        if (grow < M_ && gcol < N_) {
+      for (int j = 0; j < TN; j++) wst[rr * EPS + 32 * j + r32] = acc[i][j][e];
+#endif
+    }
+    __syncthreads();
+    #pragma unroll
+    for (int q = 0; q < WN / 8; q++) {
+      const int ch = lane + 64 * q, rr = ch / (WN / 4), cc = (ch % (WN / 4)) * 4;
+      const fg_f4 gv = *(const fg_f4*)(wst + rr * EPS + cc);
+#if A_KM
+      const int grow = m0 + wm + TM * rr + i;
+#else
+      const int grow = m0 + wm + 32 * i + rr;
+#endif
+      const int gcol = n0 + wn + cc;
+      if (grow < M_ && gcol < N_) {
 )";
   // Everything outside the reduction, for the four columns gcol..gcol+3 of
   // row grow whose sums are in gv.
@@ -1441,13 +1584,13 @@ RenderedKernel render_gemm(const KernelInfo& ki, const GemmMatch& g, const std::
     s << indent(epilogue(), "        ");
   } else {
     // Raw partial sums of this K range; the epilogue runs after they are summed.
-    s << "          *(fg_f4*)(fg_scratch + ((long)ks * M_ + grow) * NP_ + gcol) = gv;\n";
+    s << "        *(fg_f4*)(fg_scratch + ((long)ks * M_ + grow) * NP_ + gcol) = gv;\n";
   }
-  s << "        }\n      }\n      __syncthreads();\n    }\n}\n";
+  s << "      }\n    }\n    __syncthreads();\n  }\n}\n";
   if (S > 1) {
     // Second pass: one thread per 4 columns of a row sums the S partials in
     // split order, then runs the epilogue.
-    s << sig(name + "_fin", 256) << " {\n";
+    s << sig(name + "_fin", 256, false) << " {\n";
     s << R"(  const long gid = (long)blockIdx.x * 256 + threadIdx.x;
   if (gid >= (long)M_ * (NP_ / 4)) return;
   const int grow = (int)(gid / (NP_ / 4)), gcol = (int)(gid % (NP_ / 4)) * 4;
