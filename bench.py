@@ -48,11 +48,14 @@ def timed(fg, ctx, step, steps: int, warmup: int):
     for _ in range(warmup):
         step()
     fg.synchronize()
+    h0 = fg.stats()["host_ms"]
     t0 = time.perf_counter()
     for _ in range(steps):
         step()
     fg.synchronize()
     t1 = time.perf_counter()
+    h1 = fg.stats()["host_ms"]
+    timed.host_ms = {k: (h1[k] - h0[k]) / steps for k in h1}  # host pipeline phases per timed step
     ctx.profile_read()  # drop anything recorded before
     ctx.profile(True)
     for _ in range(steps):
@@ -224,13 +227,8 @@ def bench_mlp(fg, ctx, steps, warmup, batch, dims):
 
     step, _ = mlp_setup(fg, "hip", batch=batch, dims=dims)
     losses = []
-    for _ in range(warmup):  # the first step compiles (hiprtc or the code-object cache)
-        losses.append(step())
-    h0 = fg.stats()["host_ms"]
-    ms, prof = timed(fg, ctx, lambda: losses.append(step()), steps, 0)
-    h1 = fg.stats()["host_ms"]
-    # Host pipeline phases per step, over the timed and the profiled steps.
-    host = {k: (h1[k] - h0[k]) / (2 * steps) for k in h1}
+    ms, prof = timed(fg, ctx, lambda: losses.append(step()), steps, warmup)
+    host = timed.host_ms
     kern = by_kernel(prof, steps)
     # MFMA kernels: `_gemm`, or the `_gemm_part` / `_gemm_fin` pair of a split-K GEMM.
     gemm_ms = sum(v["total_ms_per_step"] for k, v in kern.items() if "_gemm" in k)

@@ -1111,27 +1111,34 @@ int64_t gemm_tile_residency(const GemmTile& t) {
   return std::max<int64_t>(1, std::min(kLdsPerCu / lds, by_waves));
 }
 
-// Tile shape, measured on MI355X at fp32 4096^3 (same box, same run):
-// 256x256 with four 128x128 waves and BK 32 ran at 134.8-137.6 TFLOP/s
-// (hipBLASLt 138.9-142.8); 256x128 / 128x256 with BK 16 at 129; 128x128 at
-// 127. The largest tile that still gives every CU a tile; when no shape does,
-// the largest that wastes at most 15% of its area on padding and can fill half
-// the chip once K is split, else 64x64; a side of at most 32 gets a 32-wide
-// tile on one wave. The K range is then split over workgroups until the grid
-// fills the resident slots.
+// Tile and K splits. Measured on MI355X (fp32, same box and run for each
+// comparison):
+// - MFMA-bound shapes: 256x256 with four 128x128 waves and BK 32 ran 4096^3 at
+//   134.8-137.6 TFLOP/s (hipBLASLt 138.9-142.8), 256x128 and 128x256 at 129,
+//   128x128 at 127. The shape and split count are chosen by estimated time:
+//   rounds of resident workgroups times the MFMA time of one tile's K range
+//   (padding included, at each shape's measured efficiency), plus the traffic
+//   of split-K partials. For dW1 of the C5 MLP (4096x784, K 8192) that picks
+//   256x256 with 4 splits (477 us), one full round of 256 workgroups, over
+//   256x128 with 2 or 4 splits (513, 521 us) or 128x128 (511 us).
+// - A side of at most 32 (N = 10 classes): one operand is streamed once, so the
+//   kernel is HBM-bound. BK 16 (less LDS, more resident workgroups) and splits
+//   up to about two workgroups per CU: the 8192x10 (K 4096) forward took 59 us
+//   with BK 32 and 8 splits, 45 with BK 16 and 16 splits.
+// - K of at most 32: the kernel is one pass over its output and epilogue
+//   operands. 64x64 tiles put many workgroups' loads and stores in flight:
+//   8192x4096 with K 10 took 91 us with 256x256 tiles, 54 with 128x128, 50 with
+//   64x64.
 GemmTile choose_gemm_tile(int64_t M, int64_t N, int64_t K) {
-  auto tiles = [&](int64_t bm, int64_t bn) { return ((M + bm - 1) / bm) * ((N + bn - 1) / bn); };
-  auto waste = [&](int64_t bm, int64_t bn) {
-    return static_cast<double>((M + bm - 1) / bm * bm) * static_cast<double>((N + bn - 1) / bn * bn) /
-           (static_cast<double>(M) * static_cast<double>(N));
-  };
-  auto slots = [](const GemmTile& t) { return kComputeUnits * gemm_tile_residency(t); };
+  auto tiles = [&](const GemmTile& t) { return ((M + t.BM - 1) / t.BM) * ((N + t.BN - 1) / t.BN); };
   const int64_t smax = std::max<int64_t>(1, K / kMinSplitK);
-  const int bk = K <= 16 ? 16 : 32;
-  const GemmTile big[4] = {{256, 256, bk, 2, 2}, {256, 128, bk, 2, 2}, {128, 256, bk, 2, 2}, {128, 128, bk, 2, 2}};
-  GemmTile t;
-  bool chosen = false;
+  auto with_splits = [&](GemmTile t, int64_t S) {
+    t.KC = ((K + S - 1) / S + t.BK - 1) / t.BK * t.BK;
+    t.S = (K + t.KC - 1) / t.KC;
+    return t;
+  };
   if (M <= 32 || N <= 32) {
+    GemmTile t;
     auto side = [](int64_t ext, int* b, int* w) {
       if (ext <= 32) { *b = 32; *w = 1; }
       else if (ext >= 256) { *b = 256; *w = 4; }
@@ -1140,26 +1147,37 @@ GemmTile choose_gemm_tile(int64_t M, int64_t N, int64_t K) {
     };
     side(M, &t.BM, &t.WGM);
     side(N, &t.BN, &t.WGN);
-    t.BK = bk;
-    chosen = true;
+    t.BK = 16;
+    const int64_t nt = tiles(t);
+    return with_splits(t, std::max<int64_t>(1, std::min(smax, (2 * kComputeUnits + nt - 1) / nt)));
   }
-  for (int i = 0; i < 4 && !chosen; i++)
-    if (M >= big[i].BM && N >= big[i].BN && tiles(big[i].BM, big[i].BN) >= kComputeUnits) {
-      t = big[i];
-      chosen = true;
+  if (K <= 32) return with_splits(GemmTile{64, 64, K <= 16 ? 16 : 32, 2, 2}, 1);
+  constexpr double kCuFlops = 157.3e12 / kComputeUnits;  // fp32 MFMA peak per CU
+  constexpr double kHbmBytes = 5.0e12;                   // sustained HBM rate for split partials
+  struct Cand {
+    GemmTile t;
+    double eff;  // measured throughput relative to 256x256
+  };
+  const Cand cands[] = {{{256, 256, 32, 2, 2}, 1.0}, {{256, 128, 32, 2, 2}, 0.9}, {{128, 256, 32, 2, 2}, 0.9},
+                        {{128, 128, 32, 2, 2}, 0.92}, {{64, 64, 32, 2, 2}, 0.6}};
+  GemmTile best = with_splits(cands[4].t, 1);
+  double best_s = 1e30;
+  for (const Cand& c : cands) {
+    if (M < c.t.BM / 2 || N < c.t.BN / 2) continue;  // mostly padding
+    const int64_t nt = tiles(c.t), res = gemm_tile_residency(c.t);
+    for (int64_t s = 1; s <= smax; s++) {
+      const GemmTile t = with_splits(c.t, s);
+      if (t.S != s) continue;
+      const int64_t rounds = (nt * t.S + kComputeUnits * res - 1) / (kComputeUnits * res);
+      const double mfma = static_cast<double>(rounds * res) * 2.0 * t.BM * t.BN * t.KC / (kCuFlops * c.eff);
+      const double partials = t.S > 1 ? static_cast<double>(t.S + 1) * M * N * 4.0 / kHbmBytes : 0.0;
+      if (mfma + partials < best_s * 0.999) {
+        best_s = mfma + partials;
+        best = t;
+      }
     }
-  for (int i = 0; i < 4 && !chosen; i++)
-    if (M >= big[i].BM && N >= big[i].BN && waste(big[i].BM, big[i].BN) <= 1.15 &&
-        tiles(big[i].BM, big[i].BN) * smax * 2 >= slots(big[i])) {
-      t = big[i];
-      chosen = true;
-    }
-  if (!chosen) t = {64, 64, bk, 2, 2};
-  const int64_t nt = tiles(t.BM, t.BN);
-  if (nt < kComputeUnits) t.S = std::max<int64_t>(1, std::min(slots(t) / nt, smax));
-  t.KC = ((K + t.S - 1) / t.S + t.BK - 1) / t.BK * t.BK;
-  t.S = (K + t.KC - 1) / t.KC;
-  return t;
+  }
+  return best;
 }
 
 bool match_gemm(const KernelInfo& ki, GemmMatch* g) {
