@@ -442,43 +442,31 @@ UOp UOp::gep(size_t i) const {
 // the first source is visited first, except `After`, whose effect (last source)
 // is walked first.
 std::vector<UOp> UOp::toposort() const {
+  // Stack entries point at the handles held in their parent's `srcs` (or at
+  // *this), which stay alive for the whole walk. The visited set is a flat
+  // pointer map; result order is the reference's (uop.rs:1044-1075).
   std::vector<UOp> result;
-  std::unordered_set<const UOpInner*> visited;
-  std::vector<std::pair<const UOpInner*, bool>> stack;
-  std::vector<const UOpInner*> order_raw;
-  stack.emplace_back(p_.get(), false);
-  UOpMap<int> dummy;
-  (void)dummy;
-  // Keep a map raw->UOp to return owning handles.
-  std::unordered_map<const UOpInner*, UOp> own;
-  own.emplace(p_.get(), *this);
+  PtrIndexMap visited(64);
+  std::vector<std::pair<const UOp*, bool>> stack;
+  stack.emplace_back(this, false);
   while (!stack.empty()) {
     auto [node, processed] = stack.back();
     stack.pop_back();
-    if (visited.count(node)) continue;
+    const UOpInner* raw = node->get();
+    if (visited.get(raw) != PtrIndexMap::kAbsent) continue;
     if (processed) {
-      visited.insert(node);
-      result.push_back(own.at(node));
+      visited.set(raw, 1);
+      result.push_back(*node);
       continue;
     }
     stack.emplace_back(node, true);
-    const auto& srcs = node->srcs;
-    if (node->op == Op::After) {
-      for (size_t i = 0; i < srcs.size(); i++) {
-        const UOpInner* s = srcs[i].get();
-        if (!visited.count(s)) {
-          own.emplace(s, srcs[i]);
-          stack.emplace_back(s, false);
-        }
-      }
+    const auto& srcs = raw->srcs;
+    if (raw->op == Op::After) {
+      for (size_t i = 0; i < srcs.size(); i++)
+        if (visited.get(srcs[i].get()) == PtrIndexMap::kAbsent) stack.emplace_back(&srcs[i], false);
     } else {
-      for (size_t i = srcs.size(); i-- > 0;) {
-        const UOpInner* s = srcs[i].get();
-        if (!visited.count(s)) {
-          own.emplace(s, srcs[i]);
-          stack.emplace_back(s, false);
-        }
-      }
+      for (size_t i = srcs.size(); i-- > 0;)
+        if (visited.get(srcs[i].get()) == PtrIndexMap::kAbsent) stack.emplace_back(&srcs[i], false);
     }
   }
   return result;

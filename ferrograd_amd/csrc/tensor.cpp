@@ -227,13 +227,29 @@ Tensor Tensor::relu() const {  // tensor.rs:517-531
   return from_uop(UOp::make_new(Op::Where, dtype(), {cond.uop(), uop(), zero.uop()}, Arg::none()), requires_grad());
 }
 
+// A constant the library itself builds into graphs (LOG2_E in exp, LN_2 in
+// log, 1/n in cross_entropy). The reference creates a fresh scalar buffer at
+// every call (tensor.rs:697-750); these buffers are never handed out or
+// written, so one buffer per (device, value) gives the same graphs and values
+// without an allocation and a host->device copy per call. The cache is never
+// destroyed: its buffers live until the process ends.
+static Tensor constant_scalar(float v, DeviceId dev) {
+  static auto* cache = new std::vector<std::pair<std::pair<DeviceId, uint32_t>, Tensor>>();
+  uint32_t bits = 0;
+  std::memcpy(&bits, &v, 4);
+  for (auto& [k, t] : *cache)
+    if (k.first == dev && k.second == bits) return t;
+  cache->emplace_back(std::make_pair(dev, bits), Tensor::scalar_f32(v, dev));
+  return cache->back().second;
+}
+
 Tensor Tensor::exp() const {  // tensor.rs:697-700 (f32 LOG2_E)
-  Tensor log2e = scalar_f32(1.44269504088896340736f, device());
+  Tensor log2e = constant_scalar(1.44269504088896340736f, device());
   return mul(log2e).exp2();
 }
 
 Tensor Tensor::log() const {  // tensor.rs:704-707 (f32 LN_2)
-  Tensor ln2 = scalar_f32(0.693147180559945309417f, device());
+  Tensor ln2 = constant_scalar(0.693147180559945309417f, device());
   return log2().mul(ln2);
 }
 
@@ -314,7 +330,7 @@ Tensor Tensor::cross_entropy(const Tensor& targets) const {  // tensor.rs:738-75
   Tensor per = targets.mul(lp).sum({cax}).neg();
   std::vector<size_t> red;
   for (size_t i = 0; i < per.ndim(); i++) red.push_back(i);
-  Tensor scale = scalar_f32(1.0f / static_cast<float>(per.numel()), device());
+  Tensor scale = constant_scalar(1.0f / static_cast<float>(per.numel()), device());
   return per.sum(red).mul(scale);
 }
 
@@ -846,16 +862,17 @@ void Tensor::backward() const {  // tensor.rs:971-998
     ~Timer() { realize_stats().ns_backward += now_ns() - t; }
   } timer;
   FG_CHECK(numel() == 1, "backward requires a scalar loss");
-  UOpSet all;
-  for (auto& n : uop().toposort()) all.insert(n);
+  const std::vector<UOp> order = uop().toposort();
+  PtrIndexMap in_graph(order.size());
+  for (size_t i = 0; i < order.size(); i++) in_graph.set(order[i].get(), static_cast<uint32_t>(i));
   std::vector<Tensor> targets;
   for (auto& t : live_tensors())
-    if (t.requires_grad() && all.count(t.uop())) targets.push_back(t);
+    if (t.requires_grad() && in_graph.get(t.uop().get()) != PtrIndexMap::kAbsent) targets.push_back(t);
   if (targets.empty()) return;
   std::vector<UOp> tu;
   for (auto& t : targets) tu.push_back(t.uop());
   UOp rg = UOp::full(shape(), DType::F32(), device(), 1.0);
-  auto grads = compute_gradient(uop(), rg, tu);
+  auto grads = compute_gradient_ordered(order, rg, tu);
   for (auto& t : targets) {
     auto it = grads.find(t.uop());
     UOp g = it != grads.end() ? it->second : UOp::full(t.shape(), DType::F32(), t.device(), 0.0);
@@ -942,51 +959,59 @@ std::vector<UOp> gradient_for_op(const UOp& node, const UOp& grad) {
   }
 }
 
-UOpSet needed_nodes(const UOp& root, const std::vector<UOp>& targets,
-                    const UOpMap<std::vector<UOp>>& consumers) {  // gradient.rs:64-81
-  UOpSet needed;
-  std::vector<UOp> stack(targets.begin(), targets.end());
-  while (!stack.empty()) {
-    UOp n = stack.back();
-    stack.pop_back();
-    if (!needed.insert(n).second) continue;
-    auto it = consumers.find(n);
-    if (it != consumers.end()) stack.insert(stack.end(), it->second.begin(), it->second.end());
-  }
-  needed.insert(root);
-  return needed;
-}
-
 }  // namespace
 
-UOpMap<UOp> compute_gradient(const UOp& root, const UOp& root_grad, const std::vector<UOp>& targets) {
-  auto order = root.toposort();
-  auto consumers = build_consumer_map(order);
-  auto needed = needed_nodes(root, targets, consumers);
-  UOpMap<UOp> grads;
-  grads[root] = root_grad;
-  for (size_t i = order.size(); i-- > 0;) {
+// gradient.rs:20-81 over `order`, the toposort of the root (its last node).
+// Nodes are addressed by their position: consumer lists, the `needed` set
+// (nodes reachable from a target along consumer edges) and the accumulated
+// gradients are flat arrays. Gradients are accumulated in reverse
+// topological order with the reference's rules and operand order.
+UOpMap<UOp> compute_gradient_ordered(const std::vector<UOp>& order, const UOp& root_grad,
+                                     const std::vector<UOp>& targets) {
+  const size_t n = order.size();
+  FG_CHECK(n > 0, "gradient of an empty graph");
+  PtrIndexMap index(n);
+  for (size_t i = 0; i < n; i++) index.set(order[i].get(), static_cast<uint32_t>(i));
+  std::vector<std::vector<uint32_t>> consumers(n);
+  for (size_t i = 0; i < n; i++)
+    for (auto& src : order[i].srcs()) consumers[index.get(src.get())].push_back(static_cast<uint32_t>(i));
+  std::vector<char> needed(n, 0);
+  std::vector<uint32_t> stack;
+  for (auto& t : targets) {
+    uint32_t ti = index.get(t.get());
+    if (ti != PtrIndexMap::kAbsent) stack.push_back(ti);
+  }
+  while (!stack.empty()) {
+    uint32_t v = stack.back();
+    stack.pop_back();
+    if (needed[v]) continue;
+    needed[v] = 1;
+    for (uint32_t c : consumers[v]) stack.push_back(c);
+  }
+  needed[n - 1] = 1;
+  std::vector<UOp> grads(n);
+  grads[n - 1] = root_grad;
+  for (size_t i = n; i-- > 0;) {
+    if (!needed[i] || !grads[i]) continue;
     const UOp& node = order[i];
-    if (!needed.count(node)) continue;
-    auto gi = grads.find(node);
-    if (gi == grads.end()) continue;
-    UOp g = gi->second;
-    auto local = gradient_for_op(node, g);
+    auto local = gradient_for_op(node, grads[i]);
     for (size_t s = 0; s < node.srcs().size() && s < local.size(); s++) {
       if (!local[s]) continue;
-      const UOp& src = node.src(s);
-      if (!needed.count(src)) continue;
-      auto ex = grads.find(src);
-      if (ex != grads.end()) ex->second = UOp::add(ex->second, local[s]);
-      else grads[src] = local[s];
+      const uint32_t si = index.get(node.src(s).get());
+      if (!needed[si]) continue;
+      grads[si] = grads[si] ? UOp::add(grads[si], local[s]) : local[s];
     }
   }
   UOpMap<UOp> result;
   for (auto& t : targets) {
-    auto it = grads.find(t);
-    result[t] = it != grads.end() ? it->second : zero_like(t);
+    const uint32_t ti = index.get(t.get());
+    result[t] = ti != PtrIndexMap::kAbsent && grads[ti] ? grads[ti] : zero_like(t);
   }
   return result;
+}
+
+UOpMap<UOp> compute_gradient(const UOp& root, const UOp& root_grad, const std::vector<UOp>& targets) {
+  return compute_gradient_ordered(root.toposort(), root_grad, targets);
 }
 
 // ── nn.rs ───────────────────────────────────────────────────────────────────
@@ -1054,7 +1079,14 @@ void Sgd::zero_grad() const {
 
 void Sgd::step() const {  // optim.rs:60-71
   for (auto& p : params) {
-    Tensor lrt = Tensor::scalar_f32(lr, p.device());
+    const Tensor* lrp = nullptr;
+    for (auto& [d, t] : lr_buffers)
+      if (d == p.device()) lrp = &t;
+    if (!lrp) {
+      lr_buffers.emplace_back(p.device(), Tensor::scalar_f32(lr, p.device()));
+      lrp = &lr_buffers.back().second;
+    }
+    const Tensor& lrt = *lrp;
     auto g = p.grad();
     FG_CHECK(g.has_value(), "optimizer step requires parameter gradients");
     Tensor update = p.detach().sub(g->mul(lrt));

@@ -105,6 +105,9 @@ struct TensorInner {
 
 // gradient.rs:20-58
 UOpMap<UOp> compute_gradient(const UOp& root, const UOp& root_grad, const std::vector<UOp>& targets);
+// compute_gradient with the root's toposort already computed (root = its last node).
+UOpMap<UOp> compute_gradient_ordered(const std::vector<UOp>& order, const UOp& root_grad,
+                                     const std::vector<UOp>& targets);
 
 // nn.rs — seeded Kaiming-normal init and Linear.
 void reset_init_seed(uint64_t seed = 42);
@@ -121,6 +124,11 @@ struct Linear {
 struct Sgd {
   std::vector<Tensor> params;
   float lr;
+  // The learning rate as a 1-element buffer per device, uploaded on the first
+  // step and only ever read (optim.rs:62 builds Tensor::scalar(lr) for every
+  // parameter on every step; the values are the same, without a host->device
+  // copy per parameter per step).
+  mutable std::vector<std::pair<DeviceId, Tensor>> lr_buffers;
   Sgd(const std::vector<Tensor>& params, float lr);
   void zero_grad() const;
   void step() const;
