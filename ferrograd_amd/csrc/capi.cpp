@@ -355,6 +355,12 @@ int fg_stats(uint64_t* k, uint64_t* p, uint64_t* h) {
   return 0;
 }
 
+int fg_graph_stats(uint64_t* replays, uint64_t* updated_launches) {
+  if (replays) *replays = fg::realize_stats().graph_replays;
+  if (updated_launches) *updated_launches = fg::realize_stats().graph_updates;
+  return 0;
+}
+
 int fg_host_times(uint64_t out[5]) {
   auto& s = fg::realize_stats();
   out[0] = s.ns_schedule;

@@ -97,6 +97,12 @@ class Device {
   // Give a reserved buffer storage. `zero` asks for zero-filled memory; kernel
   // outputs that overwrite every element pass false.
   virtual void realize_storage(BufferInner& b, bool zero) = 0;
+  // realize_storage preferring the storage at `hint` (a replayed plan asks for
+  // the blocks its outputs had last time). Devices without the notion ignore it.
+  virtual void realize_storage_at(BufferInner& b, bool zero, void* hint) {
+    (void)hint;
+    realize_storage(b, zero);
+  }
   virtual void release(BufferInner& b) = 0;
   virtual void copy_from_host(const Buffer& b, const void* src, size_t nbytes) = 0;
   virtual std::vector<uint8_t> copy_to_host(const Buffer& b) = 0;
@@ -106,6 +112,14 @@ class Device {
   virtual RenderedKernel render(const UOp& optimized, const std::string& name) = 0;
   virtual std::shared_ptr<Program> compile(const RenderedKernel& rk, size_t num_args) = 0;
   virtual void execute(Program& p, std::vector<KernelArg>& args) = 0;
+  // Run a recorded sequence of launches (a replayed realisation plan) in
+  // order. `state` is a slot owned by the sequence's record, in which the
+  // device may keep replay state between calls; it is dropped with the record.
+  virtual void execute_sequence(const std::vector<Program*>& progs, std::vector<std::vector<KernelArg>>& args,
+                                std::shared_ptr<void>& state) {
+    (void)state;
+    for (size_t i = 0; i < progs.size(); i++) execute(*progs[i], args[i]);
+  }
   virtual void synchronize() {}
   // Whether schedule-time value-preserving fusion (shared elementwise
   // subexpressions inlined into one kernel, zero buffers folded) is enabled.

@@ -7,6 +7,7 @@
 #include "../../include/ferrograd_hip.h"
 #include "device.hpp"
 #include "gpu_lower.hpp"
+#include "tensor.hpp"
 
 namespace fg {
 
@@ -51,10 +52,12 @@ class HipDevice : public Device {
     return b;
   }
 
-  void realize_storage(BufferInner& b, bool zero) override {
+  void realize_storage(BufferInner& b, bool zero) override { realize_storage_at(b, zero, nullptr); }
+
+  void realize_storage_at(BufferInner& b, bool zero, void* hint) override {
     if (b.realized) return;
     void* p = nullptr;
-    check(fg_hip_alloc(ctx(), b.nbytes(), zero ? 1 : 0, &p), "fg_hip_alloc");
+    check(fg_hip_alloc_hint(ctx(), b.nbytes(), zero ? 1 : 0, hint, &p), "fg_hip_alloc");
     b.storage = p;
     b.realized = true;
     b.zero_init = false;
@@ -123,8 +126,9 @@ class HipDevice : public Device {
     return p;
   }
 
-  void execute(Program& prog, std::vector<KernelArg>& args) override {  // cpu.rs:328-380
-    auto& p = static_cast<HipProgram&>(prog);
+  // The launch arguments of one program execution: the kernel arguments in
+  // slot order, then the program's scratch buffer if it has one.
+  std::vector<fg_arg> marshal(HipProgram& p, std::vector<KernelArg>& args) {
     FG_CHECK(args.size() == p.num_args,
              "expected " + std::to_string(p.num_args) + " kernel args, got " + std::to_string(args.size()));
     std::vector<fg_arg> a(args.size());
@@ -149,6 +153,12 @@ class HipDevice : public Device {
       s.v.p = p.scratch;
       a.push_back(s);
     }
+    return a;
+  }
+
+  void execute(Program& prog, std::vector<KernelArg>& args) override {  // cpu.rs:328-380
+    auto& p = static_cast<HipProgram&>(prog);
+    std::vector<fg_arg> a = marshal(p, args);
     if (p.passes.empty()) {
       check(fg_hip_launch(ctx(), p.prog, a.data(), static_cast<int>(a.size()), p.meta.grid, p.meta.block,
                           p.meta.lds_bytes),
@@ -160,6 +170,71 @@ class HipDevice : public Device {
       check(fg_hip_launch(ctx(), p.passes[i], a.data(), static_cast<int>(a.size()), l.grid, l.block, l.lds_bytes),
             "execution failed");
     }
+  }
+
+  // A replayed plan: launched one by one the first time, then recorded once
+  // as a HIP graph and replayed through it (one graph launch, with only the
+  // changed launch arguments updated). A sequence whose graph cannot be built
+  // keeps launching one by one.
+  void execute_sequence(const std::vector<Program*>& progs, std::vector<std::vector<KernelArg>>& args,
+                        std::shared_ptr<void>& state) override {
+    struct Replay {
+      int uses = 0;
+      bool failed = false;
+      fg_graph* graph = nullptr;
+      ~Replay() { fg_hip_graph_free(graph); }
+    };
+    if (!state) state = std::make_shared<Replay>();
+    auto* r = static_cast<Replay*>(state.get());
+    r->uses++;
+    std::vector<fg_prog*> lp;
+    std::vector<unsigned> grids, blocks, lds;
+    std::vector<int> nargs;
+    std::vector<fg_arg> all;
+    for (size_t i = 0; i < progs.size(); i++) {
+      auto& p = static_cast<HipProgram&>(*progs[i]);
+      std::vector<fg_arg> a = marshal(p, args[i]);
+      auto add = [&](fg_prog* fp, const unsigned* g, const unsigned* b, unsigned l) {
+        lp.push_back(fp);
+        grids.insert(grids.end(), g, g + 3);
+        blocks.insert(blocks.end(), b, b + 3);
+        lds.push_back(l);
+        nargs.push_back(static_cast<int>(a.size()));
+        all.insert(all.end(), a.begin(), a.end());
+      };
+      if (p.passes.empty()) add(p.prog, p.meta.grid, p.meta.block, p.meta.lds_bytes);
+      for (size_t k = 0; k < p.passes.size(); k++)
+        add(p.passes[k], p.meta.launches[k].grid, p.meta.launches[k].block, p.meta.launches[k].lds_bytes);
+    }
+    if (graphs_enabled() && !r->failed && !r->graph && r->uses >= 2 && lp.size() >= 2) {
+      if (fg_hip_graph_create(ctx(), static_cast<int>(lp.size()), lp.data(), grids.data(), blocks.data(), lds.data(),
+                              nargs.data(), all.data(), &r->graph) != FG_OK) {
+        r->failed = true;
+        r->graph = nullptr;
+      }
+    }
+    if (r->graph) {
+      int updated = 0;
+      check(fg_hip_graph_launch(ctx(), r->graph, all.data(), &updated), "execution failed");
+      realize_stats().graph_replays++;
+      realize_stats().graph_updates += static_cast<size_t>(updated);
+      return;
+    }
+    size_t off = 0;
+    for (size_t i = 0; i < lp.size(); i++) {
+      check(fg_hip_launch(ctx(), lp[i], all.data() + off, nargs[i], &grids[3 * i], &blocks[3 * i], lds[i]),
+            "execution failed");
+      off += static_cast<size_t>(nargs[i]);
+    }
+  }
+
+  // FG_HIP_GRAPHS=0 launches replayed plans one by one.
+  static bool graphs_enabled() {
+    static const bool on = [] {
+      const char* e = std::getenv("FG_HIP_GRAPHS");
+      return !(e && std::strcmp(e, "0") == 0);
+    }();
+    return on;
   }
 
   void synchronize() override {

@@ -9,6 +9,7 @@
 #include <sys/stat.h>
 #include <unistd.h>
 
+#include <algorithm>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
@@ -138,6 +139,23 @@ struct fg_ctx {
   std::string profile_json;
 };
 
+struct fg_graph {
+  struct Launch {
+    fg_prog* prog = nullptr;
+    unsigned grid[3] = {1, 1, 1}, block[3] = {1, 1, 1}, lds = 0;
+    std::vector<fg_arg> args;  // as last set on the instantiated graph
+    hipGraphNode_t node = nullptr;
+    hipKernelNodeParams params = {};
+  };
+  std::vector<Launch> launches;
+  hipGraph_t graph = nullptr;
+  hipGraphExec_t exec = nullptr;
+  ~fg_graph() {
+    if (exec) hipGraphExecDestroy(exec);
+    if (graph) hipGraphDestroy(graph);
+  }
+};
+
 namespace {
 constexpr size_t kAllocGranule = 256;
 constexpr size_t kSmallCopy = 1 << 16;
@@ -187,13 +205,26 @@ int fg_hip_destroy(fg_ctx* c) {
 }
 
 int fg_hip_alloc(fg_ctx* c, size_t nbytes, int zero, void** dptr) {
+  return fg_hip_alloc_hint(c, nbytes, zero, nullptr, dptr);
+}
+
+int fg_hip_alloc_hint(fg_ctx* c, size_t nbytes, int zero, void* hint, void** dptr) {
   if (!c || !dptr) return set_err(FG_ERR_INVALID, "fg_hip_alloc: null argument");
   size_t sz = round_up(nbytes == 0 ? 1 : nbytes);
   void* p = nullptr;
   auto it = c->free_blocks.find(sz);
   if (it != c->free_blocks.end() && !it->second.empty()) {
-    p = it->second.back();
-    it->second.pop_back();
+    auto& blocks = it->second;
+    size_t pick = blocks.size() - 1;
+    if (hint)
+      for (size_t i = blocks.size(); i-- > 0;)
+        if (blocks[i] == hint) {
+          pick = i;
+          break;
+        }
+    p = blocks[pick];
+    blocks[pick] = blocks.back();
+    blocks.pop_back();
     c->cached_bytes -= sz;
   } else {
     hipError_t e = hipMalloc(&p, sz);
@@ -354,15 +385,9 @@ int fg_hip_program_free(fg_prog* p) {
 
 int fg_hip_program_num_args(const fg_prog* p) { return p ? p->num_args : -1; }
 
-int fg_hip_launch(fg_ctx* c, fg_prog* p, const fg_arg* args, int nargs, const unsigned grid[3],
-                  const unsigned block[3], unsigned lds) {
-  if (!c || !p || !grid || !block) return set_err(FG_ERR_INVALID, "fg_hip_launch: null argument");
-  if (nargs != p->num_args)
-    return set_err(FG_ERR_ARGS, "expected " + std::to_string(p->num_args) + " kernel args, got " + std::to_string(nargs));
-  if (block[0] * block[1] * block[2] == 0 || block[0] * block[1] * block[2] > 1024)
-    return set_err(FG_ERR_INVALID, "fg_hip_launch: block size must be in [1, 1024]");
-  if (grid[0] == 0 || grid[1] == 0 || grid[2] == 0) return set_err(FG_ERR_INVALID, "fg_hip_launch: empty grid");
-  void* params[64];
+namespace {
+// Points params[i] at the value of args[i] (kernelParams for a HIP launch).
+int marshal_args(const fg_arg* args, int nargs, void** params) {
   if (nargs > 64) return set_err(FG_ERR_ARGS, "fg_hip_launch: at most 64 arguments");
   for (int i = 0; i < nargs; i++) {
     switch (args[i].kind) {
@@ -373,6 +398,33 @@ int fg_hip_launch(fg_ctx* c, fg_prog* p, const fg_arg* args, int nargs, const un
       default: return set_err(FG_ERR_ARGS, "fg_hip_launch: unknown argument kind " + std::to_string(args[i].kind));
     }
   }
+  return FG_OK;
+}
+
+bool same_args(const fg_arg* a, const fg_arg* b, int n) {
+  for (int i = 0; i < n; i++) {
+    if (a[i].kind != b[i].kind) return false;
+    switch (a[i].kind) {
+      case FG_ARG_PTR: if (a[i].v.p != b[i].v.p) return false; break;
+      case FG_ARG_I32: if (a[i].v.i != b[i].v.i) return false; break;
+      case FG_ARG_F32: if (std::memcmp(&a[i].v.f, &b[i].v.f, sizeof(float)) != 0) return false; break;
+      default: if (a[i].v.b != b[i].v.b) return false; break;
+    }
+  }
+  return true;
+}
+}  // namespace
+
+int fg_hip_launch(fg_ctx* c, fg_prog* p, const fg_arg* args, int nargs, const unsigned grid[3],
+                  const unsigned block[3], unsigned lds) {
+  if (!c || !p || !grid || !block) return set_err(FG_ERR_INVALID, "fg_hip_launch: null argument");
+  if (nargs != p->num_args)
+    return set_err(FG_ERR_ARGS, "expected " + std::to_string(p->num_args) + " kernel args, got " + std::to_string(nargs));
+  if (block[0] * block[1] * block[2] == 0 || block[0] * block[1] * block[2] > 1024)
+    return set_err(FG_ERR_INVALID, "fg_hip_launch: block size must be in [1, 1024]");
+  if (grid[0] == 0 || grid[1] == 0 || grid[2] == 0) return set_err(FG_ERR_INVALID, "fg_hip_launch: empty grid");
+  void* params[64];
+  if (int rc = marshal_args(args, nargs, params)) return rc;
   if (c->profiling) {
     // Start/stop events attached to the dispatch itself, so the duration
     // excludes any host gap before the launch reaches the queue.
@@ -392,6 +444,102 @@ int fg_hip_launch(fg_ctx* c, fg_prog* p, const fg_arg* args, int nargs, const un
   }
   HIP_TRY(hipModuleLaunchKernel(p->func, grid[0], grid[1], grid[2], block[0], block[1], block[2], lds, c->stream,
                                 params, nullptr));
+  return FG_OK;
+}
+
+int fg_hip_graph_create(fg_ctx* c, int n, fg_prog* const* progs, const unsigned* grids, const unsigned* blocks,
+                        const unsigned* lds, const int* nargs, const fg_arg* args, fg_graph** out) {
+  if (!c || !progs || !grids || !blocks || !lds || !nargs || !args || !out || n <= 0)
+    return set_err(FG_ERR_INVALID, "fg_hip_graph_create: null argument or empty sequence");
+  auto g = std::make_unique<fg_graph>();
+  size_t off = 0;
+  for (int i = 0; i < n; i++) {
+    if (!progs[i] || nargs[i] != progs[i]->num_args)
+      return set_err(FG_ERR_ARGS, "fg_hip_graph_create: launch " + std::to_string(i) + " has the wrong argument count");
+    fg_graph::Launch l;
+    l.prog = progs[i];
+    for (int d = 0; d < 3; d++) {
+      l.grid[d] = grids[3 * i + d];
+      l.block[d] = blocks[3 * i + d];
+    }
+    l.lds = lds[i];
+    l.args.assign(args + off, args + off + nargs[i]);
+    off += static_cast<size_t>(nargs[i]);
+    g->launches.push_back(std::move(l));
+  }
+  // Record the sequence by capturing its launches on the context's stream
+  // (nothing executes during capture), then walk the resulting chain from its
+  // root so node k is launch k.
+  HIP_TRY(hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal));
+  int rc = FG_OK;
+  for (auto& l : g->launches) {
+    void* params[64];
+    rc = marshal_args(l.args.data(), static_cast<int>(l.args.size()), params);
+    if (rc) break;
+    hipError_t e = hipModuleLaunchKernel(l.prog->func, l.grid[0], l.grid[1], l.grid[2], l.block[0], l.block[1],
+                                         l.block[2], l.lds, c->stream, params, nullptr);
+    if (e != hipSuccess) {
+      rc = set_err(FG_ERR_HIP, std::string("hipModuleLaunchKernel (capture): ") + hipGetErrorString(e));
+      break;
+    }
+  }
+  hipError_t ee = hipStreamEndCapture(c->stream, &g->graph);
+  if (rc) return rc;
+  if (ee != hipSuccess) return set_err(FG_ERR_HIP, std::string("hipStreamEndCapture: ") + hipGetErrorString(ee));
+  size_t nroots = 0;
+  HIP_TRY(hipGraphGetRootNodes(g->graph, nullptr, &nroots));
+  if (nroots != 1) return set_err(FG_ERR_HIP, "fg_hip_graph_create: captured graph is not a single chain");
+  hipGraphNode_t node = nullptr;
+  HIP_TRY(hipGraphGetRootNodes(g->graph, &node, &nroots));
+  for (size_t i = 0; i < g->launches.size(); i++) {
+    g->launches[i].node = node;
+    HIP_TRY(hipGraphKernelNodeGetParams(node, &g->launches[i].params));
+    size_t ndep = 0;
+    HIP_TRY(hipGraphNodeGetDependentNodes(node, nullptr, &ndep));
+    if (i + 1 < g->launches.size()) {
+      if (ndep != 1) return set_err(FG_ERR_HIP, "fg_hip_graph_create: captured graph is not a single chain");
+      HIP_TRY(hipGraphNodeGetDependentNodes(node, &node, &ndep));
+    } else if (ndep != 0) {
+      return set_err(FG_ERR_HIP, "fg_hip_graph_create: captured graph has extra nodes");
+    }
+  }
+  HIP_TRY(hipGraphInstantiate(&g->exec, g->graph, nullptr, nullptr, 0));
+  *out = g.release();
+  return FG_OK;
+}
+
+int fg_hip_graph_launch(fg_ctx* c, fg_graph* g, const fg_arg* args, int* updated) {
+  if (!c || !g || !args) return set_err(FG_ERR_INVALID, "fg_hip_graph_launch: null argument");
+  size_t off = 0;
+  if (updated) *updated = 0;
+  if (c->profiling) {
+    for (auto& l : g->launches) {
+      if (int rc = fg_hip_launch(c, l.prog, args + off, static_cast<int>(l.args.size()), l.grid, l.block, l.lds))
+        return rc;
+      off += l.args.size();
+    }
+    return FG_OK;
+  }
+  for (auto& l : g->launches) {
+    const int n = static_cast<int>(l.args.size());
+    if (!same_args(l.args.data(), args + off, n)) {
+      std::copy(args + off, args + off + n, l.args.begin());
+      void* params[64];
+      if (int rc = marshal_args(l.args.data(), n, params)) return rc;
+      hipKernelNodeParams p = l.params;
+      p.kernelParams = params;
+      p.extra = nullptr;
+      HIP_TRY(hipGraphExecKernelNodeSetParams(g->exec, l.node, &p));
+      if (updated) ++*updated;
+    }
+    off += static_cast<size_t>(n);
+  }
+  HIP_TRY(hipGraphLaunch(g->exec, c->stream));
+  return FG_OK;
+}
+
+int fg_hip_graph_free(fg_graph* g) {
+  delete g;
   return FG_OK;
 }
 

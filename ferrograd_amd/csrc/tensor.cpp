@@ -590,6 +590,8 @@ struct CachedPlan {
   std::vector<PlanKernel> kernels;
   std::vector<PlanReplacement> replacements;
   std::vector<uint32_t> written_leaves;  // leaves scheduling marked as overwritten
+  mutable std::shared_ptr<void> device_state;  // the device's replay state (Device::execute_sequence)
+  mutable std::vector<void*> last_storage;     // each kernel's output storage at the last replay
 };
 
 struct PlanCache {
@@ -690,15 +692,23 @@ std::shared_ptr<CachedPlan> record_plan(const GraphKey& k, const SchedulePlan& p
 void replay_plan(Device& backend, const GraphKey& k, const CachedPlan& plan) {
   for (uint32_t i : plan.written_leaves) k.leaves[i]->known_zero = false;
   std::vector<Buffer> outs(plan.kernels.size());
-  std::vector<KernelArg> args;
+  std::vector<Program*> progs(plan.kernels.size());
+  std::vector<std::vector<KernelArg>> seq_args(plan.kernels.size());
   int debug = debug_level();
+  uint64_t l0 = now_ns();
+  // Every output and lazily zeroed input gets storage first (zero fills are
+  // queued on the stream ahead of the launches), then the whole sequence runs.
   for (size_t j = 0; j < plan.kernels.size(); j++) {
     const PlanKernel& pk = plan.kernels[j];
-    uint64_t l0 = now_ns();
-    args.clear();
+    std::vector<KernelArg>& args = seq_args[j];
+    progs[j] = pk.program.get();
     if (pk.has_output) {
       Buffer out = backend.reserve_buffer(pk.out_dtype, pk.out_numel);
-      backend.realize_storage(*out, false);
+      // The same storage as last time when it is free again, so a device that
+      // recorded this sequence finds its launch arguments unchanged.
+      if (plan.last_storage.size() != plan.kernels.size()) plan.last_storage.assign(plan.kernels.size(), nullptr);
+      backend.realize_storage_at(*out, false, plan.last_storage[j]);
+      plan.last_storage[j] = out->storage;
       out->known_zero = false;
       outs[j] = out;
       args.push_back(KernelArg::buf(out));
@@ -719,18 +729,18 @@ void replay_plan(Device& backend, const GraphKey& k, const CachedPlan& plan) {
       }
       args.push_back(KernelArg::buf(b));
     }
-    uint64_t l1 = now_ns();
-    realize_stats().ns_lower += l1 - l0;
     realize_stats().lowering_cache_hits++;
+    realize_stats().kernels_launched++;
     if (debug >= 1) {
       size_t kid = g_kernel_count++;
       std::fprintf(stderr, "*** %s %4zu  (plan)           arg %2zu\n", backend.id() == DeviceId::Hip ? "HIP" : "CPU",
                    kid, args.size());
     }
-    backend.execute(*pk.program, args);
-    realize_stats().ns_launch += now_ns() - l1;
-    realize_stats().kernels_launched++;
   }
+  uint64_t l1 = now_ns();
+  realize_stats().ns_lower += l1 - l0;
+  backend.execute_sequence(progs, seq_args, plan.device_state);
+  realize_stats().ns_launch += now_ns() - l1;
   uint64_t t2 = now_ns();
   UOpMap<UOp> repl;
   repl.reserve(plan.replacements.size() * 2);

@@ -146,6 +146,9 @@ struct RealizeStats {
   size_t lowering_cache_hits = 0;
   // Host time (ns) spent in each stage of realize_many / backward.
   uint64_t ns_schedule = 0, ns_lower = 0, ns_launch = 0, ns_apply_map = 0, ns_backward = 0;
+  // Replayed plans that ran as one HIP graph launch, and the launches inside
+  // them whose arguments had to be updated first.
+  size_t graph_replays = 0, graph_updates = 0;
 };
 RealizeStats& realize_stats();
 int debug_level();

@@ -107,6 +107,10 @@ int fg_sgd_free(fg_sgd* s);
 int fg_synchronize(int device);
 int fg_device_context(int device, void** ctx);
 int fg_stats(uint64_t* kernels_launched, uint64_t* programs_compiled, uint64_t* lowering_hits);
+/* Replayed realisation plans that ran as one HIP graph launch, and the
+ * launches in them whose arguments had to be updated (no counterpart in the
+ * reference, which has no graphs). */
+int fg_graph_stats(uint64_t* replays, uint64_t* updated_launches);
 /* Cumulative host nanoseconds in: schedule, lowering-cache/compile, launch,
  * live-tensor rewrite after realisation, backward graph construction. */
 int fg_host_times(uint64_t out[5]);

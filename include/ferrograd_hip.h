@@ -66,6 +66,11 @@ int fg_hip_destroy(fg_ctx* ctx);
  * allocations of the same size; reuse is ordered on the context's stream. */
 int fg_hip_alloc(fg_ctx* ctx, size_t nbytes, int zero, void** dptr);
 int fg_hip_free(fg_ctx* ctx, void* dptr);
+/* fg_hip_alloc that returns the cached free block `hint` when it is free and
+ * of this size, else any block. No counterpart in the reference: a replayed
+ * launch sequence asks for the blocks it used last time, so the addresses its
+ * recorded HIP graph holds stay valid and need no update. */
+int fg_hip_alloc_hint(fg_ctx* ctx, size_t nbytes, int zero, void* hint, void** dptr);
 /* Return cached free blocks to the driver. */
 int fg_hip_trim(fg_ctx* ctx);
 
@@ -91,6 +96,25 @@ int fg_hip_launch(fg_ctx* ctx, fg_prog* prog, const fg_arg* args, int nargs, con
 
 /* Wait for all queued work. */
 int fg_hip_sync(fg_ctx* ctx);
+
+/* Launch sequences replayed as one HIP graph. No counterpart in the reference:
+ * its CPU backend calls each kernel on the host thread (cpu.rs:373-377). A
+ * realisation plan that is replayed every training step launches the same
+ * programs with the same geometry each time; only buffer addresses and scalars
+ * change. fg_hip_graph_create records `n` launches once (progs[i] with
+ * grids[3i..3i+2], blocks[3i..3i+2], lds[i] and nargs[i] arguments taken in
+ * order from `args`) by stream capture of the context's stream; nothing runs.
+ * fg_hip_graph_launch takes the arguments of every launch, concatenated in
+ * launch order, updates the launches whose arguments differ from the previous
+ * replay (their number goes to *updated when it is not NULL), and launches the
+ * graph on the context's stream. While launch
+ * profiling is enabled the launches run one by one instead, so each is timed.
+ * The graph holds no memset or copy nodes. */
+typedef struct fg_graph fg_graph;
+int fg_hip_graph_create(fg_ctx* ctx, int n, fg_prog* const* progs, const unsigned* grids, const unsigned* blocks,
+                        const unsigned* lds, const int* nargs, const fg_arg* args, fg_graph** out);
+int fg_hip_graph_launch(fg_ctx* ctx, fg_graph* graph, const fg_arg* args, int* updated);
+int fg_hip_graph_free(fg_graph* graph);
 
 /* Timing events on the context's stream (slots 0..63). */
 int fg_hip_event_record(fg_ctx* ctx, int slot);

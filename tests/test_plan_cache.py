@@ -109,3 +109,57 @@ def test_disabling_drops_recorded_plans(fg, cpu, fresh_plans):
     assert fg.plan_stats()["entries"] >= 1
     fg.plan_cache(False)
     assert fg.plan_stats()["entries"] == 0
+
+
+@pytest.mark.gpu
+def test_graph_replays_match_direct_launches_hip(fg, hip, fresh_plans):
+    # From its second replay a plan runs as one HIP graph. Every step (with
+    # the loss read back, i.e. a synchronisation, between replays) must match
+    # scheduling afresh with direct launches, bit for bit.
+    before = fg.stats()["graph_replays"]
+    l_on, p_on = train(fg, hip, 8, True)
+    replays = fg.stats()["graph_replays"] - before
+    l_off, p_off = train(fg, hip, 8, False)
+    fg.plan_cache(True)
+    assert replays >= 5
+    assert l_on == l_off
+    for a, b in zip(p_on, p_off):
+        assert np.array_equal(a, b)
+
+
+@pytest.mark.gpu
+def test_graph_replay_with_changing_input_buffers_hip(fg, hip, fresh_plans):
+    # The same two-kernel plan (transpose copy + GEMM with a relu epilogue)
+    # over three different input buffers in turn: each replay updates the
+    # graph's arguments and is checked against float64.
+    r = seeded(3)
+    xs_np = [r.standard_normal((64, 96)).astype(np.float32) for _ in range(3)]
+    w_np = r.standard_normal((96, 80)).astype(np.float32)
+    xs = [fg.Tensor.new(a, [64, 96], hip) for a in xs_np]
+    w = fg.Tensor.new(w_np, [96, 80], hip)
+    before = fg.stats()["graph_replays"]
+    for i in range(9):
+        x = xs_np[i % 3].astype(np.float64)
+        got = xs[i % 3].matmul(w).relu().numpy().reshape(64, 80)
+        want = np.maximum(x @ w_np.astype(np.float64), 0.0)
+        scale = np.abs(x) @ np.abs(w_np).astype(np.float64)
+        assert np.all(np.abs(got - want) <= 1e-4 * scale + 1e-6), i
+    assert fg.stats()["graph_replays"] - before >= 6
+
+
+@pytest.mark.gpu
+def test_steady_state_graph_replays_keep_their_arguments_hip(fg, hip, fresh_plans):
+    # A replayed plan asks the allocator for the blocks its outputs had last
+    # time; once the previous step's tensors are gone it gets them back, so the
+    # recorded graph launches with no argument updates.
+    from ferrograd_amd.mlp import mlp_setup
+
+    step, _ = mlp_setup(fg, hip, batch=64, dims=(784, 64, 10))
+    for _ in range(4):
+        step()
+    s0 = fg.stats()
+    for _ in range(6):
+        step()
+    s1 = fg.stats()
+    assert s1["graph_replays"] - s0["graph_replays"] >= 6
+    assert s1["graph_updated_launches"] - s0["graph_updated_launches"] == 0
