@@ -891,9 +891,12 @@ RenderedKernel render_column_reduce_split(const KernelInfo& ki, const std::strin
   p1.line("const int r0 = chunk * " + std::to_string(CH) + ";");
   p1.line("const int r1 = r0 + " + std::to_string(CH) + " < " + std::to_string(L) + " ? r0 + " + std::to_string(CH) +
           " : " + std::to_string(L) + ";");
-  p1.open_scope("if (active) for (int rr = r0 + tr; rr < r1; rr += " + std::to_string(TR) + ") {", "}");
+  p1.open_scope("if (active) {", "}");
+  p1.line("#pragma unroll 8");
+  p1.open_scope("for (int rr = r0 + tr; rr < r1; rr += " + std::to_string(TR) + ") {", "}");
   p1.define_range(r, "rr");
   for (int u = 0; u < V; u++) p1.line(accs[u] + " = " + combine(rop, accs[u], p1.val(R.src(0), u)) + ";");
+  p1.close_scope();
   p1.close_scope();
   p1.line(std::string("__shared__ ") + ctype(dt) + " fg_col[" + std::to_string(TR) + "][" + std::to_string(TX * V) + "];");
   for (int u = 0; u < V; u++)
@@ -912,10 +915,14 @@ RenderedKernel render_column_reduce_split(const KernelInfo& ki, const std::strin
   }
   p1.line("}");
 
-  // Pass 2: fold partials in chunk order, epilogue, store.
+  // Pass 2: one wave per group of V outputs. Lane l folds chunks l, l+64, ...
+  // in order, then a fixed wave tree combines the lanes (deterministic); every
+  // lane evaluates the epilogue and lane 0 stores. A thread per output folding
+  // all chunks serially was latency-bound (15 us for 64 chunks of 4096 sums).
   Emitter p2;
-  int64_t threads = NOUT / V;
-  p2.line("const long gid = (long)blockIdx.x * 256 + threadIdx.x;");
+  int64_t threads = NOUT / V;  // output groups, one wave each
+  p2.line("const long gid = (long)blockIdx.x * 4 + (threadIdx.x >> 6);");
+  p2.line("const int lane = threadIdx.x & 63;");
   p2.line("if (gid >= " + std::to_string(threads) + "L) return;");
   int64_t per = fext / V;
   p2.line("const int fbase = (int)(gid % " + std::to_string(per) + ") * " + std::to_string(V) + ";");
@@ -927,16 +934,17 @@ RenderedKernel render_column_reduce_split(const KernelInfo& ki, const std::strin
     FG_CHECK(RR == R, "column reduce renders exactly one reduction");
     std::string acc = "facc" + std::to_string(lane);
     std::string lin = "orest * " + std::to_string(fext) + "L + fbase + " + std::to_string(lane);
-    p2.line(std::string(ctype(dt)) + " " + acc + " = fg_scratch[" + lin + "];");
-    p2.line("for (int c = 1; c < " + std::to_string(nchunks) + "; c++) " + acc + " = " +
+    p2.line(std::string(ctype(dt)) + " " + acc + " = " + init_lit(rop, dt) + ";");
+    p2.line("for (int c = lane; c < " + std::to_string(nchunks) + "; c += 64) " + acc + " = " +
             combine(rop, acc, "fg_scratch[(long)c * " + std::to_string(NOUT) + "L + " + lin + "]") + ";");
+    p2.line(wave_reduce(acc, 64, rop, dt));
     p2.remember_here(RR, lane, acc);
     return acc;
   };
   std::vector<std::string> vals;
   for (int u = 0; u < V; u++) vals.push_back(p2.val(ki.value, u));
   for (int u = 0; u < V; u++)
-    p2.line(pname(ki.out_param) + "[" + p2.idx(ki.out_index, u) + "] = " + vals[u] + ";");
+    p2.line("if (lane == 0) " + pname(ki.out_param) + "[" + p2.idx(ki.out_index, u) + "] = " + vals[u] + ";");
 
   RenderedKernel rk;
   rk.name = name;
@@ -948,7 +956,7 @@ RenderedKernel render_column_reduce_split(const KernelInfo& ki, const std::strin
   a.grid[0] = static_cast<unsigned>(per_f * other * nchunks);
   a.block[0] = 256;
   b.func = name + "_fin";
-  b.grid[0] = static_cast<unsigned>((threads + 255) / 256);
+  b.grid[0] = static_cast<unsigned>((threads + 3) / 4);
   b.block[0] = 256;
   rk.launches = {a, b};
   rk.scratch_bytes = static_cast<size_t>(nchunks * NOUT) * dt.size_bytes();
