@@ -350,7 +350,7 @@ def main():
 
     cpu = {}
     if not args.no_cpu:
-        for c in sorted(only & {"c1", "c2", "c3", "c4"}):
+        for c in sorted(only & {"c1", "c2", "c3", "c4", "c5"}):
             cpu[c] = cpu_baseline(c)
             log(f"cpu {c}: {cpu[c]}")
     for c, v in cpu.items():

@@ -7,8 +7,10 @@ this package; the product (ferrograd_amd) never does. Two parts:
   the reference's clang backend (src/device/cpu.rs, src/codegen/clang.rs and
   the lane semantics of src/expand.rs + src/devectorize.rs), so any program
   built with ferrograd_amd runs on "cpu" exactly as the reference would run it.
-* `reference.py`: closed-form numpy restatements of the benchmark configs and
-  the reference's known-answer values, used to pin the CPU device.
+  The tests pin it against the reference's known answers and against float64
+  restatements of the benchmark configs.
+* `cpu_bench.py`: the CPU baseline leg of bench.py (the device above, timed on
+  one pinned core).
 
 The reference (Rust) cannot be compiled here (no cargo/rustc, crates need a
 network fetch), so there is no oracle/_ref build.

@@ -5,7 +5,7 @@ clang -shared -O3 -march=native, one call per kernel on the calling thread,
 cpu.rs:151-208, 328-380) on a bounded sample of a benchmark config, pinned to
 one core like the reference. Prints one JSON object.
 
-Usage: python -m oracle.cpu_bench <c1|c2|c3|c4> [--core N]
+Usage: python -m oracle.cpu_bench <c1|c2|c3|c4|c5> [--core N]
 """
 from __future__ import annotations
 
@@ -82,6 +82,25 @@ def main() -> None:
         step, _ = mlp_setup(fg, dev, batch=256, dims=(784, 128, 10))
         t = _time(step, runs=10, warmup=2)
         out.update(value=1.0 / t, unit="steps/s", seconds=t, sample="C4 train step, median of 10 after 2 warmup")
+    elif args.config == "c5":
+        # A C5 step on one core takes about 25 minutes. Every GEMM of the step
+        # scales with the batch and the SGD update does not, so time steps at
+        # the full layer widths for two batches and extrapolate t(B) = a + b*B.
+        # Measured on one core: 1.1, 2.2, 8.7 and 20 s at B = 16, 32, 64, 128.
+        # Up to B = 32 the activations stay in cache; from B = 64 on the time
+        # grows linearly, so the fit uses 64 and 128.
+        from ferrograd_amd.mlp import mlp_setup
+
+        ts = {}
+        for batch in (64, 128):
+            step, _ = mlp_setup(fg, dev, batch=batch, dims=(784, 4096, 4096, 10))
+            ts[batch] = _time(step, runs=1, warmup=1)
+        b = (ts[128] - ts[64]) / 64.0
+        a = ts[64] - 64.0 * b
+        t = a + 8192.0 * b
+        out.update(value=1.0 / t, unit="steps/s", seconds=t, sample_seconds={str(k): v for k, v in ts.items()},
+                   sample="C5 widths (784->4096->4096->10) at B=64 and B=128, one step each after 1 warmup; "
+                          "step time extrapolated linearly in B to B=8192")
     else:
         raise SystemExit(f"unknown config {args.config}")
     print(json.dumps(out))
