@@ -249,23 +249,45 @@ COPY_SRC = r"""
 extern "C" __global__ void __launch_bounds__(256) fg_copy_probe(float4* __restrict__ dst, const float4* __restrict__ src, int n4) {
   const int i = blockIdx.x * 256 + threadIdx.x;
   if (i < n4) dst[i] = src[i];
+}
+typedef float fg_probe_f4 __attribute__((ext_vector_type(4)));
+extern "C" __global__ void __launch_bounds__(256) fg_copy_probe_nt(fg_probe_f4* __restrict__ dst, const fg_probe_f4* __restrict__ src, int n4) {
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  if (i < n4) __builtin_nontemporal_store(__builtin_nontemporal_load(src + i), dst + i);
 }"""
 
 
 def copy_probe(nbytes: int = 1 << 30, reps: int = 5) -> None:
     """Launch a plain copy of `nbytes` (read + write) `reps` times: the
     reference kernel whose FETCH_SIZE / WRITE_SIZE counters calibrate the
-    byte counts of the generated kernels under rocprofv3 --pmc."""
+    byte counts of the generated kernels under rocprofv3 --pmc. Also times it,
+    and a non-temporal copy, with events: the practical streaming ceiling the
+    HBM-bound kernels are compared with (3 source/destination pairs rotate so
+    the 256 MB Infinity Cache cannot hold a launch's data)."""
     from ferrograd_amd.hip import Arg, Context
 
     ctx = Context(0)
-    src, dst = ctx.alloc(nbytes), ctx.alloc(nbytes)
+    pairs = [(ctx.alloc(nbytes), ctx.alloc(nbytes)) for _ in range(3)]
     prog = ctx.compile(COPY_SRC, "fg_copy_probe", 3)
     n4 = nbytes // 16
+    grid, block = ((n4 + 255) // 256, 1, 1), (256, 1, 1)
     for _ in range(reps):
-        ctx.launch(prog, [Arg.ptr(dst), Arg.ptr(src), Arg.i32(n4)], grid=((n4 + 255) // 256, 1, 1), block=(256, 1, 1))
+        src, dst = pairs[0]
+        ctx.launch(prog, [Arg.ptr(dst), Arg.ptr(src), Arg.i32(n4)], grid=grid, block=block)
     ctx.sync()
-    print(json.dumps({"copy_probe_bytes_read": nbytes, "copy_probe_bytes_written": nbytes, "launches": reps}))
+    rates = {}
+    for name in ("fg_copy_probe", "fg_copy_probe_nt"):
+        p = ctx.compile(COPY_SRC, name, 3)
+        ms = []
+        for i in range(3 + 20):
+            src, dst = pairs[i % 3]
+            ctx.record(0)
+            ctx.launch(p, [Arg.ptr(dst), Arg.ptr(src), Arg.i32(n4)], grid=grid, block=block)
+            ctx.record(1)
+            if i >= 3:
+                ms.append(ctx.elapsed_ms(0, 1))
+        rates[name + "_gbs"] = 2 * nbytes / (float(np.mean(ms)) / 1e3) / 1e9
+    print(json.dumps({"copy_probe_bytes_read": nbytes, "copy_probe_bytes_written": nbytes, "launches": reps, **rates}))
 
 
 def library_compare() -> None:

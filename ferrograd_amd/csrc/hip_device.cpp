@@ -241,9 +241,13 @@ class HipDevice : public Device {
     if (ctx_) check(fg_hip_sync(ctx_), "fg_hip_sync");
   }
 
+  // FG_FUSE=0 keeps the reference's kernel partition (read once per process).
   bool fuse_elementwise() const override {
-    const char* e = std::getenv("FG_FUSE");
-    return !(e && std::strcmp(e, "0") == 0);
+    static const bool on = [] {
+      const char* e = std::getenv("FG_FUSE");
+      return !(e && std::strcmp(e, "0") == 0);
+    }();
+    return on;
   }
 
  private:
