@@ -150,13 +150,17 @@ class Tensor:
     def __del__(self):
         if _lib is not None and self._h:
             _lib.fg_tensor_free(self._h)
-            self._h = ctypes.c_void_p()
 
     @staticmethod
     def _out(fn, *args) -> "Tensor":
+        # Hot path of every op: one ctypes call, and the returned handle
+        # object becomes the tensor's handle as is.
         out = ctypes.c_void_p()
-        _check(fn(*args, ctypes.byref(out)))
-        return Tensor(out.value)
+        if fn(*args, ctypes.byref(out)):
+            raise FerrogradError(_lib.fg_last_error().decode())
+        t = Tensor.__new__(Tensor)
+        t._h = out
+        return t
 
     # ── construction (tensor.rs:260-312) ─────────────────────────────────
     @staticmethod
@@ -252,11 +256,13 @@ class Tensor:
         return bool(s.value)
 
     # ── elementwise (tensor.rs:442-531) ──────────────────────────────────
+    # A Tensor exists only once the library is loaded, so its methods use
+    # `_lib` directly.
     def _u(self, op: int) -> "Tensor":
-        return Tensor._out(lib().fg_tensor_unary, self._h, op)
+        return Tensor._out(_lib.fg_tensor_unary, self._h, op)
 
     def _b(self, other: "Tensor", op: int) -> "Tensor":
-        return Tensor._out(lib().fg_tensor_binary, self._h, other._h, op)
+        return Tensor._out(_lib.fg_tensor_binary, self._h, other._h, op)
 
     def neg(self): return self._u(0)
     def reciprocal(self): return self._u(1)
@@ -277,22 +283,22 @@ class Tensor:
     # ── movement / reductions (tensor.rs:539-752) ────────────────────────
     def reshape(self, shape):
         s, n = _i64(shape)
-        return Tensor._out(lib().fg_tensor_movement, self._h, 0, s, n)
+        return Tensor._out(_lib.fg_tensor_movement, self._h, 0, s, n)
 
     def permute(self, order):
         s, n = _i64(order)
-        return Tensor._out(lib().fg_tensor_movement, self._h, 1, s, n)
+        return Tensor._out(_lib.fg_tensor_movement, self._h, 1, s, n)
 
     def expand(self, shape):
         s, n = _i64(shape)
-        return Tensor._out(lib().fg_tensor_movement, self._h, 2, s, n)
+        return Tensor._out(_lib.fg_tensor_movement, self._h, 2, s, n)
 
     def narrow(self, dim: int, start: int, length: int):
         return Tensor._out(lib().fg_tensor_narrow, self._h, dim, start, length)
 
     def sum(self, axes):
         s, n = _i64(axes)
-        return Tensor._out(lib().fg_tensor_reduce, self._h, 0, s, n)
+        return Tensor._out(_lib.fg_tensor_reduce, self._h, 0, s, n)
 
     def max(self, axes):
         s, n = _i64(axes)
@@ -317,7 +323,8 @@ class Tensor:
         _check(lib().fg_tensor_realize_many(arr, len(tensors)))
 
     def realize(self) -> "Tensor":
-        Tensor.realize_many([self])
+        if _lib.fg_tensor_realize_many(ctypes.byref(self._h), 1):  # a one-element fg_tensor* array
+            raise FerrogradError(_lib.fg_last_error().decode())
         return self
 
     def numpy(self) -> np.ndarray:
@@ -382,7 +389,7 @@ class Linear:
         self.bias = ps[1] if len(ps) > 1 else None
 
     def forward(self, x: Tensor) -> Tensor:
-        return Tensor._out(lib().fg_linear_forward, self._h, x._h)
+        return Tensor._out(_lib.fg_linear_forward, self._h, x._h)
 
     __call__ = forward
 

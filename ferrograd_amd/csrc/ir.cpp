@@ -565,9 +565,11 @@ UOp substitute_with_map(const UOp& root, const UOpMap<UOp>& replacements) {
 std::vector<UOp> substitute_many(const std::vector<UOp>& roots, const UOpMap<UOp>& replacements) {
   // Memo: node -> index into `done` (its substituted value). The walk stops at
   // replaced nodes, so the graph beneath them is never visited.
-  PtrIndexMap memo(1024);
+  // Sized for the common case (realised leaves and short lazy graphs); both
+  // grow on demand.
+  PtrIndexMap memo(64);
   std::vector<UOp> done;
-  done.reserve(1024);
+  done.reserve(64);
   std::vector<std::pair<const UOp*, bool>> stack;
   std::vector<UOp> out;
   out.reserve(roots.size());

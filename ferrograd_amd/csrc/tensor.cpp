@@ -467,11 +467,11 @@ void key_word(GraphKey& k, uint64_t w) { k.code.push_back(w); }
 GraphKey graph_key(const std::vector<UOp>& roots, bool fuse) {
   GraphKey k;
   const UOp sink = UOp::sink(roots);
-  PtrIndexMap pos(1024);
-  PtrIndexMap leaf(64);
-  k.order.reserve(1024);
+  PtrIndexMap pos(128);  // grows on demand
+  PtrIndexMap leaf(32);
+  k.order.reserve(128);
   std::vector<std::pair<const UOp*, bool>> stack;
-  stack.reserve(256);
+  stack.reserve(64);
   stack.emplace_back(&sink, false);
   bool has_bind = false;
   while (!stack.empty()) {
