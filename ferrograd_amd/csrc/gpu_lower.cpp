@@ -1123,7 +1123,7 @@ int64_t gemm_tile_residency(const GemmTile& t) {
 // comparison):
 // - MFMA-bound shapes: 256x256 with four 128x128 waves and BK 32 ran 4096^3 at
 //   134.8-137.6 TFLOP/s (hipBLASLt 138.9-142.8), 256x128 and 128x256 at 129,
-//   128x128 at 127. The shape and split count are chosen by estimated time:
+//   128x128 at 127. The shape, k-tile and split count are chosen by estimated time:
 //   rounds of resident workgroups times the MFMA time of one tile's K range
 //   (padding included, at each shape's measured efficiency), plus the traffic
 //   of split-K partials. For dW1 of the C5 MLP (4096x784, K 8192) that picks
@@ -1166,9 +1166,13 @@ GemmTile choose_gemm_tile(int64_t M, int64_t N, int64_t K) {
     GemmTile t;
     double eff;  // measured throughput relative to 256x256
   };
-  const Cand cands[] = {{{256, 256, 32, 2, 2}, 1.0}, {{256, 128, 32, 2, 2}, 0.9}, {{128, 256, 32, 2, 2}, 0.9},
-                        {{128, 128, 32, 2, 2}, 0.92}, {{64, 64, 32, 2, 2}, 0.6}};
-  GemmTile best = with_splits(cands[4].t, 1);
+  // Each shape with BK 32 and BK 16. BK 16 pads a K that is not a multiple of
+  // 32 less: the 8192x4096 forward with K 784 (49 k-tiles of 16) took 399 us
+  // against 424 us with BK 32; for K 4096 BK 32 was about 2% faster.
+  const Cand cands[] = {{{256, 256, 32, 2, 2}, 1.0},   {{256, 256, 16, 2, 2}, 0.99}, {{256, 128, 32, 2, 2}, 0.9},
+                        {{256, 128, 16, 2, 2}, 0.89},  {{128, 256, 32, 2, 2}, 0.9},  {{128, 256, 16, 2, 2}, 0.89},
+                        {{128, 128, 32, 2, 2}, 0.92},  {{128, 128, 16, 2, 2}, 0.91}, {{64, 64, 32, 2, 2}, 0.6}};
+  GemmTile best = with_splits(cands[8].t, 1);
   double best_s = 1e30;
   for (const Cand& c : cands) {
     if (M < c.t.BM / 2 || N < c.t.BN / 2) continue;  // mostly padding
