@@ -63,6 +63,7 @@ def api() -> ctypes.CDLL:
             "fg_hip_init": (c_int, [c_int, PP]),
             "fg_hip_destroy": (c_int, [P]),
             "fg_hip_alloc": (c_int, [P, c_size, c_int, PP]),
+            "fg_hip_alloc_hint": (c_int, [P, c_size, c_int, P, PP]),
             "fg_hip_free": (c_int, [P, P]),
             "fg_hip_trim": (c_int, [P]),
             "fg_hip_copy_h2d": (c_int, [P, P, P, c_size]),
@@ -73,6 +74,11 @@ def api() -> ctypes.CDLL:
             "fg_hip_program_num_args": (c_int, [P]),
             "fg_hip_launch": (c_int, [P, P, ctypes.POINTER(Arg), c_int, uint3, uint3, ctypes.c_uint]),
             "fg_hip_sync": (c_int, [P]),
+            "fg_hip_graph_create": (c_int, [P, c_int, PP, ctypes.POINTER(ctypes.c_uint), ctypes.POINTER(ctypes.c_uint),
+                                            ctypes.POINTER(ctypes.c_uint), ctypes.POINTER(c_int), ctypes.POINTER(Arg),
+                                            PP]),
+            "fg_hip_graph_launch": (c_int, [P, P, ctypes.POINTER(Arg), ctypes.POINTER(c_int)]),
+            "fg_hip_graph_free": (c_int, [P]),
             "fg_hip_event_record": (c_int, [P, c_int]),
             "fg_hip_event_elapsed_ms": (c_int, [P, c_int, c_int, ctypes.POINTER(ctypes.c_float)]),
             "fg_hip_device_info": (c_int, [P, ctypes.POINTER(c_int), ctypes.POINTER(c_int), ctypes.POINTER(c_size),
@@ -143,6 +149,13 @@ class Context:
         check(api().fg_hip_alloc(self.h, nbytes, int(zero), ctypes.byref(p)))
         return p.value
 
+    def alloc_hint(self, nbytes: int, hint: int, zero: bool = False) -> int:
+        """fg_hip_alloc_hint: the cached free block `hint` when it is free and
+        of this size, else any block."""
+        p = ctypes.c_void_p()
+        check(api().fg_hip_alloc_hint(self.h, nbytes, int(zero), hint, ctypes.byref(p)))
+        return p.value
+
     def free(self, p: int) -> None:
         check(api().fg_hip_free(self.h, p))
 
@@ -165,6 +178,32 @@ class Context:
 
     def sync(self) -> None:
         check(api().fg_hip_sync(self.h))
+
+    def graph_create(self, launches) -> int:
+        """Record launches [(prog, args, grid, block, lds), ...] as one HIP
+        graph (fg_hip_graph_create); returns the graph handle."""
+        n = len(launches)
+        progs = (ctypes.c_void_p * n)(*[l[0] for l in launches])
+        grids = (ctypes.c_uint * (3 * n))(*[g for l in launches for g in l[2]])
+        blocks = (ctypes.c_uint * (3 * n))(*[b for l in launches for b in l[3]])
+        lds = (ctypes.c_uint * n)(*[l[4] for l in launches])
+        nargs = (ctypes.c_int * n)(*[len(l[1]) for l in launches])
+        flat = [a for l in launches for a in l[1]]
+        args = (Arg * max(1, len(flat)))(*flat)
+        g = ctypes.c_void_p()
+        check(api().fg_hip_graph_create(self.h, n, progs, grids, blocks, lds, nargs, args, ctypes.byref(g)))
+        return g.value
+
+    def graph_launch(self, graph: int, args) -> int:
+        """Launch a recorded graph with every launch's arguments (concatenated);
+        returns how many launches had to be updated."""
+        arr = (Arg * max(1, len(args)))(*args)
+        updated = ctypes.c_int()
+        check(api().fg_hip_graph_launch(self.h, graph, arr, ctypes.byref(updated)))
+        return updated.value
+
+    def graph_free(self, graph: int) -> None:
+        check(api().fg_hip_graph_free(graph))
 
     def record(self, slot: int) -> None:
         check(api().fg_hip_event_record(self.h, slot))

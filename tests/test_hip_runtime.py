@@ -165,3 +165,61 @@ def test_events_time_kernels(ctx):
     ctx.launch(prog, [Arg.ptr(a), Arg.ptr(b), Arg.ptr(o), Arg.i32(n)], grid=(n // 256, 1, 1), block=(256, 1, 1))
     ctx.record(1)
     assert ctx.elapsed_ms(0, 1) > 0.0
+
+
+# ── HIP-graph replay and allocator hints (no counterpart in the reference) ──
+
+AXPY = r"""
+extern "C" __global__ void axpy(float* y, const float* x, float a, int n) {
+  int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) y[i] = y[i] * a + x[i];
+}"""
+
+
+def test_graph_replays_launches_in_order_with_updated_arguments(ctx):
+    from ferrograd_amd.hip import Arg
+
+    n = 1000
+    prog = ctx.compile(AXPY, "axpy", 4)
+    x1 = _upload(ctx, np.arange(n, dtype=np.float32))
+    x2 = _upload(ctx, np.full(n, 2.0, np.float32))
+    ya = _upload(ctx, np.ones(n, np.float32))
+    yb = _upload(ctx, np.zeros(n, np.float32))
+    grid, block = ((n + 255) // 256, 1, 1), (256, 1, 1)
+    # y = (y * 3 + x1) * 0.5 + x2: two dependent launches, order matters.
+    seq = lambda y, a: [(prog, [Arg.ptr(y), Arg.ptr(x1), Arg.f32(a), Arg.i32(n)], grid, block, 0),  # noqa: E731
+                        (prog, [Arg.ptr(y), Arg.ptr(x2), Arg.f32(0.5), Arg.i32(n)], grid, block, 0)]
+    g = ctx.graph_create(seq(ya, 3.0))  # records only: nothing runs
+    assert np.array_equal(_download(ctx, ya, n), np.ones(n, np.float32))
+    flat = lambda s: [a for l in s for a in l[1]]  # noqa: E731
+    assert ctx.graph_launch(g, flat(seq(ya, 3.0))) == 0
+    want = (np.ones(n, np.float32) * 3 + np.arange(n, dtype=np.float32)) * np.float32(0.5) + 2
+    assert np.array_equal(_download(ctx, ya, n), want.astype(np.float32))
+    # Another buffer and scalar: the first launch is updated, the second too (y).
+    assert ctx.graph_launch(g, flat(seq(yb, -1.0))) == 2
+    want_b = (np.zeros(n, np.float32) * -1 + np.arange(n, dtype=np.float32)) * np.float32(0.5) + 2
+    assert np.array_equal(_download(ctx, yb, n), want_b.astype(np.float32))
+    assert np.array_equal(_download(ctx, ya, n), want.astype(np.float32))  # untouched
+    ctx.graph_free(g)
+
+
+def test_graph_create_rejects_a_wrong_argument_count(ctx):
+    from ferrograd_amd.hip import Arg, HipError
+
+    prog = ctx.compile(AXPY, "axpy", 4)
+    y = ctx.alloc(16)
+    with pytest.raises(HipError, match="wrong argument count"):
+        ctx.graph_create([(prog, [Arg.ptr(y), Arg.f32(1.0)], (1, 1, 1), (64, 1, 1), 0)])
+
+
+def test_alloc_hint_returns_the_hinted_free_block(ctx):
+    a, b = ctx.alloc(1 << 20, zero=False), ctx.alloc(1 << 20, zero=False)
+    ctx.free(a)
+    ctx.free(b)  # the LIFO free list would hand out b first
+    assert ctx.alloc_hint(1 << 20, a) == a
+    assert ctx.alloc_hint(1 << 20, 0) == b
+    ctx.free(a)
+    ctx.free(b)
+    c = ctx.alloc_hint(1 << 21, a)  # another size: the hint does not apply
+    assert c not in (a, b)
+    ctx.free(c)
