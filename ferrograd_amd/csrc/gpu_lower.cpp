@@ -1694,6 +1694,16 @@ KernelClass classify_kernel(const UOp& kernel) {
 
 RenderedKernel render_hip(const UOp& kernel, const std::string& name, int force_class) {
   KernelInfo ki = analyze_kernel(kernel);
+  // Kernel indexes are int32, as rangeify builds them (schedule/indexing.rs:
+  // 42-62 multiplies i32 ranges by i32 strides). A buffer of 2^31 or more
+  // elements would wrap: refuse it rather than index out of bounds.
+  for (auto& [slot, p] : ki.params)
+    if (p.op() == Op::ParamBuffer)
+      FG_CHECK(p.arg().b < (int64_t(1) << 31), "buffer data" + std::to_string(slot) + " has " +
+                                                   std::to_string(p.arg().b) +
+                                                   " elements; kernel indexes are int32 (at most 2^31-1 elements)");
+  FG_CHECK(total_outputs(ki) < (int64_t(1) << 31), "kernel has " + std::to_string(total_outputs(ki)) +
+                                                         " outputs; kernel indexes are int32 (at most 2^31-1)");
   FG_CHECK(!reads_dest_elsewhere(ki),
            "in-place update reads its destination at another index; the HIP device runs kernels in parallel and "
            "cannot reproduce the sequential CPU order");

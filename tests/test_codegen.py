@@ -115,6 +115,13 @@ def test_reshape_of_permuted_view_is_an_error_not_a_crash(fg, cpu):
         hip_plan(fg, [w.permute([1, 0]).reshape([4]).add(fg.Tensor.new(np.ones(4, np.float32), [4], cpu))])
 
 
+def test_kernels_beyond_int32_indexing_are_refused(fg, cpu):
+    # 2^32 outputs from a broadcast scalar: no storage is allocated to plan it.
+    s = fg.Tensor.new([1.0], [1], cpu).reshape([1, 1]).expand([1 << 16, 1 << 16])
+    with pytest.raises(fg.FerrogradError, match="int32"):
+        hip_plan(fg, [s.add(s)])
+
+
 def test_float_literals_match_reference_text(fg, cpu):
     x = fg.Tensor.new(np.ones(8, np.float32), [8], cpu)
     items = hip_plan(fg, [x.exp()])
