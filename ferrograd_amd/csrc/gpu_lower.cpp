@@ -327,13 +327,15 @@ class Emitter {
   }
 
   // Vectorised load check: unit stride along the lane range, every other
-  // term a multiple of 4 (16-byte aligned for 4-byte elements).
+  // term a multiple of 4 (16-byte aligned for 4-byte elements). Kernel-scalar
+  // terms are int32 values, so a coefficient that is a multiple of 4 keeps
+  // the alignment too.
   bool vec4_load(const UOp& load) {
     if (lanes_ != 4 || !lane_range_) return false;
     DType dt = load.dtype();
     if (dt.kind != DTypeKind::F32 && dt.kind != DTypeKind::I32) return false;
     Affine a = affine_of(load.src(0).src(1));
-    if (!a.ok || a.has_scalar_terms() || a.c0 % 4 != 0) return false;
+    if (!a.ok || a.c0 % 4 != 0) return false;
     bool unit = false;
     for (auto& t : a.terms) {
       if (t.first.get() == lane_range_) unit = t.second == 1;
@@ -669,7 +671,7 @@ RenderedKernel render_elementwise(const KernelInfo& ki, const std::string& name)
   if (V == 4) {
     Affine a = affine_of(ki.out_index);
     DType dt = ki.out_param.dtype();
-    vstore = a.ok && !a.has_scalar_terms() && a.coef(fast) == 1 && a.c0 % 4 == 0 &&
+    vstore = a.ok && a.coef(fast) == 1 && a.c0 % 4 == 0 &&
              (dt.kind == DTypeKind::F32 || dt.kind == DTypeKind::I32);
     for (auto& t : a.terms)
       if (t.first != fast && t.second % 4 != 0) vstore = false;
@@ -726,7 +728,7 @@ RenderedKernel render_row_reduce(const KernelInfo& ki, const std::string& name) 
       Affine a = affine_of(ld.src(0).src(1));
       int64_t c = a.ok ? a.coef(r_in) : -1;
       if (c == 0) continue;
-      bool ok = a.ok && !a.has_scalar_terms() && c == 1 && a.c0 % 4 == 0 &&
+      bool ok = a.ok && c == 1 && a.c0 % 4 == 0 &&
                 (ld.dtype().kind == DTypeKind::F32 || ld.dtype().kind == DTypeKind::I32);
       for (auto& t : a.terms)
         if (t.first != r_in && t.second % 4 != 0) ok = false;
@@ -1080,8 +1082,11 @@ bool gemm_operand(const UOp& e, const UOp& rk, const KernelInfo& ki, GemmOperand
   }
   for (auto& ld : lds) {
     if (ld.src(0).src(0) == ki.out_param) return false;  // in-place tiles would race
+    // Kernel-scalar terms (narrow() starts, schedule.rs:217-239) may appear:
+    // staging only uses the range coefficients; vector loads need every
+    // scalar coefficient to be a multiple of 4, like any other term.
     Affine a = affine_of(ld.src(0).src(1));
-    if (!a.ok || a.has_scalar_terms()) return false;
+    if (!a.ok) return false;
     if (!have_lead && a.coef(rk) != 0) {
       op->lead = a;
       have_lead = true;
@@ -1576,7 +1581,7 @@ RenderedKernel render_gemm(const KernelInfo& ki, const GemmMatch& g, const std::
       std::vector<std::string> vals;
       for (int u = 0; u < 4; u++) vals.push_back(em.val(ki.value, u));
       Affine ao = affine_of(ki.out_index);
-      bool vstore = ao.ok && !ao.has_scalar_terms() && ao.coef(g.rn) == 1 && ao.c0 % 4 == 0 &&
+      bool vstore = ao.ok && ao.coef(g.rn) == 1 && ao.c0 % 4 == 0 &&
                     ki.out_param.dtype().kind == DTypeKind::F32;
       for (auto& t : ao.terms)
         if (t.first != g.rn && t.second % 4 != 0) vstore = false;

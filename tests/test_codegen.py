@@ -102,6 +102,19 @@ def test_train_step_kernels_compile_and_use_mfma(fg, cpu, batch, dims):
         compile_only(fg, it["source"], it["name"])
 
 
+def test_narrowed_operands_stay_on_mfma_with_vector_loads(fg, cpu):
+    # A batch taken with narrow() carries its start as a kernel scalar; a
+    # start times the 784-float row stride keeps 16-byte alignment.
+    x = fg.Tensor.new(np.ones((1024, 784), np.float32), [1024, 784], cpu).narrow(0, 256, 256)
+    w = fg.Tensor.new(np.ones((128, 784), np.float32), [128, 784], cpu)
+    items = hip_plan(fg, [x.matmul(w.permute([1, 0]))])
+    gemm = [it for it in items if it["class"] == "gemm_mfma_f32"]
+    assert len(gemm) == 1
+    src = gemm[0]["source"]
+    assert "*(const fg_f4*)(data" in src and "_part(" in src
+    compile_only(fg, src, gemm[0]["name"] + "_part")
+
+
 def test_in_place_update_reading_other_indices_is_rejected(fg, cpu):
     w = fg.Tensor.new(np.arange(4, dtype=np.float32), [2, 2], cpu)
     w.assign(w.add(w.permute([1, 0])))

@@ -170,7 +170,10 @@ def test_c3_linear_forward(fg, cpu, mnk):
     assert rel_err_bound(got, exact, scale, 1e-4) <= 1.0
 
 
-def mlp_step(fg, dev, x, t, hidden, seed=42, lr=0.01, steps=1):
+def mlp_step(fg, dev, x, t, hidden, seed=42, lr=0.01, steps=1, starts=None, batch=None):
+    """`steps` SGD steps; with `starts`, step i trains on rows
+    [starts[i], starts[i] + batch) of the resident x/t through narrow(), the
+    batching of examples/mnist.rs:46-62."""
     fg.reset_init_seed(seed)
     dims = [x.shape[1]] + list(hidden) + [t.shape[1]]
     layers = [fg.Linear(dims[i], dims[i + 1], dev) for i in range(len(dims) - 1)]
@@ -179,13 +182,14 @@ def mlp_step(fg, dev, x, t, hidden, seed=42, lr=0.01, steps=1):
     tx = fg.Tensor.new(x, list(x.shape), dev)
     tt = fg.Tensor.new(t, list(t.shape), dev)
     losses = []
-    for _ in range(steps):
-        h = tx
+    for i in range(steps if starts is None else len(starts)):
+        h = tx if starts is None else tx.narrow(0, starts[i], batch)
+        ts = tt if starts is None else tt.narrow(0, starts[i], batch)
         for i, l in enumerate(layers):
             h = l(h)
             if i + 1 < len(layers):
                 h = h.relu()
-        loss = h.cross_entropy(tt)
+        loss = h.cross_entropy(ts)
         opt.zero_grad()
         loss.backward()
         opt.step()
@@ -200,6 +204,20 @@ def test_mlp_train_step(fg, cpu, batch, hidden, steps):
     labels = np.floor(r.uniform(0, 1, batch) * 10).astype(np.int64)
     t = np.eye(10, dtype=np.float32)[labels]
     (lc, pc), (lh, ph) = both(lambda d: mlp_step(fg, d, x, t, hidden, steps=steps), cpu)
+    np.testing.assert_allclose(lh, lc, rtol=1e-4)
+    for a, b in zip(ph, pc):
+        np.testing.assert_allclose(a, b, rtol=1e-4, atol=1e-6)
+
+
+def test_mlp_steps_on_narrowed_batches(fg, cpu):
+    # Kernel-scalar row starts inside the MFMA operands of the forward and dW
+    # products; the start changes every step while the plan replays.
+    r = seeded(11)
+    x = r.uniform(0, 1, (1024, 784)).astype(np.float32)
+    labels = np.floor(r.uniform(0, 1, 1024) * 10).astype(np.int64)
+    t = np.eye(10, dtype=np.float32)[labels]
+    starts = [0, 256, 512, 768, 256]
+    (lc, pc), (lh, ph) = both(lambda d: mlp_step(fg, d, x, t, (128,), starts=starts, batch=256), cpu)
     np.testing.assert_allclose(lh, lc, rtol=1e-4)
     for a, b in zip(ph, pc):
         np.testing.assert_allclose(a, b, rtol=1e-4, atol=1e-6)
