@@ -95,6 +95,7 @@ def _declare(l: ctypes.CDLL) -> None:
         "fg_host_times": (c_int, [ctypes.POINTER(ctypes.c_uint64)]),
         "fg_plan_cache_enable": (c_int, [c_int]),
         "fg_plan_cache_stats": (c_int, [ctypes.POINTER(ctypes.c_uint64)] * 3),
+        "fg_set_graph_min_launches": (c_int, [c_int, ctypes.POINTER(c_int)]),
         "fg_debug_plan": (c_int, [PP, c_int, c_int, c_int, ctypes.c_char_p, c_size, ctypes.POINTER(c_size)]),
     }
     for name, (res, args) in sigs.items():
@@ -452,6 +453,14 @@ def clear_caches() -> None:
 def plan_cache(enabled: bool) -> None:
     """Turn realisation-plan replay on or off (off also drops recorded plans)."""
     _check(lib().fg_plan_cache_enable(int(enabled)))
+
+
+def graph_min_launches(n: int) -> int:
+    """Record replayed plans of at least `n` launches (n >= 2) as HIP graphs;
+    shorter ones launch one by one. Returns the previous threshold."""
+    prev = ctypes.c_int()
+    _check(lib().fg_set_graph_min_launches(int(n), ctypes.byref(prev)))
+    return prev.value
 
 
 def plan_stats() -> dict:

@@ -379,6 +379,13 @@ int fg_plan_cache_enable(int on) {
   return guard([&] { fg::set_plan_cache_enabled(on != 0); });
 }
 
+int fg_set_graph_min_launches(int n, int* previous) {
+  return guard([&] {
+    int prev = fg::set_graph_min_launches(n);
+    if (previous) *previous = prev;
+  });
+}
+
 int fg_plan_cache_stats(uint64_t* hits, uint64_t* misses, uint64_t* entries) {
   return guard([&] { fg::plan_cache_stats(hits, misses, entries); });
 }

@@ -141,6 +141,11 @@ Device& get_device(DeviceId id);
 bool has_device(DeviceId id);
 void register_device(DeviceId id, Device* dev);
 Device* make_hip_device();
+// Replayed launch sequences of at least this many launches run as one HIP
+// graph (default 2); shorter ones are launched one by one. The setter returns
+// the previous value.
+int graph_min_launches();
+int set_graph_min_launches(int n);
 // The HIP device's runtime context (an fg_ctx*), created on first use.
 void* hip_context_raw();
 

@@ -13,6 +13,8 @@ namespace fg {
 
 namespace {
 
+int g_graph_min_launches = 2;
+
 void check(int rc, const char* what) {
   if (rc != FG_OK) fail(std::string(what) + ": " + fg_hip_last_error());
 }
@@ -206,7 +208,8 @@ class HipDevice : public Device {
       for (size_t k = 0; k < p.passes.size(); k++)
         add(p.passes[k], p.meta.launches[k].grid, p.meta.launches[k].block, p.meta.launches[k].lds_bytes);
     }
-    if (graphs_enabled() && !r->failed && !r->graph && r->uses >= 2 && lp.size() >= 2) {
+    if (graphs_enabled() && !r->failed && !r->graph && r->uses >= 2 &&
+        lp.size() >= static_cast<size_t>(graph_min_launches())) {
       if (fg_hip_graph_create(ctx(), static_cast<int>(lp.size()), lp.data(), grids.data(), blocks.data(), lds.data(),
                               nargs.data(), all.data(), &r->graph) != FG_OK) {
         r->failed = true;
@@ -228,7 +231,14 @@ class HipDevice : public Device {
     }
   }
 
-  // FG_HIP_GRAPHS=0 launches replayed plans one by one.
+  // FG_HIP_GRAPHS=0 launches replayed plans one by one, and so are sequences
+  // shorter than graph_min_launches() (default 2: every multi-launch plan).
+  // On MI355X a graph launch costs about 20 us of host time plus well under
+  // 1 us per node, a direct launch 2.5-3 us; but a direct launch queued right
+  // behind a graph launch waited about as long as the graph ran on the device:
+  // with the C4 train step's 2-kernel loss plan launched directly after its
+  // 19-kernel update plan's graph, C4 ran at 4057-4455 steps/s, against
+  // 5178-5511 with both plans as graphs.
   static bool graphs_enabled() {
     static const bool on = [] {
       const char* e = std::getenv("FG_HIP_GRAPHS");
@@ -257,6 +267,15 @@ class HipDevice : public Device {
 }  // namespace
 
 Device* make_hip_device() { return new HipDevice(); }
+
+int graph_min_launches() { return g_graph_min_launches; }
+
+int set_graph_min_launches(int n) {
+  FG_CHECK(n >= 2, "graph_min_launches: a recorded graph needs at least 2 launches, got " + std::to_string(n));
+  int prev = g_graph_min_launches;
+  g_graph_min_launches = n;
+  return prev;
+}
 
 void* hip_context_raw() {
   auto& d = static_cast<HipDevice&>(get_device(DeviceId::Hip));

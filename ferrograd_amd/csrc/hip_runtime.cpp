@@ -128,6 +128,11 @@ struct fg_ctx {
   size_t staging_head = 0;
   hipEvent_t staging_event = nullptr;
   bool staging_event_pending = false;
+  // Pinned landing buffer for small device->host copies. A copy into pageable
+  // memory goes through the runtime's own staging and took 25 us for 4 bytes
+  // on MI355X, against 16.5 us into pinned memory (the kernel + sync floor is
+  // 12.9 us). Reads are synchronous, so one buffer serves them all.
+  char* readback = nullptr;
   // Launch profiling.
   bool profiling = false;
   std::vector<hipEvent_t> event_pool;
@@ -160,6 +165,7 @@ namespace {
 constexpr size_t kAllocGranule = 256;
 constexpr size_t kSmallCopy = 1 << 16;
 constexpr size_t kStagingBytes = 8 << 20;
+constexpr size_t kReadbackBytes = 1 << 20;
 constexpr size_t kMaxCachedBytes = size_t(96) << 30;
 
 size_t round_up(size_t n) { return (n + kAllocGranule - 1) / kAllocGranule * kAllocGranule; }
@@ -188,6 +194,7 @@ int fg_hip_init(int ordinal, fg_ctx** out) {
   HIP_TRY(hipEventCreateWithFlags(&c->staging_event, hipEventDisableTiming));
   HIP_TRY(hipHostMalloc(reinterpret_cast<void**>(&c->staging), kStagingBytes, hipHostMallocDefault));
   c->staging_size = kStagingBytes;
+  HIP_TRY(hipHostMalloc(reinterpret_cast<void**>(&c->readback), kReadbackBytes, hipHostMallocDefault));
   *out = c;
   return FG_OK;
 }
@@ -199,6 +206,7 @@ int fg_hip_destroy(fg_ctx* c) {
   for (auto& ev : c->events) hipEventDestroy(ev);
   hipEventDestroy(c->staging_event);
   hipHostFree(c->staging);
+  hipHostFree(c->readback);
   hipStreamDestroy(c->stream);
   delete c;
   return FG_OK;
@@ -297,6 +305,12 @@ int fg_hip_copy_h2d(fg_ctx* c, void* dst, const void* src, size_t n) {
 int fg_hip_copy_d2h(fg_ctx* c, void* dst, const void* src, size_t n) {
   if (!c || (!dst && n) || (!src && n)) return set_err(FG_ERR_INVALID, "fg_hip_copy_d2h: null argument");
   if (n == 0) return fg_hip_sync(c);
+  if (n <= kReadbackBytes) {
+    HIP_TRY(hipMemcpyAsync(c->readback, src, n, hipMemcpyDeviceToHost, c->stream));
+    HIP_TRY(hipStreamSynchronize(c->stream));
+    std::memcpy(dst, c->readback, n);
+    return FG_OK;
+  }
   HIP_TRY(hipMemcpyAsync(dst, src, n, hipMemcpyDeviceToHost, c->stream));
   HIP_TRY(hipStreamSynchronize(c->stream));
   return FG_OK;

@@ -124,6 +124,12 @@ int fg_clear_caches(void);
 int fg_plan_cache_enable(int on);
 int fg_plan_cache_stats(uint64_t* hits, uint64_t* misses, uint64_t* entries);
 
+/* HIP-graph replay threshold: a replayed plan with at least n kernel launches
+ * (n >= 2; default 2) is recorded once as a HIP graph and relaunched as one;
+ * shorter plans are launched one by one. *previous (may be NULL) receives the
+ * old value. No reference counterpart. */
+int fg_set_graph_min_launches(int n, int* previous);
+
 /* Inspection for tests and tooling: schedule the roots (without running
  * anything) and describe the plan as JSON; optionally render each kernel with
  * the HIP code generator (no device needed). Two calls: with buf == NULL it

@@ -47,3 +47,16 @@ def test_errors_cross_the_abi_as_status_codes(fg):
     shape = (ctypes.c_int64 * 1)(3)
     rc = lib.fg_tensor_zeros(7, 0, shape, 1, ctypes.byref(out))  # unknown device
     assert rc != 0 and b"unknown device" in lib.fg_last_error()
+
+
+def test_graph_threshold_knob(fg):
+    # Host-side setting only: no device is touched.
+    prev = fg.graph_min_launches(5)
+    try:
+        assert prev == 2  # the default: every multi-launch plan is graphed
+        assert fg.graph_min_launches(3) == 5
+        with pytest.raises(fg.FerrogradError, match="at least 2 launches"):
+            fg.graph_min_launches(1)
+        assert fg.graph_min_launches(3) == 3  # a rejected value leaves the setting alone
+    finally:
+        fg.graph_min_launches(prev)
