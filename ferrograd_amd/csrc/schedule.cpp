@@ -217,6 +217,82 @@ bool cheap_to_recompute(const UOp& node, const UOpMap<UOp>& materialized) {
   return loads <= 1;
 }
 
+bool has_unmaterialized_reduce(const UOp& expr, const UOpMap<UOp>& materialized, const UOp& except);
+
+// A reduction over at most kSmallReduce elements that each elementwise
+// consumer can recompute instead of reading a materialised [.., 1] buffer: the
+// class-axis max and sums of log_softmax and its gradient over 10 classes,
+// which otherwise cost one launch each in every train step. Value-preserving:
+// each consumer folds the same loaded values in the same order. Kept
+// materialised when its input still computes (more than a few elementwise ops,
+// or another pending reduction), when it feeds a reduction (whose kernel would
+// then fold serially), and when a consumer broadcasts it more than
+// kSmallReduce-fold (the recompute would multiply the loads).
+constexpr size_t kSmallReduce = 16;
+
+// Whether the kernels that would compute `node` inline all stay small enough:
+// every path from it through elementwise and movement consumers must end at a
+// root or at a node with a kernel of its own (a multi-consumer node that
+// neither reconverges nor is cheap to recompute) without meeting a
+// ReduceAxis (that kernel would fold `node` serially) or any node of more than
+// `max_numel` elements (each would fold it again).
+bool inline_consumers_fit(const UOp& node, size_t max_numel, const UOpMap<std::vector<UOp>>& consumers,
+                          const UOpSet& roots, const UOpMap<size_t>& topo_idx, const UOpMap<UOp>& materialized) {
+  std::vector<std::pair<UOp, int>> stack;
+  auto push_consumers = [&](const UOp& n, int depth) {
+    auto it = consumers.find(n);
+    if (it != consumers.end())
+      for (auto& c : it->second) stack.emplace_back(c, depth + 1);
+  };
+  push_consumers(node, 0);
+  UOpSet seen;
+  while (!stack.empty()) {
+    auto [c, depth] = stack.back();
+    stack.pop_back();
+    if (!seen.insert(c).second || c.op() == Op::Sink) continue;
+    Shape cs;
+    if (c.op() == Op::ReduceAxis || depth > 8 || !c.shape_opt(&cs) || numel(cs) > max_numel) return false;
+    if (roots.count(c)) continue;
+    if (is_alu(c.op())) {
+      auto ci = consumers.find(c);
+      bool own = ci != consumers.end() && ci->second.size() > 1 && !reconverges(c, consumers, roots, topo_idx) &&
+                 !cheap_to_recompute(c, materialized);
+      if (own) continue;
+    } else if (!is_movement(c.op()) || c.op() == Op::Contiguous) {
+      return false;
+    }
+    push_consumers(c, depth);
+  }
+  return true;
+}
+
+bool small_reduce_recomputable(const UOp& node, const UOpMap<std::vector<UOp>>& consumers, const UOpSet& roots,
+                               const UOpMap<size_t>& topo_idx, const UOpMap<UOp>& materialized) {
+  if (node.op() != Op::ReduceAxis) return false;
+  Shape in_shape, out_shape;
+  if (!node.src(0).shape_opt(&in_shape) || !node.shape_opt(&out_shape)) return false;
+  const size_t out_n = numel(out_shape), extent = numel(in_shape) / std::max<size_t>(1, out_n);
+  if (extent > kSmallReduce) return false;
+  // The input: elementwise ops over literals and loaded values only.
+  int alu = 0;
+  std::vector<UOp> stack{node.src(0)};
+  UOpSet seen;
+  while (!stack.empty()) {
+    UOp n = stack.back();
+    stack.pop_back();
+    if (!seen.insert(n).second) continue;
+    if (leaf_kind(n, materialized) != LeafKind::Computed) continue;
+    if (is_movement(n.op()) && n.op() != Op::Contiguous) {
+      stack.push_back(n.src(0));
+      continue;
+    }
+    if (!is_alu(n.op()) || ++alu > 4) return false;
+    for (auto& s : n.srcs()) stack.push_back(s);
+  }
+  if (has_unmaterialized_reduce(node.src(0), materialized, UOp())) return false;
+  return inline_consumers_fit(node, kSmallReduce * out_n, consumers, roots, topo_idx, materialized);
+}
+
 // Whether `expr` (a kernel value under construction) computes a reduction
 // that is not yet materialised.
 bool has_unmaterialized_reduce(const UOp& expr, const UOpMap<UOp>& materialized, const UOp& except) {
@@ -247,6 +323,7 @@ bool should_materialize(const UOp& node, const UOpSet& roots,
   if (node.op() == Op::Contiguous) return true;
   if (is_movement(node.op())) return false;
   if (node.has_buffer_identity()) return false;
+  if (opt.fuse && small_reduce_recomputable(node, consumers, roots, topo_idx, materialized)) return false;
   auto it = consumers.find(node);
   if (it != consumers.end() && it->second.size() > 1) {
     if (opt.fuse && (reconverges(node, consumers, roots, topo_idx) || cheap_to_recompute(node, materialized)))

@@ -166,17 +166,49 @@ def test_fusion_runs_linear_bias_as_reduce_epilogue_and_recomputes_relu_mask(fg,
 
 def test_reduce_read_through_broadcast_stays_materialised(fg, cpu):
     # y = 2 * x.sum(1) feeds a broadcast: fusing it into the consumer would
-    # recompute the sum for every broadcast element, so it keeps its kernel.
-    x = fg.Tensor.new(np.ones((4, 8), np.float32), [4, 8], cpu)
+    # recompute the 64-element sum for every broadcast element, so it keeps
+    # its kernel.
+    x = fg.Tensor.new(np.ones((4, 64), np.float32), [4, 64], cpu)
     y = x.sum([1]).mul(fg.Tensor.scalar(2.0, cpu))
-    z = y.expand([4, 8]).add(x)
+    z = y.expand([4, 64]).add(x)
     items = plan(fg, [z], fuse=True, render=True)
     assert [it["class"] for it in items] == ["row_reduce", "elementwise"]
 
 
-def test_two_reduces_into_one_consumer_keep_one_per_kernel(fg, cpu):
+def test_small_reduce_is_recomputed_by_its_consumer(fg, cpu):
+    # A sum over 8 elements read through an 8-fold broadcast (log_softmax's
+    # class-axis max and sums) is folded again by each consumer element
+    # instead of getting a kernel of its own; the reference partition keeps it.
     x = fg.Tensor.new(np.ones((4, 8), np.float32), [4, 8], cpu)
-    w = fg.Tensor.new(np.ones((4, 8), np.float32), [4, 8], cpu)
+    z = x.sum([1]).mul(fg.Tensor.scalar(2.0, cpu)).expand([4, 8]).add(x)
+    items = plan(fg, [z], fuse=True, render=True)
+    assert [it["class"] for it in items] == ["row_reduce"]
+    assert items[0]["out_shape"] == [4, 8]
+    assert len(plan(fg, [z], fuse=False)) == 2
+
+
+def test_small_reduce_broadcast_far_stays_materialised(fg, cpu):
+    # Read through a 200-fold broadcast, recomputing would multiply its loads.
+    x = fg.Tensor.new(np.ones((4, 8), np.float32), [4, 8], cpu)
+    y = x.sum([1]).mul(fg.Tensor.scalar(2.0, cpu))
+    z = y.expand([4, 200]).add(fg.Tensor.new(np.ones((4, 200), np.float32), [4, 200], cpu))
+    items = plan(fg, [z], fuse=True, render=True)
+    assert [it["class"] for it in items] == ["row_reduce", "elementwise"]
+
+
+def test_small_reduce_feeding_a_reduce_stays_materialised(fg, cpu):
+    # Inlined into the outer sum, the inner 8-element sums would make that
+    # kernel fold serially; the inner reduce keeps its kernel.
+    x = fg.Tensor.new(np.ones((64, 8), np.float32), [64, 8], cpu)
+    z = x.sum([1]).mul(fg.Tensor.scalar(2.0, cpu)).sum([0])
+    items = plan(fg, [z], fuse=True, render=True)
+    assert len(items) == 2 and "serial" not in [it["class"] for it in items]
+
+
+def test_two_reduces_into_one_consumer_keep_one_per_kernel(fg, cpu):
+    # Reductions over more elements than are recomputed inline (64 > 16).
+    x = fg.Tensor.new(np.ones((4, 64), np.float32), [4, 64], cpu)
+    w = fg.Tensor.new(np.ones((4, 64), np.float32), [4, 64], cpu)
     z = x.sum([1]).add(w.max([1]))
     items = plan(fg, [z], fuse=True, render=True)
     assert len(items) == 2 and all(it["class"] == "row_reduce" for it in items)
