@@ -199,20 +199,47 @@ LeafKind leaf_kind(const UOp& src, const UOpMap<UOp>& materialized) {
   return LeafKind::Computed;
 }
 
-// A multi-consumer node cheap enough to recompute in each consumer: one
-// comparison or arithmetic op over literals and at most one loaded value
-// (relu's mask `0 < x` is the case that matters). Recomputing it reads x where
-// the materialised node would have been read, and gives the same bits.
+// Elements behind a leaf (a materialised node, or a buffer seen through views).
+size_t leaf_numel(const UOp& src, const UOpMap<UOp>& materialized) {
+  UOp b = src;
+  while (!materialized.count(b) && is_movement(b.op()) && b.op() != Op::Contiguous) b = b.src(0);
+  if (!materialized.count(b) && b.op() == Op::Buffer && b.arg().buf) return b.arg().buf->numel;
+  Shape s;
+  return b.shape_opt(&s) ? numel(s) : 0;
+}
+
+// A multi-consumer node cheap enough to recompute in each consumer: at most
+// three comparisons or arithmetic ops over literals, 1-element scalars and at
+// most one other loaded value. relu's mask `0 < x` and the cross-entropy
+// gradient seed `t * -(1/B)` are the cases that matter. Recomputing it reads
+// that one value where the materialised node would have been read, and gives
+// the same bits.
 bool cheap_to_recompute(const UOp& node, const UOpMap<UOp>& materialized) {
-  switch (node.op()) {
-    case Op::CmpLt: case Op::Neg: case Op::Add: case Op::Mul: case Op::Max: case Op::Where: break;
-    default: return false;
-  }
-  int loads = 0;
-  for (auto& s : node.srcs()) {
-    LeafKind k = leaf_kind(s, materialized);
-    if (k == LeafKind::Computed) return false;
-    if (k == LeafKind::Buffer) loads++;
+  int ops = 0, loads = 0;
+  std::vector<UOp> stack{node};
+  UOpSet seen;
+  while (!stack.empty()) {
+    UOp n = stack.back();
+    stack.pop_back();
+    if (!seen.insert(n).second) continue;
+    if (n != node) {
+      LeafKind k = leaf_kind(n, materialized);
+      if (k == LeafKind::Literal) continue;
+      if (k == LeafKind::Buffer) {
+        if (leaf_numel(n, materialized) != 1) loads++;
+        continue;
+      }
+      if (is_movement(n.op()) && n.op() != Op::Contiguous) {  // index arithmetic only
+        stack.push_back(n.src(0));
+        continue;
+      }
+    }
+    switch (n.op()) {
+      case Op::CmpLt: case Op::Neg: case Op::Add: case Op::Mul: case Op::Max: case Op::Where: break;
+      default: return false;
+    }
+    if (++ops > 3) return false;
+    for (auto& s : n.srcs()) stack.push_back(s);
   }
   return loads <= 1;
 }

@@ -105,9 +105,11 @@ def test_fusion_makes_c1_one_kernel(fg, cpu):
 
 
 def test_fusion_keeps_nodes_with_diverging_consumers(fg, cpu):
-    # The pre-activation feeds relu and an unrelated sum: still materialised.
+    # The pre-activation feeds relu and an unrelated sum: still materialised
+    # (two loaded inputs, so it is not cheap enough to recompute either).
     x = fg.Tensor.new(np.ones((8, 8), np.float32), [8, 8], cpu)
-    z = x.add(x)
+    w = fg.Tensor.new(np.ones((8, 8), np.float32), [8, 8], cpu)
+    z = x.add(w)
     items_ref = plan(fg, [z.relu(), z.sum([1])])
     items_fused = plan(fg, [z.relu(), z.sum([1])], fuse=True)
     assert len(items_fused) == len(items_ref)
@@ -162,6 +164,17 @@ def test_fusion_runs_linear_bias_as_reduce_epilogue_and_recomputes_relu_mask(fg,
     # Every [16, 64] / [16, 48] pre-activation is written by a reduction kernel.
     pre = [it for it in fused if it.get("out_shape") in ([16, 64], [16, 48])]
     assert pre and all(it["class"] != "elementwise" for it in pre)
+
+
+def test_cheap_node_with_scalar_inputs_is_recomputed(fg, cpu):
+    # t * -(1/B) (the cross-entropy gradient seed) feeds two kernels; two ops
+    # over one loaded tensor and a 1-element scalar are recomputed by each.
+    t = fg.Tensor.new(np.ones((8, 16), np.float32), [8, 16], cpu)
+    g = t.mul(fg.Tensor.scalar(0.125, cpu).neg())
+    w = fg.Tensor.new(np.ones((8, 16), np.float32), [8, 16], cpu)
+    roots = [g.add(w).sum([1]), g.mul(w).sum([1])]
+    assert len(plan(fg, roots)) == 3
+    assert len(plan(fg, roots, fuse=True)) == 2
 
 
 def test_reduce_read_through_broadcast_stays_materialised(fg, cpu):
