@@ -5,6 +5,7 @@
 #include "schedule.hpp"
 
 #include <algorithm>
+#include <unordered_set>
 
 namespace fg {
 
@@ -335,6 +336,58 @@ bool has_unmaterialized_reduce(const UOp& expr, const UOpMap<UOp>& materialized,
   return false;
 }
 
+// When `node` (a Contiguous) copies a buffer in the buffer's own memory
+// order, the buffer node; else null. Its source must be the buffer seen only
+// through permutes and reshapes that compose to the row-major layout of the
+// copy, as nn.rs:98's `weight.permute([1, 0])` followed by matmul's
+// `other.permute([1, 0]).contiguous()` (tensor.rs:771-777) is. Readers can
+// then load the buffer where they would have loaded the copy: same elements,
+// same order.
+UOp identity_copy_source(const UOp& node) {
+  if (node.op() != Op::Contiguous) return UOp();
+  std::vector<UOp> chain;
+  UOp b = node.src(0);
+  while (b.op() == Op::Permute || b.op() == Op::Reshape) {
+    chain.push_back(b);
+    b = b.src(0);
+  }
+  if (b.op() != Op::Buffer || !b.arg().buf) return UOp();
+  Shape shape{b.arg().buf->numel};
+  std::vector<size_t> strides{1};
+  auto row_major = [](const Shape& sh, const std::vector<size_t>& st) {
+    size_t expect = 1;
+    for (size_t d = sh.size(); d-- > 0;) {
+      if (sh[d] == 1) continue;
+      if (st[d] != expect) return false;
+      expect *= sh[d];
+    }
+    return true;
+  };
+  for (auto it = chain.rbegin(); it != chain.rend(); ++it) {
+    const UOp& m = *it;
+    if (m.op() == Op::Permute) {
+      auto ax = m.arg().usizes();
+      Shape ns;
+      std::vector<size_t> nt;
+      for (auto a : ax) {
+        ns.push_back(shape[a]);
+        nt.push_back(strides[a]);
+      }
+      shape = ns;
+      strides = nt;
+      continue;
+    }
+    Shape ns = m.arg().usizes();
+    if (row_major(shape, strides)) {
+      shape = ns;
+      strides = contiguous_strides(ns);
+    } else {
+      return UOp();  // a reshape of a permuted view is no plain view
+    }
+  }
+  return row_major(shape, strides) ? b : UOp();
+}
+
 // schedule.rs:289-335
 bool should_materialize(const UOp& node, const UOpSet& roots,
                         const UOpMap<std::vector<UOp>>& consumers, const UOpSet& nested,
@@ -347,7 +400,7 @@ bool should_materialize(const UOp& node, const UOpSet& roots,
       return false;
     default: break;
   }
-  if (node.op() == Op::Contiguous) return true;
+  if (node.op() == Op::Contiguous) return !(opt.fuse && identity_copy_source(node));
   if (is_movement(node.op())) return false;
   if (node.has_buffer_identity()) return false;
   if (opt.fuse && small_reduce_recomputable(node, consumers, roots, topo_idx, materialized)) return false;
@@ -508,6 +561,32 @@ SchedulePlan schedule_many(const std::vector<UOp>& exprs, const ScheduleOptions&
       }
     }
     materialize(node);
+  }
+  if (opt.fuse) {
+    // Skipped identity copies (see identity_copy_source) are read directly by
+    // their consumers. Phase-1 kernels run before every root, so they read the
+    // buffer before any in-place store of this schedule, as the copy would
+    // have. A root kernel may run after a root that stores into the buffer:
+    // there the copy is taken here, still ahead of every root
+    // (schedule.rs:88-121).
+    std::unordered_set<const BufferInner*> stored;
+    for (auto& expr : exprs) {
+      UOp st, val;
+      if (!assignment_effect(expr, &st, &val)) continue;
+      UOp d = st.src(0);
+      while (is_movement(d.op()) && d.op() != Op::Contiguous) d = d.src(0);
+      if (d.op() == Op::Buffer && d.arg().buf) stored.insert(d.arg().buf.get());
+    }
+    if (!stored.empty()) {
+      for (auto& expr : exprs) {
+        UOp fin = substitute_materialized(expr, plan.replacements);
+        for (auto& n : fin.toposort()) {
+          if (n.op() != Op::Contiguous || plan.replacements.count(n)) continue;
+          UOp b = identity_copy_source(n);
+          if (b && stored.count(b.arg().buf.get())) materialize(n);
+        }
+      }
+    }
   }
   for (auto& expr : exprs) {
     UOp fin = substitute_materialized(expr, plan.replacements);

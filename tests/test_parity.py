@@ -267,3 +267,28 @@ def test_lazy_zero_buffers(fg, hip):
     assert z3.to_vec() == [1.0, 2.0, 3.0]
     i0 = fg.Tensor.zeros([5], hip, dtype=fg.I32)
     assert i0.numpy().tolist() == [0] * 5
+
+
+def test_identity_copy_read_after_an_in_place_store(fg, cpu):
+    # y = x @ (Wᵀ)ᵀ and W += 1 realised together with the store first: y must
+    # use W from before the store. On HIP the identity copy of W is skipped
+    # for readers that run before the store and taken for the root that runs
+    # after it.
+    r = seeded(11)
+    xs = r.standard_normal((64, 96)).astype(np.float32)
+    ws = r.standard_normal((80, 96)).astype(np.float32)
+
+    def run(dev):
+        x = fg.Tensor.new(xs, [64, 96], dev)
+        w = fg.Tensor.new(ws, [80, 96], dev)
+        y = x.matmul(w.permute([1, 0]))
+        w.assign(w.add(fg.Tensor.scalar(1.0, dev)))
+        fg.Tensor.realize_many([w, y])
+        return y.numpy().reshape(64, 80), w.numpy().reshape(80, 96)
+
+    (y_cpu, w_cpu), (y_hip, w_hip) = both(run, cpu)
+    assert np.array_equal(w_hip, ws + np.float32(1.0)) and np.array_equal(w_cpu, w_hip)
+    scale = np.abs(xs).astype(np.float64) @ np.abs(ws).T.astype(np.float64)
+    exact_old_w = xs.astype(np.float64) @ ws.T.astype(np.float64)
+    assert rel_err_bound(y_hip, exact_old_w, scale, 1e-4) <= 1.0
+    assert rel_err_bound(y_hip, y_cpu, scale, 1e-4) <= 1.0

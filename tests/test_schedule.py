@@ -177,6 +177,31 @@ def test_cheap_node_with_scalar_inputs_is_recomputed(fg, cpu):
     assert len(plan(fg, roots, fuse=True)) == 2
 
 
+def test_identity_copy_is_read_in_place_but_a_transpose_is_copied(fg, cpu):
+    x = fg.Tensor.new(np.ones((4, 8), np.float32), [4, 8], cpu)
+    w = fg.Tensor.new(np.ones((6, 8), np.float32), [6, 8], cpu)
+    # w.permute().permute().contiguous(): a copy in w's own layout
+    assert len(plan(fg, [x.matmul(w.permute([1, 0]))], fuse=True)) == 1
+    assert len(plan(fg, [x.matmul(w.permute([1, 0]))])) == 2
+    # x @ v with v [8, 6]: permute(v).contiguous() is a real transpose
+    v = fg.Tensor.new(np.ones((8, 6), np.float32), [8, 6], cpu)
+    items = plan(fg, [x.matmul(v)], fuse=True)
+    assert len(items) == 2 and items[0]["out_shape"] == [6, 8]
+
+
+def test_identity_copy_read_after_an_in_place_store_is_taken_first(fg, cpu):
+    # Root 0 stores into w; root 1 reads w through an identity copy and runs
+    # after it, so it must see the copy taken before the store.
+    x = fg.Tensor.new(np.ones((4, 8), np.float32), [4, 8], cpu)
+    w = fg.Tensor.new(np.ones((6, 8), np.float32), [6, 8], cpu)
+    y = x.matmul(w.permute([1, 0]))
+    w.assign(w.add(fg.Tensor.scalar(1.0, cpu)))
+    items = plan(fg, [w, y], fuse=True)
+    assert [it["out_shape"] for it in items] == [[6, 8], [], [4, 6]]
+    assert items[0]["inputs"] == [{"buffer": items[1]["inputs"][0]["buffer"]}]  # the copy reads w
+    assert {"buffer": items[0]["output"]} in items[2]["inputs"]  # y reads the copy
+
+
 def test_reduce_read_through_broadcast_stays_materialised(fg, cpu):
     # y = 2 * x.sum(1) feeds a broadcast: fusing it into the consumer would
     # recompute the 64-element sum for every broadcast element, so it keeps
