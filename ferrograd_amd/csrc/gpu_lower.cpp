@@ -1661,6 +1661,23 @@ RenderedKernel render_gemm(const KernelInfo& ki, const GemmMatch& g, const std::
 
 // Whether an in-place kernel reads its destination at an index other than
 // the one it stores to (the reference executes such a kernel sequentially).
+// A reduction whose value holds another reduction over the same Range node:
+// the ranges intern to one node (same axis, kind and extent), so the inner
+// loop's loads would be the outer loop's and fold the wrong elements. The
+// reference never nests reductions in one kernel (schedule.rs materialises
+// nested reduces); the HIP schedule's fusions must not either.
+bool nests_reduce_over_same_range(const UOp& kernel) {
+  for (auto& n : kernel.toposort()) {
+    if (n.op() != Op::Reduce || n.srcs().size() < 2) continue;
+    UOpSet outer(n.srcs().begin() + 1, n.srcs().end());
+    for (auto& m : n.src(0).toposort())
+      if (m.op() == Op::Reduce)
+        for (size_t i = 1; i < m.srcs().size(); i++)
+          if (outer.count(m.src(i))) return true;
+  }
+  return false;
+}
+
 bool reads_dest_elsewhere(const KernelInfo& ki) {
   for (auto& ld : loads_in(ki.value)) {
     if (ld.src(0).src(0) != ki.out_param) continue;
@@ -1709,6 +1726,8 @@ RenderedKernel render_hip(const UOp& kernel, const std::string& name, int force_
                                                    " elements; kernel indexes are int32 (at most 2^31-1 elements)");
   FG_CHECK(total_outputs(ki) < (int64_t(1) << 31), "kernel has " + std::to_string(total_outputs(ki)) +
                                                          " outputs; kernel indexes are int32 (at most 2^31-1)");
+  FG_CHECK(!nests_reduce_over_same_range(kernel),
+           "kernel nests a reduction inside another over the same range; it must be materialised first");
   FG_CHECK(!reads_dest_elsewhere(ki),
            "in-place update reads its destination at another index; the HIP device runs kernels in parallel and "
            "cannot reproduce the sequential CPU order");

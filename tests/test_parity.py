@@ -292,3 +292,35 @@ def test_identity_copy_read_after_an_in_place_store(fg, cpu):
     exact_old_w = xs.astype(np.float64) @ ws.T.astype(np.float64)
     assert rel_err_bound(y_hip, exact_old_w, scale, 1e-4) <= 1.0
     assert rel_err_bound(y_hip, y_cpu, scale, 1e-4) <= 1.0
+
+
+@pytest.mark.parametrize("case", ["ties", "large", "random"])
+def test_cross_entropy_gradient_small_class_axis(fg, cpu, case):
+    # The class-axis max and sums of log_softmax and its gradient are folded
+    # again by each consumer on HIP (reductions over at most 16 elements). Tied
+    # maxima split the max gradient by their count (gradient.rs Reduce(Max)),
+    # large logits stress the max subtraction.
+    r = seeded(13)
+    b, c = 300, 10
+    if case == "ties":
+        z = np.round(r.standard_normal((b, c)) * 2.0).astype(np.float32)  # integers: many tied maxima
+        z[:, 3] = z.max(axis=1)
+    elif case == "large":
+        z = (r.standard_normal((b, c)) * 60.0).astype(np.float32)
+    else:
+        z = r.standard_normal((b, c)).astype(np.float32)
+    t = np.eye(c, dtype=np.float32)[r.integers(0, c, b)]
+
+    def run(dev):
+        logits = fg.Tensor.new(z, [b, c], dev).with_requires_grad(True)
+        loss = logits.cross_entropy(fg.Tensor.new(t, [b, c], dev))
+        g = loss.gradient([logits])[0]
+        return loss.to_vec()[0], g.numpy().reshape(b, c)
+
+    (l_cpu, g_cpu), (l_hip, g_hip) = both(run, cpu)
+    assert abs(l_hip - l_cpu) <= 1e-5 * max(1.0, abs(l_cpu))
+    # each gradient element is a handful of terms of magnitude <= 1/b
+    assert np.max(np.abs(g_hip - g_cpu)) <= 1e-5 / b * 10
+    zz = z.astype(np.float64) - z.max(axis=1, keepdims=True)
+    p = np.exp(zz) / np.exp(zz).sum(axis=1, keepdims=True)
+    assert np.max(np.abs(g_hip - (p - t) / b)) <= 1e-5 / b * 10
