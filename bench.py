@@ -223,14 +223,23 @@ def mlp_gemm_flops(batch, dims):
 
 
 def bench_mlp(fg, ctx, steps, warmup, batch, dims):
-    from ferrograd_amd.mlp import mlp_setup
+    from ferrograd_amd.mlp import mlp_setup, train_steps_native
 
     # Step 1 schedules and compiles, step 2 replays the plan, step 3 records
     # its HIP graph: all three stay out of the timed region.
     warmup = max(warmup, 3)
-    step, _ = mlp_setup(fg, "hip", batch=batch, dims=dims)
+    step, (model, opt, x, t) = mlp_setup(fg, "hip", batch=batch, dims=dims, with_state=True)
     losses = []
     ms, prof = timed(fg, ctx, lambda: losses.append(step()), steps, warmup)
+    # The same loop body run from native code (fg_mlp_train_steps), as the
+    # reference's compiled callers run it (examples/mnist.rs:84-101): one call
+    # for all timed steps, each step still reading its loss back.
+    train_steps_native(model, opt, x, t, warmup)
+    fg.synchronize()
+    t0 = time.perf_counter()
+    native_losses = train_steps_native(model, opt, x, t, steps)
+    fg.synchronize()
+    ms_native = (time.perf_counter() - t0) * 1000.0 / steps
     host = timed.host_ms
     kern = by_kernel(prof, steps)
     # MFMA kernels: `_gemm`, or the `_gemm_part` / `_gemm_fin` pair of a split-K GEMM.
@@ -238,14 +247,18 @@ def bench_mlp(fg, ctx, steps, warmup, batch, dims):
     dev_ms = sum(v["total_ms_per_step"] for v in kern.values())
     flops = mlp_gemm_flops(batch, dims)
     tf = lambda t: flops / (t / 1e3) / 1e12 / FP32_MFMA_PEAK_TFLOPS if t else None  # noqa: E731
-    return {"ms_per_step": ms, "steps_per_s": 1e3 / ms, "device_ms_per_step": dev_ms, "host_ms_per_step": host,
+    return {"ms_per_step": ms_native, "steps_per_s": 1e3 / ms_native,
+            "caller": "native loop (fg_mlp_train_steps, examples/mnist.rs:84-101 restated); "
+                      "*_python: the same steps driven op by op from Python",
+            "ms_per_step_python": ms, "steps_per_s_python": 1e3 / ms,
+            "device_ms_per_step": dev_ms, "host_ms_per_step": host,
             "kernels_per_step": sum(v["calls_per_step"] for v in kern.values()),
             "gemm_flops_per_step": flops, "gemm_ms_per_step": gemm_ms,
             # All of the step's GEMM FLOPs over the MFMA kernels' time (the narrow
             # N=10 products, 0.2% of C5's FLOPs, run as row/column reductions and
             # are counted in the numerator only), and over all device time.
             "mfma_frac_of_gemm_kernels": tf(gemm_ms), "mfma_frac_of_device_time": tf(dev_ms),
-            "loss_first_last": [losses[0], losses[-1]] if losses else None, "kernels": kern}
+            "loss_first_last": [losses[0], native_losses[-1]] if losses else None, "kernels": kern}
 
 
 COPY_SRC = r"""
@@ -369,10 +382,11 @@ def main():
         log(f"c3: gemm {sec['c3']['roofline']['achieved']:.1f} TFLOP/s ({100 * sec['c3']['roofline']['frac']:.1f}%)")
     if "c4" in only:
         sec["c4"] = bench_mlp(fg, ctx, args.steps, args.warmup, 256, (784, 128, 10))
-        log(f"c4: {sec['c4']['steps_per_s']:.1f} steps/s")
+        log(f"c4: {sec['c4']['steps_per_s']:.1f} steps/s (native loop), {sec['c4']['steps_per_s_python']:.1f} from Python")
     if "c5" in only:
         sec["c5"] = bench_mlp(fg, ctx, max(3, args.steps // 4), 2, 8192, (784, 4096, 4096, 10))
-        log(f"c5: {sec['c5']['steps_per_s']:.2f} steps/s, gemm {sec['c5']['mfma_frac_of_gemm_kernels']}")
+        log(f"c5: {sec['c5']['steps_per_s']:.2f} steps/s (native loop), {sec['c5']['steps_per_s_python']:.2f} from Python, "
+            f"gemm {sec['c5']['mfma_frac_of_gemm_kernels']}")
     log(f"gpu legs took {time.time() - t_start:.1f}s")
 
     cpu = {}

@@ -87,6 +87,7 @@ def _declare(l: ctypes.CDLL) -> None:
         "fg_sgd_new": (c_int, [PP, c_int, ctypes.c_float, PP]),
         "fg_sgd_zero_grad": (c_int, [P]),
         "fg_sgd_step": (c_int, [P]),
+        "fg_mlp_train_steps": (c_int, [P, c_int, P, P, P, c_int, ctypes.POINTER(ctypes.c_float)]),
         "fg_sgd_free": (c_int, [P]),
         "fg_synchronize": (c_int, [c_int]),
         "fg_stats": (c_int, [ctypes.POINTER(ctypes.c_uint64)] * 3),
@@ -422,6 +423,16 @@ class Sgd:
         if _lib is not None and getattr(self, "_h", None):
             _lib.fg_sgd_free(self._h)
             self._h = None
+
+
+def train_steps_native(layers: Sequence[Linear], opt: Sgd, x: Tensor, targets: Tensor, steps: int) -> list:
+    """fg_mlp_train_steps: `steps` iterations of examples/mnist.rs:84-101's loop
+    body (forward with ReLU between layers, cross-entropy, zero_grad,
+    backward, SGD step, loss read back) run from native code; the losses."""
+    arr = (ctypes.c_void_p * max(1, len(layers)))(*[l._h.value for l in layers])
+    out = (ctypes.c_float * max(1, steps))()
+    _check(lib().fg_mlp_train_steps(arr, len(layers), opt._h, x._h, targets._h, int(steps), out))
+    return [float(out[i]) for i in range(steps)]
 
 
 def reset_init_seed(seed: int = 42) -> None:

@@ -298,6 +298,21 @@ int fg_linear_forward(fg_linear* l, fg_tensor* x, fg_tensor** out) {
   return guard([&] { *out = wrap(l->l.forward(x->t)); });
 }
 
+int fg_mlp_train_steps(fg_linear* const* layers, int nlayers, fg_sgd* opt, fg_tensor* x, fg_tensor* targets, int steps,
+                       float* losses) {
+  return guard([&] {
+    FG_CHECK(layers && nlayers > 0 && opt && x && targets && (losses || steps == 0),
+             "fg_mlp_train_steps: null argument or no layers");
+    std::vector<const fg::Linear*> ls;
+    for (int i = 0; i < nlayers; i++) {
+      FG_CHECK(layers[i], "fg_mlp_train_steps: null layer");
+      ls.push_back(&layers[i]->l);
+    }
+    std::vector<float> v = fg::train_steps(ls, opt->s, x->t, targets->t, steps);
+    std::copy(v.begin(), v.end(), losses);
+  });
+}
+
 int fg_linear_num_params(fg_linear* l, int* n) {
   return guard([&] { *n = static_cast<int>(l->l.parameters().size()); });
 }

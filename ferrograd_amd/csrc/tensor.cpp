@@ -1105,4 +1105,28 @@ void Sgd::step() const {  // optim.rs:60-71
   Tensor::realize_many(params);
 }
 
+std::vector<float> train_steps(const std::vector<const Linear*>& layers, const Sgd& opt, const Tensor& x,
+                               const Tensor& targets, int steps) {
+  FG_CHECK(!layers.empty(), "train_steps requires at least one layer");
+  FG_CHECK(steps >= 0, "train_steps: negative step count");
+  std::vector<float> losses;
+  losses.reserve(static_cast<size_t>(steps));
+  for (int i = 0; i < steps; i++) {
+    Tensor h = x;
+    for (size_t l = 0; l < layers.size(); l++) {
+      h = layers[l]->forward(h);
+      if (l + 1 < layers.size()) h = h.relu();
+    }
+    Tensor loss = h.cross_entropy(targets);
+    opt.zero_grad();
+    loss.backward();
+    opt.step();
+    std::vector<uint8_t> b = loss.to_bytes();
+    float v;
+    std::memcpy(&v, b.data(), sizeof(float));
+    losses.push_back(v);
+  }
+  return losses;
+}
+
 }  // namespace fg

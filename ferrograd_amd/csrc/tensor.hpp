@@ -134,6 +134,14 @@ struct Sgd {
   void step() const;
 };
 
+// The examples/mnist.rs:84-101 loop body run `steps` times from native code,
+// as a compiled caller of the reference runs it: logits = layers through ReLU
+// between them (mnist.rs:30-54 generalised to any depth), loss =
+// cross_entropy, zero_grad, backward, step, then the loss read back. Returns
+// each step's loss.
+std::vector<float> train_steps(const std::vector<const Linear*>& layers, const Sgd& opt, const Tensor& x,
+                               const Tensor& targets, int steps);
+
 // Offline MNIST IDX files (dataset.rs:116-161): images as f32 [count, 784]
 // scaled by 1/255 on `dev`, labels as bytes.
 Tensor idx_images(const std::string& path, DeviceId dev);

@@ -45,6 +45,15 @@ def train_step(model: Mlp, opt: Sgd, x: Tensor, targets: Tensor) -> Tensor:
     return loss
 
 
+def train_steps_native(model: Mlp, opt: Sgd, x: Tensor, targets: Tensor, steps: int) -> list:
+    """`steps` train steps as train_step, looped in native code
+    (fg_mlp_train_steps), with each step's loss read back as
+    examples/mnist.rs:98 does; returns the losses."""
+    from . import train_steps_native as native
+
+    return native(model.layers, opt, x, targets, steps)
+
+
 def synthetic_batch(batch: int, in_features: int, classes: int, seed_x: int, seed_y: int):
     """x ~ U(0,1) [batch, in]; labels floor(u*classes) one-hot."""
     x = np.random.default_rng(seed_x).uniform(0, 1, (batch, in_features)).astype(np.float32)
@@ -54,9 +63,10 @@ def synthetic_batch(batch: int, in_features: int, classes: int, seed_x: int, see
 
 
 def mlp_setup(fg, device, batch: int, dims: Sequence[int], lr: float = 0.01, seed: int = 42,
-              seeds=(7, 8)) -> tuple[Callable[[], float], Mlp]:
+              seeds=(7, 8), with_state: bool = False):
     """Model (reference LCG init, seed 42), optimizer and a resident batch;
-    returns a closure running one train step and reading the loss."""
+    returns a closure running one train step and reading the loss, and the
+    model (or, with_state, the model, optimizer, inputs and targets)."""
     fg.reset_init_seed(seed)
     model = Mlp(dims, device)
     opt = Sgd(model.parameters(), lr)
@@ -68,7 +78,7 @@ def mlp_setup(fg, device, batch: int, dims: Sequence[int], lr: float = 0.01, see
         loss = train_step(model, opt, x, t)
         return loss.to_vec()[0]
 
-    return step, model
+    return step, ((model, opt, x, t) if with_state else model)
 
 
 def predictions(logits: np.ndarray) -> np.ndarray:

@@ -95,6 +95,14 @@ int fg_linear_num_params(fg_linear* l, int* n);
 int fg_linear_param(fg_linear* l, int i, fg_tensor** out);
 int fg_linear_free(fg_linear* l);
 
+/* The training loop body of examples/mnist.rs:84-101, `steps` times, from native
+ * code: logits = layers[0..n) with ReLU between them (mnist.rs:30-54 for any
+ * depth), loss = cross_entropy(logits, targets), opt's zero_grad, backward,
+ * step, then the loss read back into losses[i]. Replaces the Rust caller's
+ * loop; it calls the same Tensor/Linear/Sgd code as the entry points above. */
+int fg_mlp_train_steps(fg_linear* const* layers, int nlayers, fg_sgd* opt, fg_tensor* x, fg_tensor* targets, int steps,
+                       float* losses);
+
 /* optim::Sgd (optim.rs:16-71). */
 int fg_sgd_new(fg_tensor** params, int n, float lr, fg_sgd** out);
 int fg_sgd_zero_grad(fg_sgd* s);
