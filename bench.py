@@ -236,10 +236,13 @@ def bench_mlp(fg, ctx, steps, warmup, batch, dims):
     # for all timed steps, each step still reading its loss back.
     train_steps_native(model, opt, x, t, warmup)
     fg.synchronize()
+    h0 = fg.stats()["host_ms"]
     t0 = time.perf_counter()
     native_losses = train_steps_native(model, opt, x, t, steps)
     fg.synchronize()
     ms_native = (time.perf_counter() - t0) * 1000.0 / steps
+    h1 = fg.stats()["host_ms"]
+    host_native = {k: (h1[k] - h0[k]) / steps for k in h1}
     host = timed.host_ms
     kern = by_kernel(prof, steps)
     # MFMA kernels: `_gemm`, or the `_gemm_part` / `_gemm_fin` pair of a split-K GEMM.
@@ -251,7 +254,7 @@ def bench_mlp(fg, ctx, steps, warmup, batch, dims):
             "caller": "native loop (fg_mlp_train_steps, examples/mnist.rs:84-101 restated); "
                       "*_python: the same steps driven op by op from Python",
             "ms_per_step_python": ms, "steps_per_s_python": 1e3 / ms,
-            "device_ms_per_step": dev_ms, "host_ms_per_step": host,
+            "device_ms_per_step": dev_ms, "host_ms_per_step": host_native, "host_ms_per_step_python": host,
             "kernels_per_step": sum(v["calls_per_step"] for v in kern.values()),
             "gemm_flops_per_step": flops, "gemm_ms_per_step": gemm_ms,
             # All of the step's GEMM FLOPs over the MFMA kernels' time (the narrow
