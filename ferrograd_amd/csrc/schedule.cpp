@@ -336,15 +336,15 @@ bool has_unmaterialized_reduce(const UOp& expr, const UOpMap<UOp>& materialized,
   return false;
 }
 
-// When `node` (a Contiguous) copies a buffer in the buffer's own memory
-// order, the buffer node; else null. Its source must be the buffer seen only
+// When `node` (matmul's own Contiguous, tagged kMatmulCopyTag) copies a buffer
+// in the buffer's own memory order, the buffer node; else null. Its source must be the buffer seen only
 // through permutes and reshapes that compose to the row-major layout of the
 // copy, as nn.rs:98's `weight.permute([1, 0])` followed by matmul's
 // `other.permute([1, 0]).contiguous()` (tensor.rs:771-777) is. Readers can
 // then load the buffer where they would have loaded the copy: same elements,
 // same order.
 UOp identity_copy_source(const UOp& node) {
-  if (node.op() != Op::Contiguous) return UOp();
+  if (node.op() != Op::Contiguous || !node.has_tag() || node.tag() != kMatmulCopyTag) return UOp();
   std::vector<UOp> chain;
   UOp b = node.src(0);
   while (b.op() == Op::Permute || b.op() == Op::Reshape) {

@@ -41,5 +41,11 @@ UOp rangeify(const UOp& sink);
 // symbolic folds leave such literals alone so the arithmetic stays identical
 // to loading the zeros.
 constexpr uint64_t kZeroBufferTag = 0x5a45524fULL;  // "ZERO"
+// Tags the Contiguous that Tensor::matmul makes of its transposed right operand
+// (tensor.rs:771-777). No tensor a caller holds points at it, so the HIP
+// schedule may read its source in place when the copy would not change the
+// layout; a contiguous() the caller asked for is materialised as in the
+// reference.
+constexpr uint64_t kMatmulCopyTag = 0x4d4d4350ULL;  // "MMCP"
 
 }  // namespace fg

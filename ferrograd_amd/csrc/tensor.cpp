@@ -341,7 +341,13 @@ Tensor Tensor::matmul(const Tensor& other) const {  // tensor.rs:762-778
   size_t m = ls[0], k = ls[1], k2 = rs[0], n = rs[1];
   FG_CHECK(k == k2, "matmul: inner dim mismatch (" + std::to_string(k) + " vs " + std::to_string(k2) + ")");
   Tensor a = reshape({m, 1, k}).expand({m, n, k});
-  Tensor b = other.permute({1, 0}).contiguous().reshape({1, n, k}).expand({m, n, k});
+  // other.permute([1, 0]).contiguous(), tagged as matmul's own copy.
+  Tensor t = other.permute({1, 0});
+  Tensor tc = t.is_realized() ? t
+                              : from_uop(UOp::make_tagged(Op::Contiguous, t.dtype(), {t.uop()}, Arg::none(),
+                                                          kMatmulCopyTag),
+                                         t.requires_grad());
+  Tensor b = tc.reshape({1, n, k}).expand({m, n, k});
   return a.mul(b).sum({2}).reshape({m, n});
 }
 

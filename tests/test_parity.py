@@ -324,3 +324,23 @@ def test_cross_entropy_gradient_small_class_axis(fg, cpu, case):
     zz = z.astype(np.float64) - z.max(axis=1, keepdims=True)
     p = np.exp(zz) / np.exp(zz).sum(axis=1, keepdims=True)
     assert np.max(np.abs(g_hip - (p - t) / b)) <= 1e-5 / b * 10
+
+
+def test_requested_identity_contiguous_is_a_snapshot(fg, cpu):
+    # c = w.T.T.contiguous() realised through y becomes its own buffer
+    # (tensor.rs:625-630, 781-828); updating w in place afterwards leaves c
+    # holding the old values, on both devices.
+    ws = seeded(17).standard_normal((6, 8)).astype(np.float32)
+
+    def run(dev):
+        w = fg.Tensor.new(ws, [6, 8], dev)
+        c = w.permute([1, 0]).permute([1, 0]).contiguous()
+        c.add(fg.Tensor.scalar(1.0, dev)).realize()
+        w.assign(w.add(fg.Tensor.scalar(1.0, dev)))
+        w.realize()
+        return c.numpy().reshape(6, 8), c.is_realized(), w.numpy().reshape(6, 8)
+
+    (c_cpu, r_cpu, w_cpu), (c_hip, r_hip, w_hip) = both(run, cpu)
+    assert r_cpu and r_hip
+    assert np.array_equal(c_cpu, ws) and np.array_equal(c_hip, ws)
+    assert np.array_equal(w_hip, ws + np.float32(1.0)) and np.array_equal(w_cpu, w_hip)

@@ -189,6 +189,17 @@ def test_identity_copy_is_read_in_place_but_a_transpose_is_copied(fg, cpu):
     assert len(items) == 2 and items[0]["out_shape"] == [6, 8]
 
 
+def test_a_requested_contiguous_is_materialised_even_in_layout_order(fg, cpu):
+    # Only matmul's own copy is read in place. A contiguous() the caller holds
+    # becomes a buffer at realize, as in the reference, so a later in-place
+    # update of w does not show through it.
+    w = fg.Tensor.new(np.arange(48, dtype=np.float32), [6, 8], cpu)
+    c = w.permute([1, 0]).permute([1, 0]).contiguous()
+    y = c.add(fg.Tensor.scalar(1.0, cpu))
+    items = plan(fg, [y], fuse=True)
+    assert len(items) == 2 and items[0]["out_shape"] == [6, 8]
+
+
 def test_identity_copy_read_after_an_in_place_store_is_taken_first(fg, cpu):
     # Root 0 stores into w; root 1 reads w through an identity copy and runs
     # after it, so it must see the copy taken before the store.
