@@ -431,6 +431,11 @@ int fg_debug_plan(fg_tensor** roots, int n, int fuse, int render, char* buf, siz
     if (!rs.empty()) {
       fg::ScheduleOptions opt;
       opt.fuse = fuse != 0;
+      fg::PtrIndexMap held(64);
+      if (opt.fuse) {
+        fg::collect_held_nodes(&held, nullptr);
+        opt.held = &held;
+      }
       auto plan = fg::schedule_many(rs, opt);
       for (size_t i = 0; i < plan.items.size(); i++) {
         auto& it = plan.items[i];

@@ -388,6 +388,10 @@ UOp identity_copy_source(const UOp& node) {
   return row_major(shape, strides) ? b : UOp();
 }
 
+bool is_held(const UOp& node, const ScheduleOptions& opt) {
+  return opt.held && opt.held->get(node.get()) != PtrIndexMap::kAbsent;
+}
+
 // schedule.rs:289-335
 bool should_materialize(const UOp& node, const UOpSet& roots,
                         const UOpMap<std::vector<UOp>>& consumers, const UOpSet& nested,
@@ -400,13 +404,14 @@ bool should_materialize(const UOp& node, const UOpSet& roots,
       return false;
     default: break;
   }
-  if (node.op() == Op::Contiguous) return !(opt.fuse && identity_copy_source(node));
+  const bool fuse = opt.fuse && !is_held(node, opt);
+  if (node.op() == Op::Contiguous) return !(fuse && identity_copy_source(node));
   if (is_movement(node.op())) return false;
   if (node.has_buffer_identity()) return false;
-  if (opt.fuse && small_reduce_recomputable(node, consumers, roots, topo_idx, materialized)) return false;
+  if (fuse && small_reduce_recomputable(node, consumers, roots, topo_idx, materialized)) return false;
   auto it = consumers.find(node);
   if (it != consumers.end() && it->second.size() > 1) {
-    if (opt.fuse && (reconverges(node, consumers, roots, topo_idx) || cheap_to_recompute(node, materialized)))
+    if (fuse && (reconverges(node, consumers, roots, topo_idx) || cheap_to_recompute(node, materialized)))
       return false;
     return true;
   }
@@ -548,7 +553,7 @@ SchedulePlan schedule_many(const std::vector<UOp>& exprs, const ScheduleOptions&
       deferred.erase(d);
     }
     if (!should_materialize(node, roots, consumers, nested, opt, topo_idx, plan.replacements)) continue;
-    if (opt.fuse && node.op() == Op::ReduceAxis) {
+    if (opt.fuse && node.op() == Op::ReduceAxis && !is_held(node, opt)) {
       UOp c = epilogue_consumer(node, consumers, roots);
       // One reduce per consumer; and not into a root that other nodes read
       // (roots are computed inline by their readers until the end).

@@ -28,6 +28,12 @@ struct ScheduleOptions {
   // interning, so nothing is recomputed), and buffers still holding the zeros
   // `allocate` produced become a literal 0.
   bool fuse = false;
+  // Nodes that live tensors point at. The reference materialises a node by
+  // its structure alone and then repoints every live tensor at that node to
+  // the buffer (tensor.rs:222-252), so the fusions above leave held nodes to
+  // the reference's rules: a held tensor is realised exactly when the
+  // reference's would be.
+  const PtrIndexMap* held = nullptr;
 };
 
 SchedulePlan schedule_many(const std::vector<UOp>& exprs, const ScheduleOptions& opt = {});

@@ -80,6 +80,25 @@ static std::vector<Tensor> live_tensors() {  // tensor.rs:201-214
   return out;
 }
 
+// A tensor at a view (reshape, permute, expand, shrink) of a node is repointed
+// when that node is materialised (apply_map_to_tensors substitutes through the
+// view), so the first node under the views counts as held too.
+void collect_held_nodes(PtrIndexMap* held, std::vector<const UOpInner*>* list) {
+  auto add = [&](const UOpInner* raw) {
+    const size_t before = held->size();
+    held->put(raw, 1);
+    if (list && held->size() != before) list->push_back(raw);
+  };
+  for (auto& w : live_list()) {
+    if (auto p = w.lock()) {
+      const UOpInner* raw = p->uop.get();
+      add(raw);
+      while (is_movement(raw->op) && !raw->srcs.empty()) raw = raw->srcs[0].get();
+      add(raw);
+    }
+  }
+}
+
 UOp Tensor::uop() const { return p_->uop; }
 void Tensor::set_uop(const UOp& u) const { p_->uop = u; }
 
@@ -470,7 +489,7 @@ void key_word(GraphKey& k, uint64_t w) { k.code.push_back(w); }
 // ParamScalar kernel arguments (schedule.rs:217-239) are serialised without
 // their value: narrow(0, start, len) over successive batches is then one plan,
 // and replays read the start from the current graph (scalar_nodes).
-GraphKey graph_key(const std::vector<UOp>& roots, bool fuse) {
+GraphKey graph_key(const std::vector<UOp>& roots, bool fuse, const std::vector<const UOpInner*>* held) {
   GraphKey k;
   const UOp sink = UOp::sink(roots);
   PtrIndexMap pos(128);  // grows on demand
@@ -563,6 +582,19 @@ GraphKey graph_key(const std::vector<UOp>& roots, bool fuse) {
       std::memcpy(&w, a.name.data() + c, std::min<size_t>(8, a.name.size() - c));
       key_word(k, w);
     }
+  }
+  if (held) {
+    // Which nodes live tensors point at decides the fused partition too.
+    std::vector<uint32_t> hp;
+    for (const UOpInner* raw : *held) {
+      uint32_t p = pos.get(raw);
+      if (p != PtrIndexMap::kAbsent) hp.push_back(p);
+    }
+    std::sort(hp.begin(), hp.end());
+    hp.erase(std::unique(hp.begin(), hp.end()), hp.end());
+    key_word(k, 0x48454c44ULL);  // "HELD"
+    key_word(k, hp.size());
+    for (auto p : hp) key_word(k, p);
   }
   uint64_t h = 1469598103934665603ULL;
   for (uint64_t w : k.code) h = (h ^ w) * 1099511628211ULL;
@@ -794,11 +826,17 @@ void Tensor::realize_many(const std::vector<Tensor>& tensors) {  // tensor.rs:78
   ScheduleOptions opt;
   opt.fuse = get_device(roots[0].device()).fuse_elementwise();
   uint64_t t0 = now_ns();
+  PtrIndexMap held(64);
+  std::vector<const UOpInner*> held_list;
+  if (opt.fuse) {
+    collect_held_nodes(&held, &held_list);
+    opt.held = &held;
+  }
   PlanCache& pc = plan_cache();
   GraphKey key;
   std::vector<uint8_t> zero_before;
   if (pc.enabled) {
-    key = graph_key(roots, opt.fuse);
+    key = graph_key(roots, opt.fuse, opt.fuse ? &held_list : nullptr);
     if (auto hit = find_plan(key)) {
       pc.hits++;
       realize_stats().ns_schedule += now_ns() - t0;

@@ -134,6 +134,10 @@ struct Sgd {
   void step() const;
 };
 
+// The nodes live tensors point at (tensor.rs:201-214), as a lookup map and a
+// list, for the HIP schedule's fusions to leave to the reference's rules.
+void collect_held_nodes(PtrIndexMap* held, std::vector<const UOpInner*>* list);
+
 // The examples/mnist.rs:84-101 loop body run `steps` times from native code,
 // as a compiled caller of the reference runs it: logits = layers through ReLU
 // between them (mnist.rs:30-54 generalised to any depth), loss =

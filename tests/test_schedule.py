@@ -174,6 +174,9 @@ def test_cheap_node_with_scalar_inputs_is_recomputed(fg, cpu):
     w = fg.Tensor.new(np.ones((8, 16), np.float32), [8, 16], cpu)
     roots = [g.add(w).sum([1]), g.mul(w).sum([1])]
     assert len(plan(fg, roots)) == 3
+    # While a tensor points at g, g gets the buffer the reference gives it.
+    assert len(plan(fg, roots, fuse=True)) == 3
+    del g
     assert len(plan(fg, roots, fuse=True)) == 2
 
 
@@ -211,6 +214,39 @@ def test_identity_copy_read_after_an_in_place_store_is_taken_first(fg, cpu):
     assert [it["out_shape"] for it in items] == [[6, 8], [], [4, 6]]
     assert items[0]["inputs"] == [{"buffer": items[1]["inputs"][0]["buffer"]}]  # the copy reads w
     assert {"buffer": items[0]["output"]} in items[2]["inputs"]  # y reads the copy
+
+
+def test_a_held_intermediate_is_realised_as_in_the_reference(fg, cpu):
+    # h = x + y feeds relu and its mask, which reconverge: fused, h has no
+    # kernel. While the caller holds h, the reference's rule applies: h is
+    # materialised and, after realize, h points at its buffer.
+    x = fg.Tensor.new(np.arange(8, dtype=np.float32) - 4, [8], cpu)
+    y = fg.Tensor.new(np.ones(8, np.float32), [8], cpu)
+    h = x.add(y)
+    r = h.relu()
+    assert len(plan(fg, [r], fuse=True)) == 2
+    r2 = x.add(y).relu()  # the same graph, no tensor at x + y other than h
+    del h
+    assert len(plan(fg, [r2], fuse=True)) == 1
+
+
+def test_a_held_view_of_a_reduce_keeps_the_reference_partition(fg, cpu):
+    # y = x @ wᵀ is a reshape of the matmul reduce. The reduce feeds a later
+    # reduction, so the reference materialises it (nested) and repoints y.
+    # Fused, it would run as the epilogue of y + b; while y is held, it keeps
+    # its kernel instead.
+    x = fg.Tensor.new(np.ones((4, 8), np.float32), [4, 8], cpu)
+    w = fg.Tensor.new(np.ones((6, 8), np.float32), [6, 8], cpu)
+    b = fg.Tensor.new(np.ones(6, np.float32), [6], cpu)
+    y = x.matmul(w.permute([1, 0]))
+    c = y.add(b)  # two consumers: a kernel of its own, with R as its epilogue when fused
+    roots = [c.relu(), c.sum([1])]
+    del c
+    held = plan(fg, roots, fuse=True)
+    del y
+    free = plan(fg, roots, fuse=True)
+    assert len(held) == len(free) + 1
+    assert [4, 6, 1] in [it["out_shape"] for it in held]  # the matmul reduce's own buffer
 
 
 def test_reduce_read_through_broadcast_stays_materialised(fg, cpu):
