@@ -203,7 +203,7 @@ LeafKind leaf_kind(const UOp& src, const UOpMap<UOp>& materialized) {
 // Elements behind a leaf (a materialised node, or a buffer seen through views).
 size_t leaf_numel(const UOp& src, const UOpMap<UOp>& materialized) {
   UOp b = src;
-  while (!materialized.count(b) && is_movement(b.op()) && b.op() != Op::Contiguous) b = b.src(0);
+  while (!materialized.count(b) && is_movement(b.op())) b = b.src(0);
   if (!materialized.count(b) && b.op() == Op::Buffer && b.arg().buf) return b.arg().buf->numel;
   Shape s;
   return b.shape_opt(&s) ? numel(s) : 0;
@@ -230,7 +230,7 @@ bool cheap_to_recompute(const UOp& node, const UOpMap<UOp>& materialized) {
         if (leaf_numel(n, materialized) != 1) loads++;
         continue;
       }
-      if (is_movement(n.op()) && n.op() != Op::Contiguous) {  // index arithmetic only
+      if (is_movement(n.op())) {  // index arithmetic only
         stack.push_back(n.src(0));
         continue;
       }
@@ -286,7 +286,7 @@ bool inline_consumers_fit(const UOp& node, size_t max_numel, const UOpMap<std::v
       bool own = ci != consumers.end() && ci->second.size() > 1 && !reconverges(c, consumers, roots, topo_idx) &&
                  !cheap_to_recompute(c, materialized);
       if (own) continue;
-    } else if (!is_movement(c.op()) || c.op() == Op::Contiguous) {
+    } else if (!is_movement(c.op())) {
       return false;
     }
     push_consumers(c, depth);
@@ -310,7 +310,7 @@ bool small_reduce_recomputable(const UOp& node, const UOpMap<std::vector<UOp>>& 
     stack.pop_back();
     if (!seen.insert(n).second) continue;
     if (leaf_kind(n, materialized) != LeafKind::Computed) continue;
-    if (is_movement(n.op()) && n.op() != Op::Contiguous) {
+    if (is_movement(n.op())) {
       stack.push_back(n.src(0));
       continue;
     }
@@ -579,7 +579,7 @@ SchedulePlan schedule_many(const std::vector<UOp>& exprs, const ScheduleOptions&
       UOp st, val;
       if (!assignment_effect(expr, &st, &val)) continue;
       UOp d = st.src(0);
-      while (is_movement(d.op()) && d.op() != Op::Contiguous) d = d.src(0);
+      while (is_movement(d.op())) d = d.src(0);
       if (d.op() == Op::Buffer && d.arg().buf) stored.insert(d.arg().buf.get());
     }
     if (!stored.empty()) {
