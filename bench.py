@@ -116,7 +116,8 @@ def bench_c2(fg, ctx, steps, warmup):
 
     n = 1 << 26
     r = np.random.default_rng(2)
-    a, b, c = (Tensor.new(r.uniform(-1, 1, n).astype(np.float32), [n], "hip") for _ in range(3))
+    host = [r.uniform(-1, 1, n).astype(np.float32) for _ in range(3)]
+    a, b, c = (Tensor.new(h, [n], "hip") for h in host)
     holder = {}
 
     def step():
@@ -126,7 +127,15 @@ def bench_c2(fg, ctx, steps, warmup):
     kern = by_kernel(prof, steps)
     name, dk = dominant(kern)
     alg = 4 * n * 4
-    return {"ms_per_step": ms, "gbs": alg / (ms / 1e3) / 1e9, "kernels": kern, "dominant": name,
+    # The timed kernel's last output against float32 numpy rounding each op
+    # once, as the reference's one-statement-per-op C does; relu as its
+    # Where(0 < t, t, 0) (tensor.rs:517-531).
+    t = host[0] * host[1] + host[2]
+    want = np.where(np.float32(0) < t, t, np.float32(0))
+    got = holder["out"].numpy().reshape(n)
+    check = {"against": "float32 numpy, each op rounded once; relu as Where(0 < t, t, 0)",
+             "elements": n, "bit_exact": bool(np.array_equal(got.view(np.uint32), want.view(np.uint32)))}
+    return {"ms_per_step": ms, "gbs": alg / (ms / 1e3) / 1e9, "kernels": kern, "dominant": name, "check": check,
             "roofline": {"bound": "hbm", "achieved": alg / (dk["avg_ms"] / 1e3) / 1e9, "peak": HBM_PEAK_GBS,
                          "unit": "GB/s", "frac": alg / (dk["avg_ms"] / 1e3) / 1e9 / HBM_PEAK_GBS,
                          "traffic": pmc_traffic(name), "kernel": name, "algorithmic_bytes": alg,
@@ -163,8 +172,9 @@ def bench_c1(fg, ctx, steps, warmup):
 
     # Six distinct inputs (6 x 64 MiB > the 256 MB Infinity Cache) rotate so
     # every step streams from HBM.
-    xs = [Tensor.new(np.random.default_rng(1 + i).standard_normal((4096, 4096)).astype(np.float32), [4096, 4096], "hip")
-          for i in range(6)]
+    x0 = np.random.default_rng(1).standard_normal((4096, 4096)).astype(np.float32)
+    xs = [Tensor.new(x0 if i == 0 else np.random.default_rng(1 + i).standard_normal((4096, 4096)).astype(np.float32),
+                     [4096, 4096], "hip") for i in range(6)]
     s0, s1 = Tensor.scalar(0.5, "hip"), Tensor.scalar(1.0, "hip")
     it = {"i": 0, "out": None}
 
@@ -178,7 +188,13 @@ def bench_c1(fg, ctx, steps, warmup):
     name, dk = dominant(kern)
     alg = 4096 * 4096 * 4 + 4096 * 4
     ach = alg / (dk["avg_ms"] / 1e3) / 1e9
-    return {"ms_per_step": ms, "gbs": alg / (ms / 1e3) / 1e9, "kernels": kern,
+    # The timed kernel on the first input against float64: every term is >= 0,
+    # so the bound 1e-4 * sum|terms| is a relative bound.
+    got = xs[0].mul(s0).add(s1).relu().sum([1]).numpy().reshape(4096)
+    want = np.maximum(x0.astype(np.float64) * 0.5 + 1.0, 0.0).sum(axis=1)
+    rel = float(np.max(np.abs(got - want) / np.maximum(want, 1e-30)))
+    check = {"against": "float64 row sums", "max_rel_err": rel, "tol": 1e-4, "ok": rel <= 1e-4}
+    return {"ms_per_step": ms, "gbs": alg / (ms / 1e3) / 1e9, "kernels": kern, "check": check,
             "roofline": {"bound": "hbm", "achieved": ach, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                          "frac": ach / HBM_PEAK_GBS, "traffic": pmc_traffic(name), "kernel": name,
                          "algorithmic_bytes": alg, "kernel_avg_ms": dk["avg_ms"]}}
@@ -188,9 +204,10 @@ def bench_c3(fg, ctx, steps, warmup):
     from ferrograd_amd import Tensor
 
     r = np.random.default_rng(5)
-    x = Tensor.new(r.standard_normal((4096, 4096)).astype(np.float32), [4096, 4096], "hip")
-    w = Tensor.new(np.random.default_rng(6).uniform(-1 / 64, 1 / 64, (4096, 4096)).astype(np.float32), [4096, 4096],
-                   "hip")
+    xh = r.standard_normal((4096, 4096)).astype(np.float32)
+    wh = np.random.default_rng(6).uniform(-1 / 64, 1 / 64, (4096, 4096)).astype(np.float32)
+    x = Tensor.new(xh, [4096, 4096], "hip")
+    w = Tensor.new(wh, [4096, 4096], "hip")
     b = Tensor.zeros([4096], "hip")
     holder = {}
 
@@ -203,7 +220,15 @@ def bench_c3(fg, ctx, steps, warmup):
     flops = 2 * 4096 ** 3
     g = kern[gemm[0]] if gemm else dominant(kern)[1]
     tf = flops / (g["avg_ms"] / 1e3) / 1e12
-    return {"ms_per_step": ms, "tflops_step": flops / (ms / 1e3) / 1e12, "kernels": kern,
+    # 64 sampled rows of the timed kernel's last output against float64, per
+    # element within 1e-4 * sum_k |x w| (b is zero).
+    rows = np.random.default_rng(7).choice(4096, 64, replace=False)
+    got = holder["y"].numpy().reshape(4096, 4096)[rows]
+    x64, w64 = xh[rows].astype(np.float64), wh.astype(np.float64)
+    bound = 1e-4 * (np.abs(x64) @ np.abs(w64).T)
+    worst = float(np.max(np.abs(got - x64 @ w64.T) / bound))
+    check = {"against": "float64, 64 sampled rows", "max_err_over_bound": worst, "ok": worst <= 1.0}
+    return {"ms_per_step": ms, "tflops_step": flops / (ms / 1e3) / 1e12, "kernels": kern, "check": check,
             "roofline": {"bound": "mfma", "achieved": tf, "peak": FP32_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
                          "frac": tf / FP32_MFMA_PEAK_TFLOPS, "kernel": gemm[0] if gemm else None,
                          "traffic": pmc_traffic(gemm[0]) if gemm else None, "algorithmic_flops": flops,
@@ -261,7 +286,8 @@ def bench_mlp(fg, ctx, steps, warmup, batch, dims):
             # N=10 products, 0.2% of C5's FLOPs, run as row/column reductions and
             # are counted in the numerator only), and over all device time.
             "mfma_frac_of_gemm_kernels": tf(gemm_ms), "mfma_frac_of_device_time": tf(dev_ms),
-            "loss_first_last": [losses[0], native_losses[-1]] if losses else None, "kernels": kern}
+            "loss_first_last": [losses[0], native_losses[-1]] if losses else None,
+            "check": {"losses_finite": bool(np.all(np.isfinite(losses + native_losses)))}, "kernels": kern}
 
 
 COPY_SRC = r"""
@@ -372,7 +398,7 @@ def main():
     if "c2" in only:
         c2 = bench_c2(fg, ctx, args.steps, args.warmup)
         log(f"c2: {c2['gbs']:.1f} GB/s per step, kernel {c2['roofline']['achieved']:.1f} GB/s "
-            f"({100 * c2['roofline']['frac']:.1f}% of HBM peak)")
+            f"({100 * c2['roofline']['frac']:.1f}% of HBM peak), bit-exact: {c2['check']['bit_exact']}")
         sec["c2_pcie_inclusive"] = bench_c2_pcie(fg, 3)
         log(f"c2 with host buffers: {sec['c2_pcie_inclusive']['gbs']:.1f} GB/s")
     if "c1" in only:
@@ -412,7 +438,7 @@ def main():
             "vs_baseline": None, "dtype": "f32", "data": "synthetic (seeded U(-1,1))",
             "config": {"workload": "C2: out = (a*b + c).relu(), a,b,c f32[2^26], one fused kernel (3 reads + 1 write)",
                        "elements": 1 << 26, "algorithmic_bytes_per_step": 4 * (1 << 26) * 4},
-            "roofline": c2["roofline"],
+            "roofline": c2["roofline"], "check": c2["check"],
             "cpu_baseline": ({"value": c2cpu["value"], "unit": "GB/s", "cores": c2cpu["cores"], "kind": c2cpu["kind"],
                               "sample": c2cpu["sample"]} if c2cpu else None),
             "device": info, "secondary": sec,
