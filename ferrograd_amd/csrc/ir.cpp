@@ -215,13 +215,71 @@ std::string Arg::str() const {
 
 // ── interner (src/uop.rs:563-591) ───────────────────────────────────────────
 namespace {
-struct InternEntry {
-  const UOpInner* raw;
-  std::weak_ptr<const UOpInner> weak;
+// The set of live nodes, keyed by their structural hash: open addressing with
+// linear probing and backward-shift deletion, so interning a node costs no
+// allocation beyond the node itself. A node enters in UOp::make and leaves in
+// the first statement of its destructor, before its sources are released, so
+// every entry belongs to a node that is still owned.
+class InternTable {
+ public:
+  InternTable() { slots_.assign(size_t(1) << bits_, nullptr); }
+  template <class Eq>
+  const UOpInner* find(size_t h, Eq&& eq) const {
+    for (size_t i = home(h);; i = next(i)) {
+      const UOpInner* e = slots_[i];
+      if (!e) return nullptr;
+      if (e->hash == h && eq(e)) return e;
+    }
+  }
+  void insert(const UOpInner* e) {
+    if ((size_ + 1) * 2 > slots_.size()) grow();
+    size_t i = home(e->hash);
+    while (slots_[i]) i = next(i);
+    slots_[i] = e;
+    size_++;
+  }
+  void erase(const UOpInner* e) {
+    size_t i = home(e->hash);
+    while (slots_[i] != e) {
+      if (!slots_[i]) return;
+      i = next(i);
+    }
+    // Shift back every later entry of the probe run that the hole would
+    // otherwise cut off from its home slot.
+    for (size_t j = next(i);; j = next(j)) {
+      const UOpInner* m = slots_[j];
+      if (!m) break;
+      const size_t k = home(m->hash);
+      const bool stays = i <= j ? (i < k && k <= j) : (i < k || k <= j);
+      if (stays) continue;
+      slots_[i] = m;
+      i = j;
+    }
+    slots_[i] = nullptr;
+    size_--;
+  }
+  size_t size() const { return size_; }
+
+ private:
+  size_t home(size_t h) const { return static_cast<size_t>((h * 0x9E3779B97F4A7C15ULL) >> (64 - bits_)); }
+  size_t next(size_t i) const { return (i + 1) & (slots_.size() - 1); }
+  void grow() {
+    std::vector<const UOpInner*> old;
+    old.swap(slots_);
+    bits_++;
+    slots_.assign(size_t(1) << bits_, nullptr);
+    size_ = 0;
+    for (const UOpInner* e : old)
+      if (e) insert(e);
+  }
+  std::vector<const UOpInner*> slots_;
+  unsigned bits_ = 12;
+  size_t size_ = 0;
 };
-std::unordered_multimap<size_t, InternEntry>& interner() {
-  static auto* m = new std::unordered_multimap<size_t, InternEntry>();
-  return *m;
+
+InternTable& interner() {
+  static auto* t = new InternTable();
+  return *t;
 }
 
 size_t node_hash(Op op, DType dt, const std::vector<UOp>& srcs, const Arg& arg, bool has_tag,
@@ -235,34 +293,23 @@ size_t node_hash(Op op, DType dt, const std::vector<UOp>& srcs, const Arg& arg, 
 }
 }  // namespace
 
-UOpInner::~UOpInner() {
-  auto& m = interner();
-  auto range = m.equal_range(hash);
-  for (auto it = range.first; it != range.second; ++it) {
-    if (it->second.raw == this) {
-      m.erase(it);
-      break;
-    }
-  }
-}
+UOpInner::~UOpInner() { interner().erase(this); }
 
 size_t interner_size() { return interner().size(); }
 void interner_clear_for_tests() {}
 
 UOp UOp::make(Op op, DType dtype, std::vector<UOp> srcs, Arg arg, bool has_tag, uint64_t tag) {
   size_t h = node_hash(op, dtype, srcs, arg, has_tag, tag);
-  auto& m = interner();
-  auto range = m.equal_range(h);
-  for (auto it = range.first; it != range.second; ++it) {
-    const UOpInner* e = it->second.raw;
-    if (e->op != op || e->dtype != dtype || e->has_tag != has_tag || e->tag != tag) continue;
-    if (e->srcs.size() != srcs.size()) continue;
-    bool same = true;
+  InternTable& t = interner();
+  const UOpInner* e = t.find(h, [&](const UOpInner* c) {
+    if (c->op != op || c->dtype != dtype || c->has_tag != has_tag || c->tag != tag) return false;
+    if (c->srcs.size() != srcs.size()) return false;
     for (size_t i = 0; i < srcs.size(); i++)
-      if (e->srcs[i] != srcs[i]) { same = false; break; }
-    if (!same || !(e->arg == arg)) continue;
-    auto sp = it->second.weak.lock();
-    if (sp) return UOp(sp);
+      if (c->srcs[i] != srcs[i]) return false;
+    return c->arg == arg;
+  });
+  if (e) {
+    if (auto sp = e->weak_from_this().lock()) return UOp(std::move(sp));
   }
   auto inner = std::make_shared<UOpInner>();
   inner->op = op;
@@ -274,9 +321,8 @@ UOp UOp::make(Op op, DType dtype, std::vector<UOp> srcs, Arg arg, bool has_tag, 
   inner->hash = h;
   if (op == Op::Device) inner->device = static_cast<DeviceId>(inner->arg.a);
   else if (!inner->srcs.empty()) inner->device = inner->srcs[0].get()->device;
-  std::shared_ptr<const UOpInner> cp = inner;
-  m.emplace(h, InternEntry{inner.get(), cp});
-  return UOp(cp);
+  t.insert(inner.get());
+  return UOp(std::shared_ptr<const UOpInner>(std::move(inner)));
 }
 
 UOp UOp::make_new(Op op, DType dtype, std::vector<UOp> srcs, Arg arg) {

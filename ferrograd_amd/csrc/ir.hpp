@@ -214,7 +214,7 @@ template <class V>
 using UOpMap = std::unordered_map<UOp, V, UOpHash>;
 using UOpSet = std::unordered_set<UOp, UOpHash>;
 
-struct UOpInner {
+struct UOpInner : std::enable_shared_from_this<UOpInner> {
   Op op;
   DType dtype;
   std::vector<UOp> srcs;
