@@ -163,3 +163,30 @@ def test_steady_state_graph_replays_keep_their_arguments_hip(fg, hip, fresh_plan
     s1 = fg.stats()
     assert s1["graph_replays"] - s0["graph_replays"] >= 6
     assert s1["graph_updated_launches"] - s0["graph_updated_launches"] == 0
+
+
+@pytest.mark.gpu
+def test_held_intermediate_selects_its_own_plan_hip(fg, hip, fresh_plans):
+    # relu(x + y): fused into one kernel while nothing holds x + y; with a
+    # tensor at x + y it is materialised (the reference's partition) and that
+    # tensor is realised. The two partitions are two plans; each replays.
+    x = fg.Tensor.new(np.arange(16, dtype=np.float32) - 8, [16], hip)
+    y = fg.Tensor.new(np.full(16, 0.5, np.float32), [16], hip)
+    want = np.maximum(np.arange(16, dtype=np.float32) - 7.5, 0)
+    # Results are taken outside `assert`: pytest's assertion rewriting keeps
+    # every subexpression alive, which would make x + y a held tensor.
+    e0 = fg.plan_stats()["entries"]
+    free = x.add(y).relu().numpy().reshape(16)
+    assert np.array_equal(free, want)
+    h = x.add(y)
+    held = h.relu().numpy().reshape(16)
+    assert np.array_equal(held, want) and h.is_realized()
+    assert fg.plan_stats()["entries"] - e0 == 2
+    hits = fg.plan_stats()["hits"]
+    h2 = x.add(y)
+    held2 = h2.relu().numpy().reshape(16)
+    assert np.array_equal(held2, want) and h2.is_realized()
+    del h, h2
+    free2 = x.add(y).relu().numpy().reshape(16)
+    assert np.array_equal(free2, want)
+    assert fg.plan_stats()["hits"] - hits == 2 and fg.plan_stats()["entries"] - e0 == 2
