@@ -364,6 +364,27 @@ def library_compare() -> None:
                       "torch_add_2^26_ms": add, "torch_add_gbs": 3 * 4 * (1 << 26) / add / 1e6}))
 
 
+def shard_sweep(steps: int) -> None:
+    """C5 (784->4096->4096->10) at B = 8192/p for p = 1, 2, 4, 8: the shape one
+    GPU runs under p-way data parallelism, before the gradient all-reduce
+    (which one GPU cannot show). One JSON line per p."""
+    import ferrograd_amd as fg
+    from ferrograd_amd.hip import Context
+
+    ctx = Context.of_device()
+    dims = (784, 4096, 4096, 10)
+    for p in (1, 2, 4, 8):
+        b = 8192 // p
+        r = bench_mlp(fg, ctx, max(4, steps // 4), 2, b, dims)
+        log(f"p={p} B={b}: {r['steps_per_s']:.1f} steps/s, device {r['device_ms_per_step']:.3f} ms, "
+            f"gemm {r['mfma_frac_of_gemm_kernels']:.3f} of peak")
+        print(json.dumps({"p": p, "batch": b, "ms_per_step": r["ms_per_step"], "steps_per_s": r["steps_per_s"],
+                          "device_ms_per_step": r["device_ms_per_step"],
+                          "gemm_ms_per_step": r["gemm_ms_per_step"],
+                          "mfma_frac_of_gemm_kernels": r["mfma_frac_of_gemm_kernels"],
+                          "samples_per_s": r["steps_per_s"] * b}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -374,12 +395,17 @@ def main():
     ap.add_argument("--kernels", action="store_true", help="include per-kernel tables")
     ap.add_argument("--copy-probe", action="store_true", help="only run the 1 GiB copy calibration kernel")
     ap.add_argument("--library-compare", action="store_true", help="only time torch's fp32 mm and add for reference")
+    ap.add_argument("--shard-sweep", action="store_true",
+                    help="only time the C5 step at the per-GPU batch of 1, 2, 4 and 8-way data parallelism")
     args = ap.parse_args()
     if args.copy_probe:
         copy_probe()
         return
     if args.library_compare:
         library_compare()
+        return
+    if args.shard_sweep:
+        shard_sweep(args.steps)
         return
     if args.gpus != 1:
         print(f"bench.py measures one MI355X; --gpus {args.gpus} is not supported in this build "
