@@ -3,6 +3,7 @@ No compute calls (CPU only)."""
 import os
 import re
 import subprocess
+import sys
 
 import pytest
 
@@ -60,3 +61,12 @@ def test_graph_threshold_knob(fg):
         assert fg.graph_min_launches(3) == 3  # a rejected value leaves the setting alone
     finally:
         fg.graph_min_launches(prev)
+
+
+def test_bench_refuses_more_than_one_gpu():
+    # Every config here runs on one GPU; --gpus N > 1 exits with a message
+    # before touching a device.
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    r = subprocess.run([sys.executable, os.path.join(root, "bench.py"), "--gpus", "2"], capture_output=True,
+                       text=True, timeout=120)
+    assert r.returncode == 2 and "one MI355X" in r.stderr and r.stdout == ""

@@ -124,6 +124,18 @@ def test_alloc_is_zeroed(ctx):  # device.rs:366-377, cpu.rs:277-280
     assert not _download(ctx, q, 1024).any()
 
 
+@pytest.mark.parametrize("nbytes", [4, (1 << 20) - 4, 1 << 20, (1 << 20) + 4, 3 << 20])
+def test_copies_round_trip_on_both_sides_of_the_staging_limits(ctx, nbytes):
+    # Host->device copies up to 64 KiB go through a pinned staging ring and
+    # device->host reads up to 1 MiB land in a pinned buffer; larger ones go
+    # direct. Every size must round-trip exactly.
+    n = nbytes // 4
+    a = np.random.default_rng(nbytes).standard_normal(n).astype(np.float32)
+    p = _upload(ctx, a)
+    assert np.array_equal(_download(ctx, p, n), a)
+    ctx.free(p)
+
+
 def test_bad_source_is_compile_error(ctx):  # cpu.rs:484-497, 639-649
     from ferrograd_amd.hip import FG_ERR_COMPILE, HipError
 
