@@ -568,28 +568,53 @@ SchedulePlan schedule_many(const std::vector<UOp>& exprs, const ScheduleOptions&
     materialize(node);
   }
   if (opt.fuse) {
-    // Skipped identity copies (see identity_copy_source) are read directly by
-    // their consumers. Phase-1 kernels run before every root, so they read the
-    // buffer before any in-place store of this schedule, as the copy would
-    // have. A root kernel may run after a root that stores into the buffer:
-    // there the copy is taken here, still ahead of every root
-    // (schedule.rs:88-121).
+    // Every node the reference materialises runs in phase 1, ahead of every
+    // root, and so reads each buffer before any in-place store of this
+    // schedule (schedule.rs:88-121). The fusions above move some of those
+    // nodes into the kernels that read them: skipped identity copies, deferred
+    // reduce epilogues, recomputed cheap nodes and small reductions. Inside
+    // root i such a node runs after the stores of roots 0..i, so when it reads
+    // a buffer one of them stores it is materialised here instead, still ahead
+    // of every root, and reads what the reference's kernel would have read.
+    ScheduleOptions ref_opt = opt;
+    ref_opt.fuse = false;
     std::unordered_set<const BufferInner*> stored;
     for (auto& expr : exprs) {
       UOp st, val;
-      if (!assignment_effect(expr, &st, &val)) continue;
-      UOp d = st.src(0);
-      while (is_movement(d.op())) d = d.src(0);
-      if (d.op() == Op::Buffer && d.arg().buf) stored.insert(d.arg().buf.get());
-    }
-    if (!stored.empty()) {
-      for (auto& expr : exprs) {
-        UOp fin = substitute_materialized(expr, plan.replacements);
-        for (auto& n : fin.toposort()) {
-          if (n.op() != Op::Contiguous || plan.replacements.count(n)) continue;
-          UOp b = identity_copy_source(n);
-          if (b && stored.count(b.arg().buf.get())) materialize(n);
+      if (assignment_effect(expr, &st, &val)) {
+        UOp d = st.src(0);
+        while (is_movement(d.op())) d = d.src(0);
+        if (d.op() == Op::Buffer && d.arg().buf) stored.insert(d.arg().buf.get());
+      }
+      if (stored.empty()) continue;
+      // The nodes this root's kernel computes (the walk stops at nodes that
+      // already have a buffer), children first, and whether each reads a
+      // stored buffer.
+      std::vector<UOp> order;
+      UOpMap<bool> reads;
+      std::vector<std::pair<UOp, bool>> stack{{expr, false}};
+      while (!stack.empty()) {
+        auto [n, expanded] = stack.back();
+        stack.pop_back();
+        if (reads.count(n)) continue;
+        if (!expanded) {
+          if (n != expr && plan.replacements.count(n)) {
+            reads[n] = false;
+            continue;
+          }
+          stack.emplace_back(n, true);
+          for (auto& s : n.srcs())
+            if (!reads.count(s)) stack.emplace_back(s, false);
+          continue;
         }
+        bool r = n.op() == Op::Buffer && n.arg().buf && stored.count(n.arg().buf.get());
+        for (auto& s : n.srcs()) r = r || reads.at(s);
+        reads[n] = r;
+        order.push_back(n);
+      }
+      for (auto& n : order) {
+        if (n == expr || !reads.at(n)) continue;
+        if (should_materialize(n, roots, consumers, nested, ref_opt, topo_idx, plan.replacements)) materialize(n);
       }
     }
   }

@@ -43,6 +43,17 @@ def load() -> ctypes.CDLL:
     return _loaded
 
 
+def set_fuse(on: bool) -> bool:
+    """Run the CPU device's realisations with the HIP device's fusions (True)
+    or the reference partition (False, the default); returns the previous
+    setting. Fused and unfused runs on this one device use the same lowering,
+    so a fusion that preserves values gives the same bits."""
+    l = load()
+    l.fg_oracle_set_fuse.restype = ctypes.c_int
+    l.fg_oracle_set_fuse.argtypes = [ctypes.c_int]
+    return bool(l.fg_oracle_set_fuse(int(on)))
+
+
 def plan_c(roots) -> list:
     """Oracle C source of every kernel the reference schedule makes for `roots`."""
     import json

@@ -508,6 +508,13 @@ class CpuDevice : public Device {
  public:
   DeviceId id() const override { return DeviceId::Cpu; }
 
+  // Off by default: the reference's kernel partition. On, the CPU device
+  // runs the HIP device's value-preserving fusions (schedule.cpp), so a test
+  // can compare the fused and the reference partition on one device, where
+  // every kernel keeps the reference's lowering and accumulation order.
+  bool fuse = false;
+  bool fuse_elementwise() const override { return fuse; }
+
   Buffer allocate(DType dtype, size_t numel) override {  // cpu.rs:277-280
     Buffer b = reserve_buffer(dtype, numel);
     realize_storage(*b, true);
@@ -601,14 +608,24 @@ class CpuDevice : public Device {
 
 extern "C" {
 
+static fg::oracle::CpuDevice* g_cpu_device = nullptr;
+
 // Register the oracle CPU device as device 0 ("cpu").
 int fg_oracle_register(void) {
-  static fg::oracle::CpuDevice* dev = nullptr;
-  if (!dev) {
-    dev = new fg::oracle::CpuDevice();
-    fg::register_device(fg::DeviceId::Cpu, dev);
+  if (!g_cpu_device) {
+    g_cpu_device = new fg::oracle::CpuDevice();
+    fg::register_device(fg::DeviceId::Cpu, g_cpu_device);
   }
   return 0;
+}
+
+// Schedule the CPU device's realisations with (1) or without (0) the HIP
+// device's fusions; returns the previous setting.
+int fg_oracle_set_fuse(int on) {
+  fg_oracle_register();
+  int prev = g_cpu_device->fuse ? 1 : 0;
+  g_cpu_device->fuse = on != 0;
+  return prev;
 }
 
 }  // extern "C"

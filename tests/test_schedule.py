@@ -297,3 +297,18 @@ def test_two_reduces_into_one_consumer_keep_one_per_kernel(fg, cpu):
     z = x.sum([1]).add(w.max([1]))
     items = plan(fg, [z], fuse=True, render=True)
     assert len(items) == 2 and all(it["class"] == "row_reduce" for it in items)
+
+
+def test_reduce_read_after_an_in_place_store_is_materialised_first(fg, cpu):
+    # realize_many([w.assign(w + 1), 2 * w.sum(0)]): the reference materialises
+    # the sum (a reduce consumed by ALU) in phase 1, before the store. Fused,
+    # the sum would otherwise run as the epilogue of the root that reads it,
+    # after root 0's store.
+    w = fg.Tensor.new(np.arange(6, dtype=np.float32), [2, 3], cpu)
+    y = w.sum([0]).mul(fg.Tensor.scalar(2.0, cpu))
+    w.assign(w.add(fg.Tensor.scalar(1.0, cpu)))
+    items = plan(fg, [w, y], fuse=True)
+    assert [it["out_shape"] for it in items] == [[1, 3], [], [1, 3]]
+    assert {"buffer": items[0]["output"]} in items[2]["inputs"]
+    # Read before any store, the sum stays the root's epilogue.
+    assert [it["out_shape"] for it in plan(fg, [y, w], fuse=True)] == [[1, 3], []]
