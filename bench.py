@@ -270,6 +270,9 @@ def bench_mlp(fg, ctx, steps, warmup, batch, dims):
     host_native = {k: (h1[k] - h0[k]) / steps for k in h1}
     host = timed.host_ms
     kern = by_kernel(prof, steps)
+    check = check_mlp_step_on_device(fg, model, opt, x, t, batch, dims)
+    check["losses_finite"] = bool(np.all(np.isfinite(losses + native_losses)))
+    check["ok"] = check["ok"] and check["losses_finite"]
     # MFMA kernels: `_gemm`, or the `_gemm_part` / `_gemm_fin` pair of a split-K GEMM.
     gemm_ms = sum(v["total_ms_per_step"] for k, v in kern.items() if "_gemm" in k)
     dev_ms = sum(v["total_ms_per_step"] for v in kern.values())
@@ -287,7 +290,38 @@ def bench_mlp(fg, ctx, steps, warmup, batch, dims):
             # are counted in the numerator only), and over all device time.
             "mfma_frac_of_gemm_kernels": tf(gemm_ms), "mfma_frac_of_device_time": tf(dev_ms),
             "loss_first_last": [losses[0], native_losses[-1]] if losses else None,
-            "check": {"losses_finite": bool(np.all(np.isfinite(losses + native_losses)))}, "kernels": kern}
+            "check": check, "kernels": kern}
+
+
+def check_mlp_step_on_device(fg, model, opt, x, t, batch, dims):
+    """One more train step of the timed kernels (the same programs; the
+    step holds its pre-activations, which the reference partition
+    materialises anyway), checked product by product against float64 on the
+    device's own values (tests/f64ref.py check_mlp_step): every forward
+    product on 64 sampled batch rows, the loss, and each parameter's
+    effective gradient (p0 - p1)/lr, for 64 sampled rows of each hidden
+    layer's weight and every row of the last layer's."""
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import f64ref
+    from ferrograd_amd.mlp import synthetic_batch, train_step
+
+    xs, ts = synthetic_batch(batch, dims[0], dims[-1], 7, 8)  # the inputs mlp_setup made
+    params = model.parameters()
+    p0 = [p.numpy().copy() for p in params]
+    zs = []
+    loss = train_step(model, opt, x, t, zs).to_vec()[0]
+    p1 = [p.numpy() for p in params]
+    hidden = [z.numpy().reshape(batch, -1) for z in zs[:-1]]
+    logits = zs[-1].numpy().reshape(batch, -1)
+    r = np.random.default_rng(12)
+    rows = [r.choice(d, min(d, 64), replace=False) for d in dims[1:-1]]
+    t0 = time.perf_counter()
+    rep = f64ref.check_mlp_step(xs, ts, p0, p1, loss, hidden, logits, rows=rows,
+                                batch_rows=r.choice(batch, min(batch, 64), replace=False))
+    rep["against"] = ("float64 on the device's own forward values: forward products on 64 batch rows, loss, "
+                      "effective gradients (p0-p1)/lr on 64 sampled rows per hidden layer, 1e-4 of sum|terms|")
+    rep["check_s"] = time.perf_counter() - t0
+    return rep
 
 
 COPY_SRC = r"""

@@ -24,21 +24,34 @@ class Mlp:
         self.layers = [Linear(dims[i], dims[i + 1], device) for i in range(len(dims) - 1)]
 
     def forward(self, x: Tensor) -> Tensor:
-        h = x
+        return self.forward_preactivations(x)[-1]
+
+    def forward_preactivations(self, x: Tensor) -> list:
+        """Every layer's output before its ReLU, the logits last. Holding
+        them across a train step keeps the reference's partition for them
+        (each is materialised anyway, as a multi-consumer node), and after the
+        step's realize they point at the buffers the step computed
+        (tensor.rs:222-252)."""
+        zs, h = [], x
         for i, layer in enumerate(self.layers):
             h = layer(h)
+            zs.append(h)
             if i + 1 < len(self.layers):
                 h = h.relu()
-        return h
+        return zs
 
     def parameters(self) -> list:
         return [p for layer in self.layers for p in layer.parameters()]
 
 
-def train_step(model: Mlp, opt: Sgd, x: Tensor, targets: Tensor) -> Tensor:
-    """One step as mnist.rs:90-97: forward, cross-entropy, zero_grad, backward, SGD."""
-    logits = model.forward(x)
-    loss = logits.cross_entropy(targets)
+def train_step(model: Mlp, opt: Sgd, x: Tensor, targets: Tensor, preactivations: list | None = None) -> Tensor:
+    """One step as mnist.rs:90-97: forward, cross-entropy, zero_grad, backward,
+    SGD. With a list for `preactivations`, the layers' outputs before ReLU
+    (logits last) are appended to it, realised by the step itself."""
+    zs = model.forward_preactivations(x)
+    if preactivations is not None:
+        preactivations.extend(zs)
+    loss = zs[-1].cross_entropy(targets)
     opt.zero_grad()
     loss.backward()
     opt.step()

@@ -15,8 +15,9 @@ Before a fixture is written its outputs are checked against an independent
 float64 computation in numpy (the elementwise case per operation, rounded to
 f32 after each op as IEEE arithmetic fixes it; reductions and products within
 1e-4 * sum|terms|; the train step by the textbook softmax-cross-entropy
-gradient (softmax - t)/B propagated by hand), so a fixture never records an
-oracle mistake. Run from the repository root:
+gradient (softmax - t)/B propagated by hand, each parameter's effective
+gradient (p0 - p1)/lr held to 1e-4 of the gradient's condition scale), so a
+fixture never records an oracle mistake. Run from the repository root:
 
     python tests/golden/make_golden.py
 """
@@ -30,6 +31,8 @@ import numpy as np
 HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(os.path.dirname(HERE))
 sys.path.insert(0, ROOT)
+sys.path.insert(0, os.path.dirname(HERE))
+import f64ref  # noqa: E402  (tests/f64ref.py)
 
 
 def c1_inputs():
@@ -115,10 +118,16 @@ def check_c3(inp, out):
 
 
 def mlp_step_f64(x, t, p0, lr=0.01):
+    """The two-layer step by hand, in float64: loss, params after SGD, the
+    gradients, and each gradient's condition scale (the same sum over its
+    terms with every input replaced by its absolute value, carried through
+    the layers: |x| -> |x|·|W1|ᵀ + |b1| -> ...)."""
     w1, b1, w2, b2 = (p.astype(np.float64) for p in p0)
     x, t = x.astype(np.float64), t.astype(np.float64)
     h_pre = x @ w1.T + b1
+    mask = h_pre > 0
     h = np.maximum(h_pre, 0)
+    h_s = np.where(mask, np.abs(x) @ np.abs(w1).T + np.abs(b1), 0.0)
     z = h @ w2.T + b2
     zs = z - z.max(1, keepdims=True)
     logp = zs - np.log(np.exp(zs).sum(1, keepdims=True))
@@ -126,19 +135,24 @@ def mlp_step_f64(x, t, p0, lr=0.01):
     B = x.shape[0]
     dz = (np.exp(logp) - t) / B
     dw2, db2 = dz.T @ h, dz.sum(0)
-    dh = (dz @ w2) * (h_pre > 0)
+    dh = (dz @ w2) * mask
     dw1, db1 = dh.T @ x, dh.sum(0)
+    dh_s = (np.abs(dz) @ np.abs(w2)) * mask
     grads = [dw1, db1, dw2, db2]
-    return loss, [p - lr * g for p, g in zip((w1, b1, w2, b2), grads)], grads
+    scales = [dh_s.T @ np.abs(x), dh_s.sum(0), np.abs(dz).T @ h_s, np.abs(dz).sum(0)]
+    lr32 = float(np.float32(lr))
+    return loss, [p - lr32 * g for p, g in zip((w1, b1, w2, b2), grads)], grads, scales
 
 
 def check_c4(inp, p0, loss, p1):
-    want_loss, want_p1, grads = mlp_step_f64(inp["x"], inp["t"], p0)
+    """Loss within 1e-5 relative; each parameter's effective gradient
+    (p0 - p1)/lr within 1e-4 of its condition scale plus the roundings of the
+    update itself (tests/f64ref.py: sgd_effective_gradient_err)."""
+    want_loss, _, grads, scales = mlp_step_f64(inp["x"], inp["t"], p0)
     assert abs(loss - want_loss) <= 1e-5 * abs(want_loss), ("c4 loss", loss, want_loss)
-    for got, want, p, g in zip(p1, want_p1, p0, grads):
-        # parameter after the update: the gradient term carries the reduction error
-        scale = np.abs(p) + 0.01 * (np.abs(g) + 1e-3)
-        assert within(got, want, scale, 1e-4), "c4 params vs float64"
+    for name, a, b, g, s in zip(("w1", "b1", "w2", "b2"), p0, p1, grads, scales):
+        worst = f64ref.sgd_effective_gradient_err(a, b, g, s)
+        assert worst <= 1.0, f"c4 {name}: effective gradient off by {worst:.3g} x bound"
 
 
 def main():

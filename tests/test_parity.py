@@ -7,7 +7,7 @@ reductions and matmuls within 1e-4 * sum|terms| per element.
 import numpy as np
 import pytest
 
-from conftest import rel_err_bound, seeded
+from conftest import check_recorded_steps, recorded_steps, rel_err_bound, seeded
 
 pytestmark = pytest.mark.gpu
 
@@ -170,43 +170,19 @@ def test_c3_linear_forward(fg, cpu, mnk):
     assert rel_err_bound(got, exact, scale, 1e-4) <= 1.0
 
 
-def mlp_step(fg, dev, x, t, hidden, seed=42, lr=0.01, steps=1, starts=None, batch=None):
-    """`steps` SGD steps; with `starts`, step i trains on rows
-    [starts[i], starts[i] + batch) of the resident x/t through narrow(), the
-    batching of examples/mnist.rs:46-62."""
-    fg.reset_init_seed(seed)
-    dims = [x.shape[1]] + list(hidden) + [t.shape[1]]
-    layers = [fg.Linear(dims[i], dims[i + 1], dev) for i in range(len(dims) - 1)]
-    params = [p for l in layers for p in l.parameters()]
-    opt = fg.Sgd(params, lr)
-    tx = fg.Tensor.new(x, list(x.shape), dev)
-    tt = fg.Tensor.new(t, list(t.shape), dev)
-    losses = []
-    for i in range(steps if starts is None else len(starts)):
-        h = tx if starts is None else tx.narrow(0, starts[i], batch)
-        ts = tt if starts is None else tt.narrow(0, starts[i], batch)
-        for i, l in enumerate(layers):
-            h = l(h)
-            if i + 1 < len(layers):
-                h = h.relu()
-        loss = h.cross_entropy(ts)
-        opt.zero_grad()
-        loss.backward()
-        opt.step()
-        losses.append(loss.to_vec()[0])
-    return losses, [p.numpy() for p in params]
-
-
 @pytest.mark.parametrize("batch,hidden,steps", [(8, (16,), 2), (256, (128,), 2), (64, (96, 64), 1)])
 def test_mlp_train_step(fg, cpu, batch, hidden, steps):
+    # Every step on each device product by product against float64 on that
+    # device's own values (forward products, loss, and each parameter's
+    # effective gradient (p0 - p1)/lr, all within 1e-4 of their scales); the
+    # two devices' losses within 1e-4 of each other.
     r = seeded(7)
     x = r.uniform(0, 1, (batch, 784)).astype(np.float32)
     labels = np.floor(r.uniform(0, 1, batch) * 10).astype(np.int64)
     t = np.eye(10, dtype=np.float32)[labels]
-    (lc, pc), (lh, ph) = both(lambda d: mlp_step(fg, d, x, t, hidden, steps=steps), cpu)
+    dims = (784,) + tuple(hidden) + (10,)
+    lc, lh = (check_recorded_steps(recorded_steps(fg, d, x, t, dims, steps=steps)) for d in (cpu, "hip"))
     np.testing.assert_allclose(lh, lc, rtol=1e-4)
-    for a, b in zip(ph, pc):
-        np.testing.assert_allclose(a, b, rtol=1e-4, atol=1e-6)
 
 
 def test_mlp_steps_on_narrowed_batches(fg, cpu):
@@ -217,10 +193,9 @@ def test_mlp_steps_on_narrowed_batches(fg, cpu):
     labels = np.floor(r.uniform(0, 1, 1024) * 10).astype(np.int64)
     t = np.eye(10, dtype=np.float32)[labels]
     starts = [0, 256, 512, 768, 256]
-    (lc, pc), (lh, ph) = both(lambda d: mlp_step(fg, d, x, t, (128,), starts=starts, batch=256), cpu)
+    lc, lh = (check_recorded_steps(recorded_steps(fg, d, x, t, (784, 128, 10), starts=starts, batch=256))
+              for d in (cpu, "hip"))
     np.testing.assert_allclose(lh, lc, rtol=1e-4)
-    for a, b in zip(ph, pc):
-        np.testing.assert_allclose(a, b, rtol=1e-4, atol=1e-6)
 
 
 @pytest.mark.parametrize("shape", [(8192, 512), (1000, 12), (4096, 4096), (3, 257), (256, 128)])

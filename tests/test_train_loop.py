@@ -53,7 +53,14 @@ def test_native_loop_matches_python_loop_hip(fg, cpu, batch, dims):
     assert l_nat == l_py
     for a, b in zip(p_nat, p_py):
         assert np.array_equal(a, b)
-    l_cpu, p_cpu = run(fg, cpu, dims, batch, 3, native=True)
+    # The loop's steps are the recorded steps' kernels: each step of the
+    # Python-driven loop, product by product against float64 on the device's
+    # own values, and the oracle's losses within 1e-4.
+    from conftest import check_recorded_steps, recorded_steps
+    from ferrograd_amd.mlp import synthetic_batch
+
+    xs, ts = synthetic_batch(batch, dims[0], dims[-1], 7, 8)
+    l_rec = check_recorded_steps(recorded_steps(fg, "hip", xs, ts, dims, steps=3))
+    assert np.allclose(l_rec, l_nat, rtol=1e-6)
+    l_cpu, _ = run(fg, cpu, dims, batch, 3, native=True)
     assert np.allclose(l_nat, l_cpu, rtol=1e-4, atol=1e-6)
-    for a, b in zip(p_nat, p_cpu):
-        np.testing.assert_allclose(a, b, rtol=1e-4, atol=1e-6)
