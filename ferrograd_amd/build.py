@@ -20,7 +20,7 @@ OBJ = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libferrograd_amd.so")
 
 SOURCES = ["ir.cpp", "device.cpp", "schedule.cpp", "tensor.cpp", "gpu_lower.cpp", "hip_device.cpp",
-           "hip_runtime.cpp", "dataset.cpp", "capi.cpp"]
+           "hip_runtime.cpp", "kernel_text.cpp", "hip_kernel.cpp", "dataset.cpp", "capi.cpp"]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 CXXFLAGS = ["-O2", "-g0", "-fPIC", "-std=c++17", "-Wall", "-Wno-unused-function",

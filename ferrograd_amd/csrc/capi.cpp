@@ -6,6 +6,7 @@
 #include <string>
 
 #include "gpu_lower.hpp"
+#include "kernel_text.hpp"
 #include "schedule.hpp"
 #include "tensor.hpp"
 
@@ -458,7 +459,9 @@ int fg_debug_plan(fg_tensor** roots, int n, int fuse, int render, char* buf, siz
         }
         os << "]";
         if (render) {
-          fg::UOp k = fg::gpu_optimize(fg::rangeify(it.sink));
+          fg::UOp rangeified = fg::rangeify(it.sink);
+          os << ", \"kernel\": \"" << json_escape(fg::kernel_to_text(rangeified)) << "\"";
+          fg::UOp k = fg::gpu_optimize(rangeified);
           auto rk = fg::render_hip_stable(k);
           os << ", \"name\": \"" << rk.name << "\", \"class\": \"" << rk.kind << "\", \"grid\": [" << rk.grid[0] << ", " << rk.grid[1] << ", "
              << rk.grid[2] << "], \"block\": [" << rk.block[0] << ", " << rk.block[1] << ", " << rk.block[2]

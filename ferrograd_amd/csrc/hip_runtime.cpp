@@ -85,15 +85,28 @@ bool read_file(const std::string& path, std::vector<char>* out) {
   return static_cast<bool>(f);
 }
 
+// Writes `data` to a temporary file and renames it into place only when every
+// byte reached the file, so a reader never sees a partial code object.
 void write_file_atomic(const std::string& path, const std::vector<char>& data) {
   std::string tmp = path + ".tmp" + std::to_string(getpid());
+  bool ok;
   {
     std::ofstream f(tmp, std::ios::binary);
-    if (!f) return;
     f.write(data.data(), static_cast<std::streamsize>(data.size()));
-    if (!f) return;
+    f.flush();
+    ok = static_cast<bool>(f);
+    f.close();
+    ok = ok && !f.fail();
   }
-  std::rename(tmp.c_str(), path.c_str());
+  if (!ok || std::rename(tmp.c_str(), path.c_str()) != 0) std::remove(tmp.c_str());
+}
+
+// The hiprtc version, part of every cache key: a code object cached by one
+// toolchain is never loaded under another.
+std::string hiprtc_version() {
+  int major = 0, minor = 0;
+  if (hiprtcVersion(&major, &minor) != HIPRTC_SUCCESS) return "hiprtc ?";
+  return "hiprtc " + std::to_string(major) + "." + std::to_string(minor);
 }
 
 }  // namespace
@@ -324,34 +337,49 @@ int fg_hip_copy_d2d(fg_ctx* c, void* dst, const void* src, size_t n) {
   return FG_OK;
 }
 
-int fg_hip_compile(fg_ctx* c, const char* source, const char* func, int num_args, fg_prog** out) {
-  if (!source || !func || !out) return set_err(FG_ERR_INVALID, "fg_hip_compile: null argument");
-  std::string src(source);
-  std::string key_material = src;
+namespace {
+// hiprtc compile of `source` into `code`.
+int rtc_compile(const char* source, const char* func, std::vector<char>* code) {
+  hiprtcProgram prog;
+  hiprtcResult r = hiprtcCreateProgram(&prog, source, (std::string(func) + ".hip").c_str(), 0, nullptr, nullptr);
+  if (r != HIPRTC_SUCCESS) return set_err(FG_ERR_COMPILE, std::string("hiprtcCreateProgram: ") + hiprtcGetErrorString(r));
+  r = hiprtcCompileProgram(prog, kNumRtcOptions, kRtcOptions);
+  if (r != HIPRTC_SUCCESS) {
+    size_t ls = 0;
+    hiprtcGetProgramLogSize(prog, &ls);
+    std::string log(ls, '\0');
+    if (ls) hiprtcGetProgramLog(prog, &log[0]);
+    hiprtcDestroyProgram(&prog);
+    return set_err(FG_ERR_COMPILE, "hiprtc compilation failed:\n" + log);
+  }
+  size_t cs = 0;
+  hiprtcGetCodeSize(prog, &cs);
+  code->resize(cs);
+  hiprtcGetCode(prog, code->data());
+  hiprtcDestroyProgram(&prog);
+  return FG_OK;
+}
+
+// Where the code object of `source` is cached: a file named by the FNV-1a
+// hash of the source, every compile option (the gfx950 target included) and
+// the hiprtc version.
+std::string cache_path(const char* source) {
+  std::string key_material = std::string(source) + "\n" + hiprtc_version();
   for (int i = 0; i < kNumRtcOptions; i++) key_material += std::string("\n") + kRtcOptions[i];
   char hex[32];
   std::snprintf(hex, sizeof(hex), "%016llx", static_cast<unsigned long long>(fnv1a(key_material)));
+  return cache_dir() + "/" + hex + ".co";
+}
+}  // namespace
+
+int fg_hip_compile(fg_ctx* c, const char* source, const char* func, int num_args, fg_prog** out) {
+  if (!source || !func || !out) return set_err(FG_ERR_INVALID, "fg_hip_compile: null argument");
   std::string dir = cache_dir();
-  std::string path = dir + "/" + hex + ".co";
+  std::string path = cache_path(source);
   std::vector<char> code;
-  if (!read_file(path, &code)) {
-    hiprtcProgram prog;
-    hiprtcResult r = hiprtcCreateProgram(&prog, source, (std::string(func) + ".hip").c_str(), 0, nullptr, nullptr);
-    if (r != HIPRTC_SUCCESS) return set_err(FG_ERR_COMPILE, std::string("hiprtcCreateProgram: ") + hiprtcGetErrorString(r));
-    r = hiprtcCompileProgram(prog, kNumRtcOptions, kRtcOptions);
-    if (r != HIPRTC_SUCCESS) {
-      size_t ls = 0;
-      hiprtcGetProgramLogSize(prog, &ls);
-      std::string log(ls, '\0');
-      if (ls) hiprtcGetProgramLog(prog, &log[0]);
-      hiprtcDestroyProgram(&prog);
-      return set_err(FG_ERR_COMPILE, "hiprtc compilation failed:\n" + log);
-    }
-    size_t cs = 0;
-    hiprtcGetCodeSize(prog, &cs);
-    code.resize(cs);
-    hiprtcGetCode(prog, code.data());
-    hiprtcDestroyProgram(&prog);
+  bool cached = read_file(path, &code);
+  if (!cached) {
+    if (int rc = rtc_compile(source, func, &code)) return rc;
     mkdir(dir.c_str(), 0755);
     write_file_atomic(path, code);
   }
@@ -365,6 +393,17 @@ int fg_hip_compile(fg_ctx* c, const char* source, const char* func, int num_args
   p->name = func;
   p->module = std::make_shared<ModuleRef>();
   hipError_t e = hipModuleLoadData(&p->module->module, code.data());
+  if (e != hipSuccess && cached) {
+    // A cached file the runtime rejects (damaged, or written by something
+    // else) is replaced by a fresh compile, once.
+    std::remove(path.c_str());
+    if (int rc = rtc_compile(source, func, &code)) {
+      delete p;
+      return rc;
+    }
+    write_file_atomic(path, code);
+    e = hipModuleLoadData(&p->module->module, code.data());
+  }
   if (e != hipSuccess) {
     delete p;
     return set_err(FG_ERR_HIP, std::string("hipModuleLoadData: ") + hipGetErrorString(e));
@@ -377,6 +416,14 @@ int fg_hip_compile(fg_ctx* c, const char* source, const char* func, int num_args
   *out = p;
   return FG_OK;
 }
+
+const char* fg_hip_code_object_path(const char* source) {
+  static thread_local std::string path;
+  path = cache_path(source ? source : "");
+  return path.c_str();
+}
+
+int fg_hip_set_error(int code, const char* msg) { return set_err(code, msg ? msg : ""); }
 
 int fg_hip_program_function(fg_prog* prog, const char* func, int num_args, fg_prog** out) {
   if (!prog || !func || !out) return set_err(FG_ERR_INVALID, "fg_hip_program_function: null argument");

@@ -87,6 +87,17 @@ def api() -> ctypes.CDLL:
             "fg_hip_profile_read": (c_int, [P, ctypes.c_char_p, c_size, ctypes.POINTER(c_size)]),
             "fg_device_context": (c_int, [c_int, PP]),
             "fg_hip_last_error": (ctypes.c_char_p, []),
+            "fg_hip_render": (c_int, [ctypes.c_char_p, PP]),
+            "fg_hip_rendered_info": (c_int, [P, ctypes.POINTER(ctypes.c_char_p), ctypes.POINTER(ctypes.c_char_p),
+                                             ctypes.POINTER(c_int), ctypes.POINTER(c_int), ctypes.POINTER(c_size)]),
+            "fg_hip_rendered_param": (c_int, [P, c_int, ctypes.POINTER(c_int)]),
+            "fg_hip_rendered_launch": (c_int, [P, c_int, ctypes.POINTER(ctypes.c_char_p), uint3, uint3,
+                                               ctypes.POINTER(ctypes.c_uint)]),
+            "fg_hip_rendered_free": (c_int, [P]),
+            "fg_hip_kernel_load": (c_int, [P, P, PP]),
+            "fg_hip_kernel_run": (c_int, [P, P, ctypes.POINTER(Arg), c_int]),
+            "fg_hip_kernel_free": (c_int, [P]),
+            "fg_hip_code_object_path": (ctypes.c_char_p, [ctypes.c_char_p]),
         }
         for name, (res, args) in sigs.items():
             f = getattr(l, name)
@@ -218,3 +229,57 @@ class Context:
         arch = ctypes.create_string_buffer(64)
         check(api().fg_hip_device_info(self.h, ctypes.byref(cu), ctypes.byref(clk), ctypes.byref(lds), arch, 64))
         return {"cu_count": cu.value, "clock_khz": clk.value, "lds_per_block": lds.value, "arch": arch.value.decode()}
+
+
+class Rendered:
+    """fg_hip_render: one rangeified kernel (its fg-kernel text) rendered for
+    gfx950, with its launch passes, parameter kinds and scratch size."""
+
+    def __init__(self, kernel_text: str):
+        h = ctypes.c_void_p()
+        check(api().fg_hip_render(kernel_text.encode(), ctypes.byref(h)))
+        self.h = h
+        src, kind = ctypes.c_char_p(), ctypes.c_char_p()
+        npar, nl, scratch = ctypes.c_int(), ctypes.c_int(), ctypes.c_size_t()
+        check(api().fg_hip_rendered_info(h, ctypes.byref(src), ctypes.byref(kind), ctypes.byref(npar),
+                                         ctypes.byref(nl), ctypes.byref(scratch)))
+        self.source, self.kind, self.scratch_bytes = src.value.decode(), kind.value.decode(), scratch.value
+        self.params = []
+        for i in range(npar.value):
+            k = ctypes.c_int()
+            check(api().fg_hip_rendered_param(h, i, ctypes.byref(k)))
+            self.params.append(k.value)
+        self.launches = []
+        for i in range(nl.value):
+            f, g, b, lds = ctypes.c_char_p(), (ctypes.c_uint * 3)(), (ctypes.c_uint * 3)(), ctypes.c_uint()
+            check(api().fg_hip_rendered_launch(h, i, ctypes.byref(f), g, b, ctypes.byref(lds)))
+            self.launches.append({"func": f.value.decode(), "grid": tuple(g), "block": tuple(b), "lds": lds.value})
+
+    def __del__(self):
+        if getattr(self, "h", None):
+            api().fg_hip_rendered_free(self.h)
+            self.h = None
+
+
+class Kernel:
+    """A rendered kernel loaded on a context (fg_hip_kernel_load)."""
+
+    def __init__(self, ctx: "Context", rendered: Rendered):
+        h = ctypes.c_void_p()
+        check(api().fg_hip_kernel_load(ctx.h, rendered.h, ctypes.byref(h)))
+        self.h, self.ctx, self.rendered = h, ctx, rendered
+
+    def run(self, args) -> None:
+        """fg_hip_kernel_run: every pass, with the library's scratch."""
+        arr = (Arg * max(1, len(args)))(*args)
+        check(api().fg_hip_kernel_run(self.ctx.h, self.h, arr, len(args)))
+
+    def __del__(self):
+        if getattr(self, "h", None):
+            api().fg_hip_kernel_free(self.h)
+            self.h = None
+
+
+def code_object_path(source: str) -> str:
+    """Where fg_hip_compile caches the code object of `source`."""
+    return api().fg_hip_code_object_path(source.encode()).decode()

@@ -140,7 +140,8 @@ int fg_set_graph_min_launches(int n, int* previous);
 
 /* Inspection for tests and tooling: schedule the roots (without running
  * anything) and describe the plan as JSON; optionally render each kernel with
- * the HIP code generator (no device needed). Two calls: with buf == NULL it
+ * the HIP code generator (no device needed), adding each kernel's rangeified
+ * form as fg_hip_render's kernel text ("kernel"). Two calls: with buf == NULL it
  * plans and reports the JSON size in *needed; with a buffer it copies the
  * JSON of the last plan on this thread. */
 int fg_debug_plan(fg_tensor** roots, int n, int fuse, int render_hip, char* buf, size_t len, size_t* needed);

@@ -116,6 +116,59 @@ int fg_hip_graph_create(fg_ctx* ctx, int n, fg_prog* const* progs, const unsigne
 int fg_hip_graph_launch(fg_ctx* ctx, fg_graph* graph, const fg_arg* args, int* updated);
 int fg_hip_graph_free(fg_graph* graph);
 
+/* The Renderer half of the boundary. The reference renders a kernel with
+ * `Renderer::render(uops, name) -> String` (src/codegen.rs:17-20), called with
+ * a hard-coded ClangRenderer in execute_item (src/tensor.rs:845-852), and
+ * compiles the string with no launch geometry (device.rs:309-314). For this
+ * device a caller hands over the kernel as rangeify leaves it
+ * (rangeify.rs:42-206, parameterised by schedule.rs:131-170), in the text
+ * form below, and gets back everything a launch needs: the gfx950 HIP source,
+ * the launch passes in order (function, grid, block, LDS bytes), the kinds of
+ * the kernel parameters in slot order (FG_ARG_*), and the bytes of scratch
+ * the passes share (split-K and split column-reduction partials; written
+ * before read, so never zeroed). The gfx950 passes of `optimize`
+ * (optimize/mod.rs:116-141 on the CPU) run inside: launch mapping, DPP/LDS
+ * reductions, MFMA GEMM recognition.
+ *
+ * Kernel text: a header line "fg-kernel 1", then one node per line in
+ * topological order, line i defining node i:
+ *   <Op> <dtype> <arg> [#<tag>] [<source node numbers>...]
+ * Op is the uop.rs:26-339 variant name; dtype f32|i32|bool|void (xN for
+ * vectors); arg "-", device:hip, int:<n>, bool:<0|1>, float:<16 hex digits of
+ * the f64 bits>, range:<axis>:<LOOP|GLOBAL|REDUCE|...>, param:<slot>:<numel>,
+ * scalar:<slot>, index:<n>, reduce:<Op>:<axes,...>, axes:/shape:/bounds:/
+ * lanes:<list>, var:<name>:<min>:<max>. The last node is the kernel's Sink.
+ * Malformed text fails with FG_ERR_INVALID and a message naming the line. */
+typedef struct fg_rendered fg_rendered;
+int fg_hip_render(const char* kernel_text, fg_rendered** out);
+/* Any output pointer may be NULL. Strings live as long as the fg_rendered. */
+int fg_hip_rendered_info(const fg_rendered* r, const char** source, const char** kind, int* num_params,
+                         int* num_launches, size_t* scratch_bytes);
+int fg_hip_rendered_param(const fg_rendered* r, int slot, int* kind);
+int fg_hip_rendered_launch(const fg_rendered* r, int i, const char** func, unsigned grid[3], unsigned block[3],
+                           unsigned* lds_bytes);
+int fg_hip_rendered_free(fg_rendered* r);
+
+/* A rendered kernel compiled (fg_hip_compile's cache applies) and loaded:
+ * Device::compile (device.rs:309-314) with the geometry attached.
+ * fg_hip_kernel_run is Device::execute (device.rs:321, cpu.rs:328-380) for it:
+ * the arguments in slot order, as the kernel's parameter kinds require (a
+ * wrong count or kind fails with FG_ERR_ARGS before anything is queued); every
+ * pass is queued on the context's stream. A kernel with scratch gets it from
+ * the library: allocated with fg_hip_alloc by the first run, kept with the
+ * kernel, reused by later runs on the same context, freed with the kernel. */
+typedef struct fg_kernel fg_kernel;
+int fg_hip_kernel_load(fg_ctx* ctx, const fg_rendered* r, fg_kernel** out);
+int fg_hip_kernel_run(fg_ctx* ctx, fg_kernel* k, const fg_arg* args, int nargs);
+int fg_hip_kernel_free(fg_kernel* k);
+
+/* The file fg_hip_compile caches the code object of `source` in: named by a
+ * hash of the source, every hiprtc option (the gfx950 target among them) and
+ * the hiprtc version. A cached file the runtime rejects is compiled again.
+ * No reference counterpart (the reference compiles into a temporary
+ * directory, cpu.rs:151-208). */
+const char* fg_hip_code_object_path(const char* source);
+
 /* Timing events on the context's stream (slots 0..63). */
 int fg_hip_event_record(fg_ctx* ctx, int slot);
 int fg_hip_event_elapsed_ms(fg_ctx* ctx, int start_slot, int end_slot, float* ms);
