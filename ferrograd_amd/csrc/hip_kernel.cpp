@@ -8,17 +8,32 @@
 // the source, the launch passes (function, grid, block, LDS) in order, the
 // kernel parameters in slot order with their kinds, and the bytes of scratch
 // its passes share (split-K and split column-reduction partials).
+#include <hip/hip_runtime.h>
+
 #include <cstring>
 #include <map>
 #include <memory>
+#include <mutex>
 #include <string>
 #include <vector>
 
 #include "../../include/ferrograd_hip.h"
 #include "gpu_lower.hpp"
+#include "hip_internal.hpp"
 #include "kernel_text.hpp"
 
-extern "C" int fg_hip_set_error(int code, const char* msg);
+// Scratch of fg_hip_kernel_run_noalloc: FG_NOALLOC_SCRATCH_BYTES on every GPU
+// the library is initialised on, held until the process ends. Host code never
+// uses this name as an address (on the host it is a stand-in for the symbol):
+// fg_hip_kernel_device_setup looks up each device's copy once and every later
+// use goes through that pointer.
+static __device__ __align__(256) unsigned char scratch[FG_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+void* g_scratch_ptr[kMaxDevices] = {};  // device address of `scratch` per ordinal
+}  // namespace
 
 struct fg_rendered {
   fg::RenderedKernel rk;
@@ -50,9 +65,9 @@ int guard(const char* what, F&& f) {
   }
 }
 
-// The launch arguments: the caller's, checked against the kernel's
-// parameter kinds, then the scratch pointer when the kernel has scratch.
-int marshal(const fg_kernel* k, const fg_arg* args, int nargs, void* scratch, std::vector<fg_arg>* out) {
+// The caller's arguments against the kernel's parameter kinds. Builds no
+// heap object unless it reports an error.
+int check_args(const fg_kernel* k, const fg_arg* args, int nargs) {
   if (nargs != static_cast<int>(k->param_kinds.size()))
     return fg_hip_set_error(FG_ERR_ARGS, ("kernel takes " + std::to_string(k->param_kinds.size()) +
                                           " arguments, got " + std::to_string(nargs)).c_str());
@@ -69,22 +84,34 @@ int marshal(const fg_kernel* k, const fg_arg* args, int nargs, void* scratch, st
     if (args[i].kind == FG_ARG_PTR && !args[i].v.p)
       return fg_hip_set_error(FG_ERR_INVALID, ("argument " + std::to_string(i) + " is a null pointer").c_str());
   }
-  out->assign(args, args + nargs);
+  return FG_OK;
+}
+
+// The launch arguments: the caller's, then the scratch pointer when the
+// kernel has scratch. `out` holds at least 65 entries (launches take at most
+// 64 arguments, fg_hip_launch's limit, which it checks).
+int launch_args(const fg_kernel* k, const fg_arg* args, int nargs, void* scratch_ptr, fg_arg* out, int* n) {
+  if (int rc = check_args(k, args, nargs)) return rc;
+  if (nargs > 64) return fg_hip_set_error(FG_ERR_ARGS, "a kernel takes at most 64 arguments");
+  if (nargs) std::memcpy(out, args, sizeof(fg_arg) * static_cast<size_t>(nargs));
+  *n = nargs;
   if (k->scratch_bytes) {
-    fg_arg s;
-    std::memset(&s, 0, sizeof(s));
-    s.kind = FG_ARG_PTR;
-    s.v.p = scratch;
-    out->push_back(s);
+    std::memset(&out[nargs], 0, sizeof(fg_arg));
+    out[nargs].kind = FG_ARG_PTR;
+    out[nargs].v.p = scratch_ptr;
+    *n = nargs + 1;
   }
   return FG_OK;
 }
 
-int launch_all(fg_ctx* ctx, const fg_kernel* k, const std::vector<fg_arg>& a) {
+// Queues every pass. `direct` launches skip launch profiling, which records
+// events.
+int launch_all(fg_ctx* ctx, const fg_kernel* k, const fg_arg* a, int n, bool direct) {
   for (size_t i = 0; i < k->passes.size(); i++) {
     const fg::LaunchSpec& l = k->launches[i];
-    if (int rc = fg_hip_launch(ctx, k->passes[i], a.data(), static_cast<int>(a.size()), l.grid, l.block, l.lds_bytes))
-      return rc;
+    int rc = direct ? fg_hip_launch_direct(ctx, k->passes[i], a, n, l.grid, l.block, l.lds_bytes)
+                    : fg_hip_launch(ctx, k->passes[i], a, n, l.grid, l.block, l.lds_bytes);
+    if (rc) return rc;
   }
   return FG_OK;
 }
@@ -191,9 +218,44 @@ int fg_hip_kernel_run(fg_ctx* ctx, fg_kernel* k, const fg_arg* args, int nargs) 
   }
   if (k->scratch && k->scratch_ctx != ctx)
     return fg_hip_set_error(FG_ERR_INVALID, "fg_hip_kernel_run: the kernel's scratch belongs to another context");
-  std::vector<fg_arg> a;
-  if (int rc = marshal(k, args, nargs, k->scratch, &a)) return rc;
-  return launch_all(ctx, k, a);
+  fg_arg a[65];
+  int n = 0;
+  if (int rc = launch_args(k, args, nargs, k->scratch, a, &n)) return rc;
+  return launch_all(ctx, k, a, n, false);
+}
+
+int fg_hip_kernel_device_setup(int ordinal) {
+  if (ordinal < 0 || ordinal >= kMaxDevices)
+    return fg_hip_set_error(FG_ERR_INVALID, ("device ordinal " + std::to_string(ordinal) + " beyond the " +
+                                             std::to_string(kMaxDevices) + " this library supports").c_str());
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (g_scratch_ptr[ordinal]) return FG_OK;
+  void* ptr = nullptr;
+  hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+  if (e != hipSuccess || !ptr)
+    return fg_hip_set_error(FG_ERR_HIP, (std::string("hipGetSymbolAddress(scratch) on device ") +
+                                         std::to_string(ordinal) + ": " + hipGetErrorString(e))
+                                            .c_str());
+  g_scratch_ptr[ordinal] = ptr;
+  return FG_OK;
+}
+
+int fg_hip_kernel_run_noalloc(fg_ctx* ctx, fg_kernel* k, const fg_arg* args, int nargs) {
+  if (!ctx || !k) return fg_hip_set_error(FG_ERR_INVALID, "fg_hip_kernel_run_noalloc: null argument");
+  if (k->scratch_bytes > FG_NOALLOC_SCRATCH_BYTES)
+    return fg_hip_set_error(FG_ERR_INVALID, ("fg_hip_kernel_run_noalloc: the kernel needs " +
+                                             std::to_string(k->scratch_bytes) + " bytes of scratch, more than the " +
+                                             std::to_string(FG_NOALLOC_SCRATCH_BYTES) +
+                                             " the library holds per GPU; run it with fg_hip_kernel_run")
+                                                .c_str());
+  const int dev = fg_hip_context_device(ctx);
+  void* ptr = dev >= 0 && dev < kMaxDevices ? g_scratch_ptr[dev] : nullptr;
+  if (k->scratch_bytes && !ptr)
+    return fg_hip_set_error(FG_ERR_INVALID, "fg_hip_kernel_run_noalloc: no scratch set up for this context's device");
+  fg_arg a[65];
+  int n = 0;
+  if (int rc = launch_args(k, args, nargs, ptr, a, &n)) return rc;
+  return launch_all(ctx, k, a, n, true);
 }
 
 int fg_hip_kernel_free(fg_kernel* k) {

@@ -22,6 +22,7 @@
 #include <vector>
 
 #include "../../include/ferrograd_hip.h"
+#include "hip_internal.hpp"
 
 namespace {
 
@@ -196,6 +197,7 @@ int fg_hip_init(int ordinal, fg_ctx** out) {
     return set_err(FG_ERR_INVALID, "fg_hip_init: device ordinal " + std::to_string(ordinal) + " out of range (" +
                                        std::to_string(count) + " devices)");
   HIP_TRY(hipSetDevice(ordinal));
+  if (int rc = fg_hip_kernel_device_setup(ordinal)) return rc;
   auto* c = new fg_ctx();
   c->device = ordinal;
   hipError_t e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking);
@@ -477,14 +479,34 @@ bool same_args(const fg_arg* a, const fg_arg* b, int n) {
 }
 }  // namespace
 
-int fg_hip_launch(fg_ctx* c, fg_prog* p, const fg_arg* args, int nargs, const unsigned grid[3],
-                  const unsigned block[3], unsigned lds) {
+namespace {
+// The checks every launch makes before anything is queued.
+int check_launch(const fg_ctx* c, const fg_prog* p, int nargs, const unsigned grid[3], const unsigned block[3]) {
   if (!c || !p || !grid || !block) return set_err(FG_ERR_INVALID, "fg_hip_launch: null argument");
   if (nargs != p->num_args)
     return set_err(FG_ERR_ARGS, "expected " + std::to_string(p->num_args) + " kernel args, got " + std::to_string(nargs));
   if (block[0] * block[1] * block[2] == 0 || block[0] * block[1] * block[2] > 1024)
     return set_err(FG_ERR_INVALID, "fg_hip_launch: block size must be in [1, 1024]");
   if (grid[0] == 0 || grid[1] == 0 || grid[2] == 0) return set_err(FG_ERR_INVALID, "fg_hip_launch: empty grid");
+  return FG_OK;
+}
+}  // namespace
+
+int fg_hip_launch_direct(fg_ctx* c, fg_prog* p, const fg_arg* args, int nargs, const unsigned grid[3],
+                         const unsigned block[3], unsigned lds) {
+  if (int rc = check_launch(c, p, nargs, grid, block)) return rc;
+  void* params[64];
+  if (int rc = marshal_args(args, nargs, params)) return rc;
+  HIP_TRY(hipModuleLaunchKernel(p->func, grid[0], grid[1], grid[2], block[0], block[1], block[2], lds, c->stream,
+                                params, nullptr));
+  return FG_OK;
+}
+
+int fg_hip_context_device(const fg_ctx* c) { return c ? c->device : -1; }
+
+int fg_hip_launch(fg_ctx* c, fg_prog* p, const fg_arg* args, int nargs, const unsigned grid[3],
+                  const unsigned block[3], unsigned lds) {
+  if (int rc = check_launch(c, p, nargs, grid, block)) return rc;
   void* params[64];
   if (int rc = marshal_args(args, nargs, params)) return rc;
   if (c->profiling) {

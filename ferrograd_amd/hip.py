@@ -11,6 +11,7 @@ from . import lib
 
 FG_ARG_PTR, FG_ARG_I32, FG_ARG_F32, FG_ARG_BOOL = 0, 1, 2, 3
 FG_OK, FG_ERR_HIP, FG_ERR_COMPILE, FG_ERR_SYMBOL, FG_ERR_ARGS, FG_ERR_INVALID = range(6)
+FG_NOALLOC_SCRATCH_BYTES = 64 << 20  # include/ferrograd_hip.h
 
 
 class _Val(ctypes.Union):
@@ -97,6 +98,7 @@ def api() -> ctypes.CDLL:
             "fg_hip_kernel_load": (c_int, [P, P, PP]),
             "fg_hip_kernel_run": (c_int, [P, P, ctypes.POINTER(Arg), c_int]),
             "fg_hip_kernel_free": (c_int, [P]),
+            "fg_hip_kernel_run_noalloc": (c_int, [P, P, ctypes.POINTER(Arg), c_int]),
             "fg_hip_code_object_path": (ctypes.c_char_p, [ctypes.c_char_p]),
         }
         for name, (res, args) in sigs.items():
@@ -273,6 +275,12 @@ class Kernel:
         """fg_hip_kernel_run: every pass, with the library's scratch."""
         arr = (Arg * max(1, len(args)))(*args)
         check(api().fg_hip_kernel_run(self.ctx.h, self.h, arr, len(args)))
+
+    def run_noalloc(self, args) -> None:
+        """fg_hip_kernel_run_noalloc: every pass, with the library's static
+        per-GPU scratch; allocates nothing."""
+        arr = (Arg * max(1, len(args)))(*args)
+        check(api().fg_hip_kernel_run_noalloc(self.ctx.h, self.h, arr, len(args)))
 
     def __del__(self):
         if getattr(self, "h", None):

@@ -162,6 +162,21 @@ int fg_hip_kernel_load(fg_ctx* ctx, const fg_rendered* r, fg_kernel** out);
 int fg_hip_kernel_run(fg_ctx* ctx, fg_kernel* k, const fg_arg* args, int nargs);
 int fg_hip_kernel_free(fg_kernel* k);
 
+/* fg_hip_kernel_run that allocates nothing. No counterpart in the reference
+ * (its CPU backend allocates on the host as it likes): it is for callers that
+ * cannot allocate device memory, such as code under HIP graph capture and
+ * tight serving loops. Its scratch is a static device array of
+ * FG_NOALLOC_SCRATCH_BYTES that the library holds on every GPU fg_hip_init
+ * was called for, until the process ends; a kernel needing more is rejected
+ * with FG_ERR_INVALID before anything is queued. It calls no hipMalloc or
+ * hipFree and records no profiling events. The scratch of one GPU is shared
+ * by every call on it and keeps the last call's contents (the kernels write
+ * every partial before reading it, so nothing needs clearing); calls that
+ * overlap on one GPU, from contexts whose streams run concurrently, race on
+ * it. Calls on one context are ordered by its stream and do not. */
+#define FG_NOALLOC_SCRATCH_BYTES ((size_t)64 << 20)
+int fg_hip_kernel_run_noalloc(fg_ctx* ctx, fg_kernel* k, const fg_arg* args, int nargs);
+
 /* The file fg_hip_compile caches the code object of `source` in: named by a
  * hash of the source, every hiprtc option (the gfx950 target among them) and
  * the hiprtc version. A cached file the runtime rejects is compiled again.
