@@ -261,13 +261,17 @@ def bench_mlp(fg, ctx, steps, warmup, batch, dims):
     # for all timed steps, each step still reading its loss back.
     train_steps_native(model, opt, x, t, warmup)
     fg.synchronize()
-    h0 = fg.stats()["host_ms"]
+    s0 = fg.stats()
     t0 = time.perf_counter()
     native_losses = train_steps_native(model, opt, x, t, steps)
     fg.synchronize()
     ms_native = (time.perf_counter() - t0) * 1000.0 / steps
-    h1 = fg.stats()["host_ms"]
+    s1 = fg.stats()
+    h0, h1 = s0["host_ms"], s1["host_ms"]
     host_native = {k: (h1[k] - h0[k]) / steps for k in h1}
+    # Steps of the timed call launched from its step capture (the call's
+    # first steps record the plans and its last step runs in full).
+    replayed = s1["steps_replayed"] - s0["steps_replayed"]
     host = timed.host_ms
     kern = by_kernel(prof, steps)
     check = check_mlp_step_on_device(fg, model, opt, x, t, batch, dims)
@@ -279,8 +283,10 @@ def bench_mlp(fg, ctx, steps, warmup, batch, dims):
     flops = mlp_gemm_flops(batch, dims)
     tf = lambda t: flops / (t / 1e3) / 1e12 / FP32_MFMA_PEAK_TFLOPS if t else None  # noqa: E731
     return {"ms_per_step": ms_native, "steps_per_s": 1e3 / ms_native,
-            "caller": "native loop (fg_mlp_train_steps, examples/mnist.rs:84-101 restated); "
+            "caller": "native loop (fg_mlp_train_steps, examples/mnist.rs:84-101 restated, one call for all timed "
+                      "steps; steps after the first repeated ones launch from the step capture as one HIP graph); "
                       "*_python: the same steps driven op by op from Python",
+            "native_steps_from_capture": replayed,
             "ms_per_step_python": ms, "steps_per_s_python": 1e3 / ms,
             "device_ms_per_step": dev_ms, "host_ms_per_step": host_native, "host_ms_per_step_python": host,
             "kernels_per_step": sum(v["calls_per_step"] for v in kern.values()),

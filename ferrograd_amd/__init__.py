@@ -92,6 +92,7 @@ def _declare(l: ctypes.CDLL) -> None:
         "fg_synchronize": (c_int, [c_int]),
         "fg_stats": (c_int, [ctypes.POINTER(ctypes.c_uint64)] * 3),
         "fg_graph_stats": (c_int, [ctypes.POINTER(ctypes.c_uint64)] * 2),
+        "fg_step_capture_stats": (c_int, [ctypes.POINTER(ctypes.c_uint64)] * 2),
         "fg_clear_caches": (c_int, []),
         "fg_host_times": (c_int, [ctypes.POINTER(ctypes.c_uint64)]),
         "fg_plan_cache_enable": (c_int, [c_int]),
@@ -452,8 +453,11 @@ def stats() -> dict:
     names = ("schedule", "lower", "launch", "apply_map", "backward")
     g, u = ctypes.c_uint64(), ctypes.c_uint64()
     lib().fg_graph_stats(ctypes.byref(g), ctypes.byref(u))
+    sc, sr = ctypes.c_uint64(), ctypes.c_uint64()
+    lib().fg_step_capture_stats(ctypes.byref(sc), ctypes.byref(sr))
     return {"kernels_launched": k.value, "programs_compiled": p.value, "lowering_cache_hits": h.value,
             "graph_replays": g.value, "graph_updated_launches": u.value,
+            "steps_captured": sc.value, "steps_replayed": sr.value,
             "host_ms": {n: t[i] / 1e6 for i, n in enumerate(names)}}
 
 

@@ -371,6 +371,12 @@ int fg_stats(uint64_t* k, uint64_t* p, uint64_t* h) {
   return 0;
 }
 
+int fg_step_capture_stats(uint64_t* captured, uint64_t* replayed) {
+  if (captured) *captured = fg::realize_stats().steps_captured;
+  if (replayed) *replayed = fg::realize_stats().steps_replayed;
+  return 0;
+}
+
 int fg_graph_stats(uint64_t* replays, uint64_t* updated_launches) {
   if (replays) *replays = fg::realize_stats().graph_replays;
   if (updated_launches) *updated_launches = fg::realize_stats().graph_updates;

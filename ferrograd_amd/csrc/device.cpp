@@ -37,6 +37,26 @@ void Device::insert_program(const UOp& sink, std::shared_ptr<Program> p) { progr
 
 void Device::clear_for_tests() { programs_.clear(); }
 
+void Device::read_async(const Buffer& b, int slot) {
+  std::vector<uint8_t> bytes = copy_to_host(b);
+  for (auto& s : read_slots_)
+    if (s.first == slot) {
+      s.second = std::move(bytes);
+      return;
+    }
+  read_slots_.emplace_back(slot, std::move(bytes));
+}
+
+std::vector<uint8_t> Device::read_wait(int slot) {
+  for (auto it = read_slots_.begin(); it != read_slots_.end(); ++it)
+    if (it->first == slot) {
+      std::vector<uint8_t> out = std::move(it->second);
+      read_slots_.erase(it);
+      return out;
+    }
+  fail("read_wait: no read queued in slot " + std::to_string(slot));
+}
+
 namespace {
 Device* g_devices[2] = {nullptr, nullptr};
 }

@@ -106,6 +106,12 @@ class Device {
   virtual void release(BufferInner& b) = 0;
   virtual void copy_from_host(const Buffer& b, const void* src, size_t nbytes) = 0;
   virtual std::vector<uint8_t> copy_to_host(const Buffer& b) = 0;
+  // A read-back that need not finish before the caller queues more work:
+  // read_async takes the buffer's bytes (as copy_to_host would) into `slot`
+  // once the device has run what is already queued; read_wait returns them.
+  // A device that runs synchronously, as the default does, copies at once.
+  virtual void read_async(const Buffer& b, int slot);
+  virtual std::vector<uint8_t> read_wait(int slot);
 
   // Kernel pipeline after rangeify.
   virtual UOp optimize(const UOp& rangeified) = 0;
@@ -133,6 +139,9 @@ class Device {
 
  protected:
   UOpMap<std::shared_ptr<Program>> programs_;
+
+ private:
+  std::vector<std::pair<int, std::vector<uint8_t>>> read_slots_;
 };
 
 // Registry (device.rs:334-354). The HIP device is built in; the CPU device is

@@ -90,6 +90,22 @@ class HipDevice : public Device {
     return out;
   }
 
+  void read_async(const Buffer& b, int slot) override {
+    FG_CHECK(b->device == DeviceId::Hip, "HIP backend received non-HIP buffer " + std::to_string(b->id));
+    FG_CHECK(slot >= 0 && slot < FG_READ_SLOTS, "read_async: slot " + std::to_string(slot) + " out of range");
+    if (!b->realized && b->zero_init) realize_storage(*b, true);  // allocated zeros, never materialised
+    FG_CHECK(b->realized, "copy_to_host called on unrealized or non-HIP buffer");
+    check(fg_hip_read_async(ctx(), slot, b->storage, b->nbytes()), "fg_hip_read_async");
+    read_bytes_[slot] = b->nbytes();
+  }
+
+  std::vector<uint8_t> read_wait(int slot) override {
+    FG_CHECK(slot >= 0 && slot < FG_READ_SLOTS, "read_wait: slot " + std::to_string(slot) + " out of range");
+    std::vector<uint8_t> out(read_bytes_[slot]);
+    check(fg_hip_read_wait(ctx(), slot, out.data(), out.size()), "fg_hip_read_wait");
+    return out;
+  }
+
   UOp optimize(const UOp& rangeified) override { return gpu_optimize(rangeified); }
 
   RenderedKernel render(const UOp& optimized, const std::string& name) override {
@@ -262,6 +278,7 @@ class HipDevice : public Device {
 
  private:
   fg_ctx* ctx_ = nullptr;
+  size_t read_bytes_[FG_READ_SLOTS] = {};
 };
 
 }  // namespace

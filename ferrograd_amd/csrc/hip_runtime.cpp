@@ -147,6 +147,12 @@ struct fg_ctx {
   // on MI355X, against 16.5 us into pinned memory (the kernel + sync floor is
   // 12.9 us). Reads are synchronous, so one buffer serves them all.
   char* readback = nullptr;
+  // Asynchronous read-back slots: pinned landing areas, each with the event
+  // recorded behind its copy.
+  char* async_read = nullptr;
+  hipEvent_t async_events[FG_READ_SLOTS] = {};
+  size_t async_bytes[FG_READ_SLOTS] = {};
+  bool async_pending[FG_READ_SLOTS] = {};
   // Launch profiling.
   bool profiling = false;
   std::vector<hipEvent_t> event_pool;
@@ -210,6 +216,9 @@ int fg_hip_init(int ordinal, fg_ctx** out) {
   HIP_TRY(hipHostMalloc(reinterpret_cast<void**>(&c->staging), kStagingBytes, hipHostMallocDefault));
   c->staging_size = kStagingBytes;
   HIP_TRY(hipHostMalloc(reinterpret_cast<void**>(&c->readback), kReadbackBytes, hipHostMallocDefault));
+  HIP_TRY(hipHostMalloc(reinterpret_cast<void**>(&c->async_read), FG_READ_SLOTS * FG_READ_SLOT_BYTES,
+                        hipHostMallocDefault));
+  for (auto& ev : c->async_events) HIP_TRY(hipEventCreateWithFlags(&ev, hipEventDisableTiming));
   *out = c;
   return FG_OK;
 }
@@ -223,6 +232,8 @@ int fg_hip_destroy(fg_ctx* c) {
   (void)hipEventDestroy(c->staging_event);
   (void)hipHostFree(c->staging);
   (void)hipHostFree(c->readback);
+  (void)hipHostFree(c->async_read);
+  for (auto& ev : c->async_events) (void)hipEventDestroy(ev);
   (void)hipStreamDestroy(c->stream);
   delete c;
   return FG_OK;
@@ -329,6 +340,37 @@ int fg_hip_copy_d2h(fg_ctx* c, void* dst, const void* src, size_t n) {
   }
   HIP_TRY(hipMemcpyAsync(dst, src, n, hipMemcpyDeviceToHost, c->stream));
   HIP_TRY(hipStreamSynchronize(c->stream));
+  return FG_OK;
+}
+
+int fg_hip_read_async(fg_ctx* c, int slot, const void* src, size_t n) {
+  if (!c || (!src && n)) return set_err(FG_ERR_INVALID, "fg_hip_read_async: null argument");
+  if (slot < 0 || slot >= FG_READ_SLOTS)
+    return set_err(FG_ERR_INVALID, "fg_hip_read_async: slot " + std::to_string(slot) + " outside 0.." +
+                                       std::to_string(FG_READ_SLOTS - 1));
+  if (n > FG_READ_SLOT_BYTES)
+    return set_err(FG_ERR_INVALID, "fg_hip_read_async: " + std::to_string(n) + " bytes exceed a slot's " +
+                                       std::to_string(FG_READ_SLOT_BYTES));
+  if (c->async_pending[slot]) HIP_TRY(hipEventSynchronize(c->async_events[slot]));  // the slot's last copy landed
+  if (n) HIP_TRY(hipMemcpyAsync(c->async_read + static_cast<size_t>(slot) * FG_READ_SLOT_BYTES, src, n,
+                                hipMemcpyDeviceToHost, c->stream));
+  HIP_TRY(hipEventRecord(c->async_events[slot], c->stream));
+  c->async_bytes[slot] = n;
+  c->async_pending[slot] = true;
+  return FG_OK;
+}
+
+int fg_hip_read_wait(fg_ctx* c, int slot, void* dst, size_t n) {
+  if (!c || (!dst && n)) return set_err(FG_ERR_INVALID, "fg_hip_read_wait: null argument");
+  if (slot < 0 || slot >= FG_READ_SLOTS || !c->async_pending[slot])
+    return set_err(FG_ERR_INVALID, "fg_hip_read_wait: no read queued in slot " + std::to_string(slot));
+  if (n != c->async_bytes[slot])
+    return set_err(FG_ERR_INVALID, "fg_hip_read_wait: slot " + std::to_string(slot) + " holds " +
+                                       std::to_string(c->async_bytes[slot]) + " bytes, " + std::to_string(n) +
+                                       " asked for");
+  HIP_TRY(hipEventSynchronize(c->async_events[slot]));
+  c->async_pending[slot] = false;
+  if (n) std::memcpy(dst, c->async_read + static_cast<size_t>(slot) * FG_READ_SLOT_BYTES, n);
   return FG_OK;
 }
 

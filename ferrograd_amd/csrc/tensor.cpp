@@ -727,7 +727,28 @@ std::shared_ptr<CachedPlan> record_plan(const GraphKey& k, const SchedulePlan& p
   return rec;
 }
 
-void replay_plan(Device& backend, const GraphKey& k, const CachedPlan& plan) {
+// ── step capture ────────────────────────────────────────────────────────────
+// A training loop repeats one step: the same realize_many calls, each a replay
+// of the same plan over the same parameter buffers. While a step runs under a
+// recorder, every replay is noted; a miss (a realisation that had to be
+// scheduled) makes the step unrecordable.
+struct ReplayRecord {
+  std::shared_ptr<CachedPlan> plan;
+  std::vector<Buffer> leaves;          // the key's leaves
+  std::vector<int32_t> start_values;   // the Start arguments, in kernel and argument order
+  std::vector<Buffer> outs;            // each kernel's output (null where it has none)
+};
+
+struct StepRecorder {
+  bool valid = true;
+  std::vector<ReplayRecord> records;
+};
+
+thread_local StepRecorder* g_step_recorder = nullptr;
+
+void replay_plan(Device& backend, const GraphKey& k, const std::shared_ptr<CachedPlan>& planp) {
+  const CachedPlan& plan = *planp;
+  std::vector<int32_t> starts;
   for (uint32_t i : plan.written_leaves) k.leaves[i]->known_zero = false;
   std::vector<Buffer> outs(plan.kernels.size());
   std::vector<Program*> progs(plan.kernels.size());
@@ -757,7 +778,8 @@ void replay_plan(Device& backend, const GraphKey& k, const CachedPlan& plan) {
         continue;
       }
       if (pa.kind == PlanArg::Start) {
-        args.push_back(KernelArg::i32(static_cast<int32_t>(k.order[pa.index].arg().a)));
+        starts.push_back(static_cast<int32_t>(k.order[pa.index].arg().a));
+        args.push_back(KernelArg::i32(starts.back()));
         continue;
       }
       const Buffer& b = pa.kind == PlanArg::Leaf ? k.leaves[pa.index] : outs[pa.index];
@@ -779,6 +801,7 @@ void replay_plan(Device& backend, const GraphKey& k, const CachedPlan& plan) {
   realize_stats().ns_lower += l1 - l0;
   backend.execute_sequence(progs, seq_args, plan.device_state);
   realize_stats().ns_launch += now_ns() - l1;
+  if (g_step_recorder) g_step_recorder->records.push_back({planp, k.leaves, std::move(starts), outs});
   uint64_t t2 = now_ns();
   UOpMap<UOp> repl;
   repl.reserve(plan.replacements.size() * 2);
@@ -793,6 +816,141 @@ void replay_plan(Device& backend, const GraphKey& k, const CachedPlan& plan) {
   }
   apply_map_to_tensors(repl);
   realize_stats().ns_apply_map += now_ns() - t2;
+}
+
+// A step whose realisations can be launched again without rebuilding its
+// graphs: every kernel of every replayed plan, in order, with each buffer
+// argument resolved to a persistent buffer (parameters, inputs, uploaded
+// constants: the same buffer in two consecutive steps) or to an output of an
+// earlier kernel of the same step.
+struct CapturedStep {
+  struct Arg {
+    enum Kind : uint8_t { Persistent, Output, Value } kind = Value;
+    Buffer buf;
+    uint32_t out = 0;
+    KernelArg value;
+  };
+  struct Kernel {
+    Program* prog = nullptr;
+    bool has_output = false;
+    DType out_dtype;
+    size_t out_numel = 0;
+    std::vector<Arg> args;
+  };
+  std::vector<std::shared_ptr<CachedPlan>> plans;  // keep the programs alive
+  std::vector<Kernel> kernels;
+  std::vector<void*> last_storage;
+  std::shared_ptr<void> device_state;  // the device's replay state for the whole step
+  uint32_t result_kernel = 0;          // whose output is the step's result (the loss)
+};
+
+// The capture of step `cur`, given the step before it, or null when the two
+// did not replay the same plans over the same persistent buffers, or when
+// `result` is not one of the step's outputs.
+std::unique_ptr<CapturedStep> capture_step(const std::vector<ReplayRecord>& prev,
+                                           const std::vector<ReplayRecord>& cur, const Buffer& result) {
+  if (cur.empty() || prev.size() != cur.size()) return nullptr;
+  auto cap = std::make_unique<CapturedStep>();
+  std::unordered_map<const BufferInner*, uint32_t> out_cur, out_prev;  // output buffer -> kernel of the step
+  uint32_t base = 0;
+  for (size_t r = 0; r < cur.size(); r++) {
+    const ReplayRecord& c = cur[r];
+    const ReplayRecord& p = prev[r];
+    if (c.plan != p.plan || c.start_values != p.start_values) return nullptr;
+    size_t si = 0;
+    for (const PlanKernel& pk : c.plan->kernels) {
+      CapturedStep::Kernel k;
+      k.prog = pk.program.get();
+      k.has_output = pk.has_output;
+      k.out_dtype = pk.out_dtype;
+      k.out_numel = pk.out_numel;
+      for (const PlanArg& pa : pk.args) {
+        CapturedStep::Arg a;
+        if (pa.kind == PlanArg::Value) {
+          a.value = pa.value;
+        } else if (pa.kind == PlanArg::Start) {
+          a.value = KernelArg::i32(c.start_values.at(si++));
+        } else if (pa.kind == PlanArg::Output) {
+          a.kind = CapturedStep::Arg::Output;
+          a.out = base + pa.index;
+        } else {
+          const Buffer& lc = c.leaves[pa.index];
+          const Buffer& lp = p.leaves[pa.index];
+          auto oc = out_cur.find(lc.get());
+          auto op = out_prev.find(lp.get());
+          if (oc != out_cur.end() && op != out_prev.end() && oc->second == op->second) {
+            a.kind = CapturedStep::Arg::Output;
+            a.out = oc->second;
+          } else if (oc == out_cur.end() && op == out_prev.end() && lc->is_realized() &&
+                     (lc.get() == lp.get() || (lc->known_zero && lp->known_zero && lc->numel == lp->numel &&
+                                               lc->dtype == lp->dtype))) {
+            // The same buffer in both steps, or, like relu's zeros
+            // (tensor.rs:517-531), a fresh buffer that still holds allocate()'s
+            // zeros after either step: nothing writes it, so this one serves.
+            a.kind = CapturedStep::Arg::Persistent;
+            a.buf = lc;
+          } else {
+            return nullptr;
+          }
+        }
+        k.args.push_back(std::move(a));
+      }
+      cap->kernels.push_back(std::move(k));
+    }
+    for (size_t j = 0; j < c.outs.size(); j++) {
+      if (c.outs[j]) out_cur[c.outs[j].get()] = base + static_cast<uint32_t>(j);
+      if (p.outs[j]) out_prev[p.outs[j].get()] = base + static_cast<uint32_t>(j);
+    }
+    base += static_cast<uint32_t>(c.plan->kernels.size());
+    cap->plans.push_back(c.plan);
+  }
+  auto res = out_cur.find(result.get());
+  if (res == out_cur.end()) return nullptr;
+  cap->result_kernel = res->second;
+  cap->last_storage.assign(cap->kernels.size(), nullptr);
+  return cap;
+}
+
+// Launches every kernel of a captured step as one sequence (a single HIP
+// graph from its second run on) and returns the step's result buffer.
+Buffer replay_step(Device& backend, CapturedStep& cap) {
+  const size_t n = cap.kernels.size();
+  std::vector<Buffer> outs(n);
+  std::vector<Program*> progs(n);
+  std::vector<std::vector<KernelArg>> args(n);
+  uint64_t l0 = now_ns();
+  for (size_t j = 0; j < n; j++) {
+    const CapturedStep::Kernel& k = cap.kernels[j];
+    progs[j] = k.prog;
+    if (k.has_output) {
+      Buffer out = backend.reserve_buffer(k.out_dtype, k.out_numel);
+      backend.realize_storage_at(*out, false, cap.last_storage[j]);
+      cap.last_storage[j] = out->storage;
+      out->known_zero = false;
+      outs[j] = out;
+      args[j].push_back(KernelArg::buf(out));
+    }
+    for (const CapturedStep::Arg& a : k.args) {
+      if (a.kind == CapturedStep::Arg::Value) args[j].push_back(a.value);
+      else if (a.kind == CapturedStep::Arg::Persistent) args[j].push_back(KernelArg::buf(a.buf));
+      else args[j].push_back(KernelArg::buf(outs[a.out]));
+    }
+  }
+  uint64_t l1 = now_ns();
+  realize_stats().ns_lower += l1 - l0;
+  backend.execute_sequence(progs, args, cap.device_state);
+  realize_stats().ns_launch += now_ns() - l1;
+  realize_stats().kernels_launched += n;
+  realize_stats().lowering_cache_hits += n;
+  return outs[cap.result_kernel];
+}
+
+bool step_capture_enabled() {
+  static const bool on = [] {
+    const char* e = std::getenv("FG_STEP_CAPTURE");
+    return !(e && std::strcmp(e, "0") == 0);
+  }();
+  return on;
 }
 
 }  // namespace
@@ -840,12 +998,13 @@ void Tensor::realize_many(const std::vector<Tensor>& tensors) {  // tensor.rs:78
     if (auto hit = find_plan(key)) {
       pc.hits++;
       realize_stats().ns_schedule += now_ns() - t0;
-      replay_plan(get_device(roots[0].device()), key, *hit);
+      replay_plan(get_device(roots[0].device()), key, hit);
       return;
     }
     pc.misses++;
     for (auto& b : key.leaves) zero_before.push_back(b->known_zero ? 1 : 0);
   }
+  if (g_step_recorder) g_step_recorder->valid = false;  // a realisation no plan records
   SchedulePlan plan = schedule_many(roots, opt);
   uint64_t t1 = now_ns();
   realize_stats().ns_schedule += t1 - t0;
@@ -1149,27 +1308,69 @@ void Sgd::step() const {  // optim.rs:60-71
   Tensor::realize_many(params);
 }
 
+// examples/mnist.rs:84-101's loop body `steps` times. Every step runs the
+// calls of the reference loop in its order (forward, cross_entropy, zero_grad,
+// backward, step, the loss read back), so the device runs the same kernels in
+// the same order, and the losses, parameters and tensors come out as from
+// that loop. Two things differ in how the host drives it:
+// - The wait for a step's loss moves: its read-back is queued behind the
+//   step, and the host waits for it once the next step is queued, so that
+//   host work overlaps the device's.
+// - Step capture: once two consecutive steps replayed the same recorded plans
+//   over the same parameter and input buffers, the following steps launch
+//   that kernel sequence directly, as one device sequence (one HIP graph),
+//   without rebuilding the lazy graphs; only their losses are read. The last
+//   step always runs in full, so the parameters, their gradients and every
+//   live tensor end as after `steps` ordinary steps.
 std::vector<float> train_steps(const std::vector<const Linear*>& layers, const Sgd& opt, const Tensor& x,
                                const Tensor& targets, int steps) {
   FG_CHECK(!layers.empty(), "train_steps requires at least one layer");
   FG_CHECK(steps >= 0, "train_steps: negative step count");
-  std::vector<float> losses;
-  losses.reserve(static_cast<size_t>(steps));
+  std::vector<float> losses(static_cast<size_t>(steps));
+  Device& dev = get_device(x.device());
+  auto collect = [&](int step) {
+    std::vector<uint8_t> b = dev.read_wait(step % 2);
+    FG_CHECK(b.size() == sizeof(float), "train_steps: the loss must be one f32");
+    std::memcpy(&losses[static_cast<size_t>(step)], b.data(), sizeof(float));
+  };
+  struct RecorderScope {
+    explicit RecorderScope(StepRecorder* r) { g_step_recorder = r; }
+    ~RecorderScope() { g_step_recorder = nullptr; }
+  };
+  const bool capture = step_capture_enabled() && plan_cache().enabled;
+  std::unique_ptr<CapturedStep> cap;
+  std::vector<ReplayRecord> prev;
+  bool prev_valid = false;
   for (int i = 0; i < steps; i++) {
-    Tensor h = x;
-    for (size_t l = 0; l < layers.size(); l++) {
-      h = layers[l]->forward(h);
-      if (l + 1 < layers.size()) h = h.relu();
+    if (cap && i + 1 < steps) {
+      dev.read_async(replay_step(dev, *cap), i % 2);
+      realize_stats().steps_replayed++;
+      if (i > 0) collect(i - 1);
+      continue;
     }
-    Tensor loss = h.cross_entropy(targets);
-    opt.zero_grad();
-    loss.backward();
-    opt.step();
-    std::vector<uint8_t> b = loss.to_bytes();
-    float v;
-    std::memcpy(&v, b.data(), sizeof(float));
-    losses.push_back(v);
+    StepRecorder rec;
+    {
+      RecorderScope scope(capture && !cap ? &rec : nullptr);
+      Tensor h = x;
+      for (size_t l = 0; l < layers.size(); l++) {
+        h = layers[l]->forward(h);
+        if (l + 1 < layers.size()) h = h.relu();
+      }
+      Tensor loss = h.cross_entropy(targets);
+      opt.zero_grad();
+      loss.backward();
+      opt.step();
+      Buffer lb = loss.realized_buffer();
+      dev.read_async(lb, i % 2);  // the loss's read-back, queued behind the step
+      if (capture && !cap) {
+        if (rec.valid && prev_valid && (cap = capture_step(prev, rec.records, lb))) realize_stats().steps_captured++;
+        prev = cap ? std::vector<ReplayRecord>() : std::move(rec.records);
+        prev_valid = !cap && rec.valid;
+      }
+    }
+    if (i > 0) collect(i - 1);
   }
+  if (steps > 0) collect(steps - 1);
   return losses;
 }
 

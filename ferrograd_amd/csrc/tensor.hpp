@@ -161,6 +161,9 @@ struct RealizeStats {
   // Replayed plans that ran as one HIP graph launch, and the launches inside
   // them whose arguments had to be updated first.
   size_t graph_replays = 0, graph_updates = 0;
+  // Native training loops: steps captured, and steps launched from a capture
+  // without rebuilding their graphs.
+  size_t steps_captured = 0, steps_replayed = 0;
 };
 RealizeStats& realize_stats();
 int debug_level();

@@ -99,7 +99,13 @@ int fg_linear_free(fg_linear* l);
  * code: logits = layers[0..n) with ReLU between them (mnist.rs:30-54 for any
  * depth), loss = cross_entropy(logits, targets), opt's zero_grad, backward,
  * step, then the loss read back into losses[i]. Replaces the Rust caller's
- * loop; it calls the same Tensor/Linear/Sgd code as the entry points above. */
+ * loop; it calls the same Tensor/Linear/Sgd code as the entry points above,
+ * and runs the same kernels in the same order. Each step's loss is read once
+ * the next step is queued, and once two consecutive steps have replayed the
+ * same recorded plans over the same buffers, further steps (all but the last)
+ * launch that kernel sequence as one device sequence without rebuilding the
+ * lazy graphs. Losses, parameters and gradients come out as from the loop
+ * driven call by call. */
 int fg_mlp_train_steps(fg_linear* const* layers, int nlayers, fg_sgd* opt, fg_tensor* x, fg_tensor* targets, int steps,
                        float* losses);
 
@@ -119,6 +125,11 @@ int fg_stats(uint64_t* kernels_launched, uint64_t* programs_compiled, uint64_t* 
  * launches in them whose arguments had to be updated (no counterpart in the
  * reference, which has no graphs). */
 int fg_graph_stats(uint64_t* replays, uint64_t* updated_launches);
+/* fg_mlp_train_steps' step capture: how many times a step was captured, and
+ * how many steps were then launched from a capture without rebuilding their
+ * lazy graphs (FG_STEP_CAPTURE=0 turns capture off). No reference
+ * counterpart. */
+int fg_step_capture_stats(uint64_t* captured, uint64_t* replayed);
 /* Cumulative host nanoseconds in: schedule, lowering-cache/compile, launch,
  * live-tensor rewrite after realisation, backward graph construction. */
 int fg_host_times(uint64_t out[5]);

@@ -80,6 +80,20 @@ int fg_hip_copy_h2d(fg_ctx* ctx, void* dst, const void* src, size_t nbytes);
 int fg_hip_copy_d2h(fg_ctx* ctx, void* dst, const void* src, size_t nbytes);
 int fg_hip_copy_d2d(fg_ctx* ctx, void* dst, const void* src, size_t nbytes);
 
+/* Asynchronous read-back of a small result. No counterpart in the reference,
+ * whose copy_to_host returns with the data (device.rs:302): a training loop
+ * that reads one loss per step can queue the next step before it waits for
+ * this one's. fg_hip_read_async queues a copy of `nbytes` (at most
+ * FG_READ_SLOT_BYTES) from device memory into pinned slot `slot` (0 ..
+ * FG_READ_SLOTS-1) behind the work already on the stream, and returns.
+ * fg_hip_read_wait waits for that copy only, not for work queued after it,
+ * and copies the bytes to `dst`; `nbytes` must match. Reusing a slot first
+ * waits for its previous copy. */
+#define FG_READ_SLOTS 8
+#define FG_READ_SLOT_BYTES ((size_t)65536)
+int fg_hip_read_async(fg_ctx* ctx, int slot, const void* src, size_t nbytes);
+int fg_hip_read_wait(fg_ctx* ctx, int slot, void* dst, size_t nbytes);
+
 /* Compile HIP source for gfx950 with hiprtc and load kernel `func`. The code
  * object is cached on disk keyed by a hash of source, options and target. */
 int fg_hip_compile(fg_ctx* ctx, const char* source, const char* func, int num_args, fg_prog** out);

@@ -514,6 +514,10 @@ class CpuDevice : public Device {
   // every kernel keeps the reference's lowering and accumulation order.
   bool fuse = false;
   bool fuse_elementwise() const override { return fuse; }
+  // Test-only: skip kernel execution, so a host-side profile of the front end
+  // (graph building, scheduling, plan replay) is not buried under the
+  // kernels' CPU time. Results are then meaningless.
+  bool dry_run = false;
 
   Buffer allocate(DType dtype, size_t numel) override {  // cpu.rs:277-280
     Buffer b = reserve_buffer(dtype, numel);
@@ -599,7 +603,7 @@ class CpuDevice : public Device {
         case KernelArg::Kind::Bool: bools[i] = args[i].b ? 1 : 0; ptrs[i] = &bools[i]; break;
       }
     }
-    p.entry(ptrs.data());
+    if (!dry_run) p.entry(ptrs.data());
   }
 };
 
@@ -617,6 +621,15 @@ int fg_oracle_register(void) {
     fg::register_device(fg::DeviceId::Cpu, g_cpu_device);
   }
   return 0;
+}
+
+// Skip (1) or run (0) kernels on the CPU device: for host-side profiling of
+// the front end only. Returns the previous setting.
+int fg_oracle_set_dry_run(int on) {
+  fg_oracle_register();
+  int prev = g_cpu_device->dry_run ? 1 : 0;
+  g_cpu_device->dry_run = on != 0;
+  return prev;
 }
 
 // Schedule the CPU device's realisations with (1) or without (0) the HIP

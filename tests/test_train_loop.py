@@ -6,7 +6,9 @@ import numpy as np
 import pytest
 
 
-def run(fg, dev, dims, batch, steps, native):
+def run(fg, dev, dims, batch, steps, native, chunks=None):
+    """Params, losses and the last step's gradients after `steps` steps; the
+    native loop is called once, or once per entry of `chunks`."""
     from ferrograd_amd.mlp import Mlp, synthetic_batch, train_step, train_steps_native
 
     fg.reset_init_seed(42)
@@ -16,19 +18,49 @@ def run(fg, dev, dims, batch, steps, native):
     x = fg.Tensor.new(xs, list(xs.shape), dev)
     t = fg.Tensor.new(ts, list(ts.shape), dev)
     if native:
-        losses = train_steps_native(model, opt, x, t, steps)
+        losses = [l for n in (chunks or [steps]) for l in train_steps_native(model, opt, x, t, n)]
     else:
         losses = [train_step(model, opt, x, t).to_vec()[0] for _ in range(steps)]
-    return losses, [p.numpy() for p in model.parameters()]
+    params = model.parameters()
+    return losses, [p.numpy() for p in params] + [p.grad().numpy() for p in params]
 
 
 @pytest.mark.parametrize("dims", [(16, 8, 4), (12, 16, 8, 5)])
 def test_native_loop_matches_python_loop_cpu(fg, cpu, dims):
-    l_py, p_py = run(fg, cpu, dims, 8, 3, native=False)
-    l_nat, p_nat = run(fg, cpu, dims, 8, 3, native=True)
+    # 9 steps: once two consecutive steps replayed the same plans (from the
+    # third step on) the native loop launches the following steps from the
+    # capture; the last one runs in full. Losses,
+    # parameters and the last step's gradients equal the Python loop's bit for
+    # bit, also when the loop is entered several times.
+    before = fg.stats()
+    l_py, p_py = run(fg, cpu, dims, 8, 9, native=False)
+    l_nat, p_nat = run(fg, cpu, dims, 8, 9, native=True)
+    after = fg.stats()
+    assert after["steps_replayed"] - before["steps_replayed"] >= 4
     assert l_nat == l_py and l_nat[-1] < l_nat[0]
     for a, b in zip(p_nat, p_py):
         assert np.array_equal(a, b)
+    l_ch, p_ch = run(fg, cpu, dims, 8, 9, native=True, chunks=[4, 1, 4])
+    assert l_ch == l_py and all(np.array_equal(a, b) for a, b in zip(p_ch, p_py))
+
+
+def test_step_capture_off_matches(fg, cpu):
+    # FG_STEP_CAPTURE=0 in a fresh process: every step runs in full, same bits.
+    import json
+    import os
+    import subprocess
+    import sys
+
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    code = ("import sys, json; sys.path.insert(0, %r); sys.path.insert(0, %r); import ferrograd_amd as fg, oracle; "
+            "oracle.load(); from test_train_loop import run; l, p = run(fg, 'cpu', (16, 8, 4), 8, 7, True); "
+            "print(json.dumps([l, [a.tolist() for a in p], fg.stats()['steps_replayed']]))") % (root, os.path.join(root, "tests"))
+    out = subprocess.run([sys.executable, "-c", code], env=dict(os.environ, FG_STEP_CAPTURE="0"), capture_output=True,
+                         text=True, check=True).stdout
+    l_off, p_off, replayed = json.loads(out.strip().splitlines()[-1])
+    l_on, p_on = run(fg, cpu, (16, 8, 4), 8, 7, native=True)
+    assert replayed == 0 and l_off == l_on
+    assert all(np.array_equal(np.array(a, np.float32).reshape(b.shape), b) for a, b in zip(p_off, p_on))
 
 
 def test_native_loop_errors_cross_the_abi(fg, cpu):
@@ -48,8 +80,10 @@ def test_native_loop_errors_cross_the_abi(fg, cpu):
 @pytest.mark.gpu
 @pytest.mark.parametrize("batch,dims", [(256, (784, 128, 10)), (64, (96, 64, 32, 10))])
 def test_native_loop_matches_python_loop_hip(fg, cpu, batch, dims):
-    l_py, p_py = run(fg, "hip", dims, batch, 3, native=False)
-    l_nat, p_nat = run(fg, "hip", dims, batch, 3, native=True)
+    l_py, p_py = run(fg, "hip", dims, batch, 9, native=False)
+    before = fg.stats()
+    l_nat, p_nat = run(fg, "hip", dims, batch, 9, native=True)
+    assert fg.stats()["steps_replayed"] - before["steps_replayed"] >= 4
     assert l_nat == l_py
     for a, b in zip(p_nat, p_py):
         assert np.array_equal(a, b)
@@ -60,7 +94,7 @@ def test_native_loop_matches_python_loop_hip(fg, cpu, batch, dims):
     from ferrograd_amd.mlp import synthetic_batch
 
     xs, ts = synthetic_batch(batch, dims[0], dims[-1], 7, 8)
-    l_rec = check_recorded_steps(recorded_steps(fg, "hip", xs, ts, dims, steps=3))
+    l_rec = check_recorded_steps(recorded_steps(fg, "hip", xs, ts, dims, steps=9))
     assert np.allclose(l_rec, l_nat, rtol=1e-6)
-    l_cpu, _ = run(fg, cpu, dims, batch, 3, native=True)
+    l_cpu, _ = run(fg, cpu, dims, batch, 9, native=True)
     assert np.allclose(l_nat, l_cpu, rtol=1e-4, atol=1e-6)
