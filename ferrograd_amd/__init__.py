@@ -70,6 +70,7 @@ def _declare(l: ctypes.CDLL) -> None:
         "fg_tensor_replace": (c_int, [P, P]),
         "fg_tensor_realize_many": (c_int, [PP, c_int]),
         "fg_tensor_read": (c_int, [P, P, c_size]),
+        "fg_tensor_write": (c_int, [P, P, c_size]),
         "fg_tensor_shape": (c_int, [P, i64p, ctypes.POINTER(c_int)]),
         "fg_tensor_info": (c_int, [P] + [ctypes.POINTER(c_int)] * 4),
         "fg_tensor_set_requires_grad": (c_int, [P, c_int]),
@@ -339,6 +340,15 @@ class Tensor:
         if code == BOOL:
             out = out.astype(np.bool_)
         return out.reshape(shape)
+
+    def write(self, data) -> "Tensor":
+        """Device::copy_from_host into this realised tensor's buffer; the
+        byte count must match (device.rs:294, cpu.rs:282-302)."""
+        arr = np.ascontiguousarray(data)
+        if self.dtype == BOOL:
+            arr = arr.astype(np.uint8)
+        _check(lib().fg_tensor_write(self._h, arr.ctypes.data_as(ctypes.c_void_p), arr.nbytes))
+        return self
 
     def raw_bytes(self) -> bytes:
         """The realised buffer's bytes (bool as 0/1 bytes)."""

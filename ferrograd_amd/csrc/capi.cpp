@@ -227,6 +227,14 @@ int fg_tensor_read(fg_tensor* t, void* dst, size_t nbytes) {
   });
 }
 
+int fg_tensor_write(fg_tensor* t, const void* src, size_t nbytes) {
+  return guard([&] {
+    FG_CHECK(src || nbytes == 0, "fg_tensor_write: null source");
+    fg::Buffer b = t->t.realized_buffer();
+    fg::get_device(b->device).copy_from_host(b, src, nbytes);
+  });
+}
+
 int fg_tensor_shape(fg_tensor* t, int64_t* shape, int* ndim) {
   return guard([&] {
     auto s = t->t.shape();

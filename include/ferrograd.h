@@ -69,6 +69,11 @@ int fg_tensor_replace(fg_tensor* t, fg_tensor* value);
  * tensor's byte size. */
 int fg_tensor_realize_many(fg_tensor** ts, int n);
 int fg_tensor_read(fg_tensor* t, void* dst, size_t nbytes);
+/* Device::copy_from_host (device.rs:294, cpu.rs:282-302) into the realised
+ * tensor's buffer (realised first): `nbytes` must equal the buffer's size, or
+ * the call fails with the reference's "copy_from_host: expected N bytes, got
+ * M". Every alias of the tensor sees the new contents. */
+int fg_tensor_write(fg_tensor* t, const void* src, size_t nbytes);
 
 /* Metadata. `ndim` is in/out: capacity of `shape` in, rank out. */
 int fg_tensor_shape(fg_tensor* t, int64_t* shape, int* ndim);

@@ -235,3 +235,17 @@ def test_alloc_hint_returns_the_hinted_free_block(ctx):
     c = ctx.alloc_hint(1 << 21, a)  # another size: the hint does not apply
     assert c not in (a, b)
     ctx.free(c)
+
+
+@pytest.mark.gpu
+def test_hip_device_copy_from_host_size_error(fg, hip):  # device.rs:457-466, cpu.rs:294-300
+    # The HIP device's own size check (the reference's message), reached
+    # through Device::copy_from_host on a realised tensor's buffer.
+    t = fg.Tensor.new(np.ones(2, np.float32), [2], hip)
+    with pytest.raises(fg.FerrogradError, match="copy_from_host: expected 8 bytes, got 4"):
+        t.write(np.ones(1, np.float32))
+    t.write(np.array([3.0, 4.0], np.float32))
+    assert t.to_vec() == [3.0, 4.0]
+    z = fg.Tensor.zeros([3], hip)  # lazily zero-filled storage is materialised first
+    z.write(np.array([1.0, 2.0, 3.0], np.float32))
+    assert z.to_vec() == [1.0, 2.0, 3.0]

@@ -245,6 +245,14 @@ def test_opt_env_disables_passes(cpu, fg, monkeypatch):  # optimize/mod.rs:85-11
     assert "idx0 < 8" in src and "ridx1 < 16" in src
 
 
-def test_copy_from_host_size_error(fg, cpu):  # device.rs:457-466
+def test_tensor_new_shape_mismatch(fg, cpu):  # tensor.rs:260-276
     with pytest.raises(fg.FerrogradError, match="doesn't match shape"):
         fg.Tensor.new(np.ones(3, np.float32), [2, 2], cpu)
+
+
+def test_copy_from_host_size_error(fg, cpu):  # device.rs:457-466, cpu.rs:294-300
+    t = fg.Tensor.new(np.ones(2, np.float32), [2], cpu)
+    with pytest.raises(fg.FerrogradError, match="copy_from_host: expected 8 bytes, got 4"):
+        t.write(np.ones(1, np.float32))
+    t.write(np.array([3.0, 4.0], np.float32))
+    assert t.to_vec() == [3.0, 4.0]
