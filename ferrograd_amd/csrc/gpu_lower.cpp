@@ -23,6 +23,7 @@
 #include <charconv>
 #include <cmath>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <functional>
 #include <map>
@@ -98,6 +99,7 @@ const char* kernel_class_name(KernelClass k) {
     case KernelClass::RowReduce: return "row_reduce";
     case KernelClass::ColumnReduce: return "column_reduce";
     case KernelClass::Serial: return "serial";
+    case KernelClass::NarrowGemm: return "gemm_narrow_f32";
   }
   return "?";
 }
@@ -1142,6 +1144,39 @@ int64_t gemm_tile_residency(const GemmTile& t) {
 //   operands. 64x64 tiles put many workgroups' loads and stores in flight:
 //   8192x4096 with K 10 took 91 us with 256x256 tiles, 54 with 128x128, 50 with
 //   64x64.
+// FG_GEMM_TILE="BM,BN,BK,WGM,WGN,S" fixes the tile and split count of every
+// GEMM in the process: a tuning override for measuring alternatives to the
+// choice below on one box. Read once; a malformed value fails.
+bool gemm_tile_override(GemmTile* t) {
+  static const std::vector<int64_t> v = [] {
+    std::vector<int64_t> out;
+    const char* e = std::getenv("FG_GEMM_TILE");
+    if (!e || !*e) return out;
+    std::string s(e);
+    size_t p = 0;
+    while (p <= s.size()) {
+      size_t q = s.find(',', p);
+      std::string f = s.substr(p, q == std::string::npos ? std::string::npos : q - p);
+      char* end = nullptr;
+      long long x = std::strtoll(f.c_str(), &end, 10);
+      FG_CHECK(!f.empty() && *end == '\0' && x > 0, "FG_GEMM_TILE must be BM,BN,BK,WGM,WGN,S; got '" + s + "'");
+      out.push_back(x);
+      if (q == std::string::npos) break;
+      p = q + 1;
+    }
+    FG_CHECK(out.size() == 6, "FG_GEMM_TILE must be BM,BN,BK,WGM,WGN,S; got '" + s + "'");
+    return out;
+  }();
+  if (v.empty()) return false;
+  t->BM = static_cast<int>(v[0]);
+  t->BN = static_cast<int>(v[1]);
+  t->BK = static_cast<int>(v[2]);
+  t->WGM = static_cast<int>(v[3]);
+  t->WGN = static_cast<int>(v[4]);
+  t->S = v[5];
+  return true;
+}
+
 GemmTile choose_gemm_tile(int64_t M, int64_t N, int64_t K) {
   auto tiles = [&](const GemmTile& t) { return ((M + t.BM - 1) / t.BM) * ((N + t.BN - 1) / t.BN); };
   const int64_t smax = std::max<int64_t>(1, K / kMinSplitK);
@@ -1150,6 +1185,8 @@ GemmTile choose_gemm_tile(int64_t M, int64_t N, int64_t K) {
     t.S = (K + t.KC - 1) / t.KC;
     return t;
   };
+  GemmTile forced;
+  if (gemm_tile_override(&forced)) return with_splits(forced, forced.S);
   if (M <= 32 || N <= 32) {
     GemmTile t;
     auto side = [](int64_t ext, int* b, int* w) {
@@ -1659,6 +1696,289 @@ RenderedKernel render_gemm(const KernelInfo& ki, const GemmMatch& g, const std::
   return rk;
 }
 
+// ── Narrow GEMM (VALU, HBM-bound) ───────────────────────────────────────────
+// A product with one output side of at most kNarrow elements (the 10 classes
+// of an MLP's last layer) streams its wide operand once and does only
+// kNarrow FMAs per wide element: an HBM-bound kernel, for which a 32-wide
+// MFMA tile is mostly padding. Two layouts, by which way the wide operand is
+// contiguous:
+// - rows: the wide operand is contiguous along k (out[w, n] = sum_k
+//   W[w, k] N[n, k], the forward x·Wᵀ). Each wave owns RW wide rows; its
+//   lanes stride k by four floats, so every load is a coalesced 16-byte load
+//   that streams the row once. The narrow operand's float4 at (n, k) serves
+//   all RW rows. Each accumulator is then summed across the wave by a fixed
+//   DPP/swizzle tree, and the totals go through LDS to the lanes that run the
+//   epilogue.
+// - cols: the wide operand is contiguous along the wide output (out[n, w] =
+//   sum_k N[k, n] W[k, w], the weight gradient dZᵀ·H). Lanes own V
+//   consecutive wide outputs and loop over k, where the narrow values are the
+//   same for every lane. The k range is split over workgroups into scratch
+//   partials that a finishing pass sums in split order before the epilogue.
+// Both fold in a fixed order, so results are deterministic. The products are
+// accumulated with fused multiply-adds (one rounding per term, as the MFMA
+// GEMM's are): these kernels are bound by HBM, and unfused they spent as long
+// on separate multiplies and adds as on their loads.
+constexpr int64_t kNarrow = 16;
+
+struct NarrowPlan {
+  bool rows = false;       // the rows layout (else cols)
+  UOp rw, rn;              // wide and narrow output ranges
+  GemmOperand wide, nar;   // their operands
+  int64_t W = 0, NN = 0, K = 0;
+};
+
+bool narrow_plan(const GemmMatch& g, NarrowPlan* np) {
+  const bool a_narrow = g.M <= kNarrow, b_narrow = g.N <= kNarrow;
+  if (a_narrow == b_narrow) return false;
+  np->rw = a_narrow ? g.rn : g.rm;
+  np->rn = a_narrow ? g.rm : g.rn;
+  np->wide = a_narrow ? g.b : g.a;
+  np->nar = a_narrow ? g.a : g.b;
+  np->W = a_narrow ? g.N : g.M;
+  np->NN = a_narrow ? g.M : g.N;
+  np->K = g.K;
+  const int64_t sk = np->wide.lead.coef(g.rk), sw = np->wide.lead.coef(np->rw);
+  if (sk == 1 && np->K % 4 == 0) np->rows = true;
+  else if (sw == 1) np->rows = false;
+  else return false;
+  return np->W >= 256 && np->K >= 64;
+}
+
+RenderedKernel render_narrow_rows(const KernelInfo& ki, const GemmMatch& g, const NarrowPlan& np,
+                                  const std::string& name) {
+  // A workgroup owns RB wide rows. Thread t owns k positions 4t + 1024j
+  // (j < JT); for a group of JG blocks it first issues the 16-byte loads of all
+  // RB rows, then folds them with the narrow operand's float4 at each (n, k),
+  // so a workgroup's whole share of the wide operand is in flight at once.
+  const int NN = static_cast<int>(np.NN);
+  const int RB = static_cast<int>(std::max<int64_t>(1, std::min<int64_t>(4, 48 / np.NN)));
+  const int64_t W = np.W, K = np.K, JT = (K + 1023) / 1024;
+  const int JG = static_cast<int>(std::min<int64_t>(JT, 4));
+  Emitter em;
+  em.set_nontemporal_loads(true);
+  em.set_streaming_ranges({np.rw});
+  em.line("const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;");
+  em.line("const long row0 = (long)blockIdx.x * " + std::to_string(RB) + ";");
+  for (int r = 0; r < RB; r++) {
+    em.line("const int wr" + std::to_string(r) + " = (int)(row0 + " + std::to_string(r) + " < " + std::to_string(W) +
+            "L ? row0 + " + std::to_string(r) + " : " + std::to_string(W - 1) + ");");
+    for (int n = 0; n < NN; n++) em.line("float acc" + std::to_string(r) + "_" + std::to_string(n) + " = 0.0f;");
+  }
+  em.open_scope("for (int jg = 0; jg < " + std::to_string(JT) + "; jg += " + std::to_string(JG) + ") {", "}");
+  // The wide operand's values for the group (rows past the end read the
+  // last row; k past the end contributes nothing).
+  for (int j = 0; j < JG; j++) {
+    const std::string kj = "k" + std::to_string(j);
+    em.line("const int " + kj + " = (jg + " + std::to_string(j) + ") * 1024 + tid * 4;");
+    for (int r = 0; r < RB; r++) em.line("float a" + std::to_string(r) + "_" + std::to_string(j) + "[4] = {0.0f, 0.0f, 0.0f, 0.0f};");
+    em.open_scope("if (" + kj + " < " + std::to_string(K) + ") {", "}");
+    em.define_range(g.rk, kj);
+    em.set_lane_range(g.rk, 4);
+    for (int r = 0; r < RB; r++) {
+      em.open_scope("{", "}");
+      em.define_range(np.rw, "wr" + std::to_string(r));
+      for (int u = 0; u < 4; u++)
+        em.line("a" + std::to_string(r) + "_" + std::to_string(j) + "[" + std::to_string(u) + "] = " +
+                em.val(np.wide.expr, u) + ";");
+      em.close_scope();
+    }
+    em.clear_lane_range();
+    em.close_scope();
+  }
+  for (int j = 0; j < JG; j++) {
+    const std::string kj = "k" + std::to_string(j);
+    em.open_scope("if (" + kj + " < " + std::to_string(K) + ") {", "}");
+    em.define_range(g.rk, kj);
+    em.set_lane_range(g.rk, 4);
+    for (int n = 0; n < NN; n++) {
+      em.open_scope("{", "}");
+      em.define_range(np.rn, std::to_string(n));
+      std::vector<std::string> b;
+      for (int u = 0; u < 4; u++) b.push_back(em.val(np.nar.expr, u));
+      for (int r = 0; r < RB; r++) {
+        const std::string acc = "acc" + std::to_string(r) + "_" + std::to_string(n);
+        const std::string a = "a" + std::to_string(r) + "_" + std::to_string(j);
+        em.line(acc + " = __builtin_fmaf(" + a + "[3], " + b[3] + ", __builtin_fmaf(" + a + "[2], " + b[2] +
+                ", __builtin_fmaf(" + a + "[1], " + b[1] + ", __builtin_fmaf(" + a + "[0], " + b[0] + ", " + acc + "))));");
+      }
+      em.close_scope();
+    }
+    em.clear_lane_range();
+    em.close_scope();
+  }
+  em.close_scope();
+  // Sums over the workgroup: a fixed DPP/swizzle tree in each wave, then the
+  // four waves in order through LDS.
+  const int outs = RB * NN;
+  em.line("__shared__ float fg_nt[4][" + std::to_string(outs) + "];");
+  for (int r = 0; r < RB; r++)
+    for (int n = 0; n < NN; n++) {
+      const std::string acc = "acc" + std::to_string(r) + "_" + std::to_string(n);
+      std::istringstream is(wave_reduce(acc, 64, Op::Add, DType::F32()));
+      std::string l;
+      while (std::getline(is, l)) em.line(l);
+      em.line("if (lane == 0) fg_nt[wave][" + std::to_string(r * NN + n) + "] = " + acc + ";");
+    }
+  em.line("__syncthreads();");
+  em.open_scope("if (tid < " + std::to_string(outs) + ") {", "}");
+  em.line("const long orow = row0 + tid / " + std::to_string(NN) + ";");
+  em.open_scope("if (orow < " + std::to_string(W) + "L) {", "}");
+  em.line("const int ow = (int)orow, on = tid % " + std::to_string(NN) + ";");
+  em.line("const float tot = ((fg_nt[0][tid] + fg_nt[1][tid]) + fg_nt[2][tid]) + fg_nt[3][tid];");
+  em.define_range(np.rw, "ow");
+  em.define_range(np.rn, "on");
+  em.reduce_cb_ = [&](const UOp& RR, int) -> std::string {
+    FG_CHECK(RR == g.R, "narrow gemm epilogue sees one reduction");
+    return "tot";
+  };
+  std::string v = em.val(ki.value, 0);
+  em.line(pname(ki.out_param) + "[" + em.idx(ki.out_index, 0) + "] = " + v + ";");
+  em.close_scope();
+  em.close_scope();
+  RenderedKernel rk;
+  rk.name = name;
+  rk.kind = kernel_class_name(KernelClass::NarrowGemm);
+  rk.source = std::string(kPrelude) + signature(ki, name, 256) + " {\n" + em.code() + "}\n";
+  rk.block[0] = 256;
+  rk.grid[0] = static_cast<unsigned>((W + RB - 1) / RB);
+  return rk;
+}
+
+RenderedKernel render_narrow_cols(const KernelInfo& ki, const GemmMatch& g, const NarrowPlan& np,
+                                  const std::string& name) {
+  const int NN = static_cast<int>(np.NN);
+  const int64_t W = np.W, K = np.K;
+  // V wide outputs per lane (16-byte loads when the wide extent allows).
+  const int V = W % 4 == 0 ? 4 : 1;
+  const int64_t cols_per_wg = 64 * V, cblocks = (W + cols_per_wg - 1) / cols_per_wg;
+  // k splits: about 1024 workgroups, each wave running at least 16 k. The
+  // partials (S x NN x W floats) stay under a tenth of the wide operand.
+  int64_t S = std::max<int64_t>(1, std::min<int64_t>((1024 + cblocks - 1) / cblocks, K / 64));
+  const int64_t KC = ((K + S - 1) / S + 3) / 4 * 4;  // per workgroup, a multiple of the 4 waves
+  S = (K + KC - 1) / KC;
+  const int64_t KW = KC / 4;                         // per wave
+  const bool split = S > 1;
+  const std::string sig_extra = split ? ", float* __restrict__ fg_scratch" : "";
+  auto sig = [&](const std::string& fn) {
+    std::string s = signature(ki, fn, 256);
+    return s.substr(0, s.size() - 1) + sig_extra + ")";
+  };
+  // Output (n, w)'s epilogue with its sum in `sum`.
+  auto epilogue = [&](Emitter& em, const std::string& n, const std::string& w, const std::string& sum) {
+    em.define_range(np.rn, n);
+    em.define_range(np.rw, w);
+    em.reduce_cb_ = [&g, sum](const UOp& RR, int) -> std::string {
+      FG_CHECK(RR == g.R, "narrow gemm epilogue sees one reduction");
+      return sum;
+    };
+    std::string v = em.val(ki.value, 0);
+    em.line(pname(ki.out_param) + "[" + em.idx(ki.out_index, 0) + "] = " + v + ";");
+  };
+
+  Emitter em;
+  em.set_nontemporal_loads(true);
+  em.set_streaming_ranges({np.rw});
+  // The wave index as a wave-uniform value: k is then uniform across lanes, so
+  // the narrow operand's loads are scalar loads.
+  em.line("const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);");
+  em.line("const long cb = blockIdx.x % " + std::to_string(cblocks) + ";");
+  em.line("const int ks = (int)(blockIdx.x / " + std::to_string(cblocks) + ");");
+  em.line("const long wl = cb * " + std::to_string(cols_per_wg) + " + lane * " + std::to_string(V) + ";");
+  em.line("const bool active = wl < " + std::to_string(W) + "L;");
+  em.line("const int w0 = active ? (int)wl : 0;");
+  em.line("const int kw0 = ks * " + std::to_string(KC) + " + wave * " + std::to_string(KW) + ";");
+  em.line("const int kw1 = kw0 + " + std::to_string(KW) + " < " + std::to_string(K) + " ? kw0 + " + std::to_string(KW) +
+          " : " + std::to_string(K) + ";");
+  for (int n = 0; n < NN; n++)
+    for (int u = 0; u < V; u++) em.line("float acc" + std::to_string(n) + "_" + std::to_string(u) + " = 0.0f;");
+  em.define_range(np.rw, "w0");
+  // Batches of KB rows: the batch's wide loads are issued before its FMAs.
+  constexpr int KB = 8;
+  em.open_scope("for (int kb = kw0; kb < kw1; kb += " + std::to_string(KB) + ") {", "}");
+  for (int q = 0; q < KB; q++) {
+    const std::string kq = "kq" + std::to_string(q);
+    em.line("const int " + kq + " = kb + " + std::to_string(q) + " < kw1 ? kb + " + std::to_string(q) + " : kw1 - 1;");
+    em.line("float wv" + std::to_string(q) + "[" + std::to_string(V) + "];");
+    em.open_scope("{", "}");
+    em.define_range(g.rk, kq);
+    if (V > 1) em.set_lane_range(np.rw, V);
+    for (int u = 0; u < V; u++)
+      em.line("wv" + std::to_string(q) + "[" + std::to_string(u) + "] = " + em.val(np.wide.expr, u) + ";");
+    em.clear_lane_range();
+    em.close_scope();
+  }
+  for (int q = 0; q < KB; q++) {
+    const std::string kq = "kq" + std::to_string(q);
+    em.open_scope("if (kb + " + std::to_string(q) + " < kw1) {", "}");
+    em.define_range(g.rk, kq);
+    for (int n = 0; n < NN; n++) {
+      em.open_scope("{", "}");
+      em.define_range(np.rn, std::to_string(n));
+      const std::string b = em.val(np.nar.expr, 0);
+      for (int u = 0; u < V; u++) {
+        const std::string acc = "acc" + std::to_string(n) + "_" + std::to_string(u);
+        em.line(acc + " = __builtin_fmaf(" + b + ", wv" + std::to_string(q) + "[" + std::to_string(u) + "], " + acc + ");");
+      }
+      em.close_scope();
+    }
+    em.close_scope();
+  }
+  em.close_scope();
+  // The four waves' sums, in wave order, through LDS.
+  const int per_wg = NN * static_cast<int>(cols_per_wg);
+  em.line("__shared__ float fg_nc[4][" + std::to_string(per_wg) + "];");
+  for (int n = 0; n < NN; n++)
+    for (int u = 0; u < V; u++)
+      em.line("fg_nc[wave][" + std::to_string(n) + " * " + std::to_string(cols_per_wg) + " + lane * " + std::to_string(V) +
+              " + " + std::to_string(u) + "] = acc" + std::to_string(n) + "_" + std::to_string(u) + ";");
+  em.line("__syncthreads();");
+  em.open_scope("for (int o = threadIdx.x; o < " + std::to_string(per_wg) + "; o += 256) {", "}");
+  em.line("const int on = o / " + std::to_string(cols_per_wg) + ";");
+  em.line("const long owl = cb * " + std::to_string(cols_per_wg) + " + o % " + std::to_string(cols_per_wg) + ";");
+  em.open_scope("if (owl < " + std::to_string(W) + "L) {", "}");
+  em.line("const int ow = (int)owl;");
+  em.line("const float tot = ((fg_nc[0][o] + fg_nc[1][o]) + fg_nc[2][o]) + fg_nc[3][o];");
+  if (split) {
+    em.line("fg_scratch[((long)ks * " + std::to_string(NN) + " + on) * " + std::to_string(W) + "L + ow] = tot;");
+  } else {
+    epilogue(em, "on", "ow", "tot");
+  }
+  em.close_scope();
+  em.close_scope();
+
+  RenderedKernel rk;
+  rk.name = name;
+  rk.kind = kernel_class_name(KernelClass::NarrowGemm);
+  const std::string main_name = split ? name + "_part" : name;
+  rk.source = std::string(kPrelude) + sig(main_name) + " {\n" + em.code() + "}\n";
+  rk.block[0] = 256;
+  rk.grid[0] = static_cast<unsigned>(cblocks * S);
+  if (split) {
+    // Finishing pass: one thread per output sums the S partials in split
+    // order, then runs the epilogue.
+    Emitter fin;
+    const int64_t outs = np.NN * W;
+    fin.line("const long gid = (long)blockIdx.x * 256 + threadIdx.x;");
+    fin.line("if (gid >= " + std::to_string(outs) + "L) return;");
+    fin.line("const int on = (int)(gid / " + std::to_string(W) + "), ow = (int)(gid % " + std::to_string(W) + ");");
+    fin.line("float tot = fg_scratch[gid];");
+    fin.line("for (int s = 1; s < " + std::to_string(S) + "; s++) tot = tot + fg_scratch[(long)s * " + std::to_string(outs) +
+             "L + gid];");
+    epilogue(fin, "on", "ow", "tot");
+    rk.source += sig(name + "_fin") + " {\n" + fin.code() + "}\n";
+    LaunchSpec a, b;
+    a.func = name + "_part";
+    a.grid[0] = rk.grid[0];
+    a.block[0] = 256;
+    b.func = name + "_fin";
+    b.grid[0] = static_cast<unsigned>((outs + 255) / 256);
+    b.block[0] = 256;
+    rk.launches = {a, b};
+    rk.scratch_bytes = static_cast<size_t>(S * outs) * sizeof(float);
+  }
+  return rk;
+}
+
 // Whether an in-place kernel reads its destination at an index other than
 // the one it stores to (the reference executes such a kernel sequentially).
 // A reduction whose value holds another reduction over the same Range node:
@@ -1693,7 +2013,10 @@ KernelClass classify_kernel(const UOp& kernel) {
   if (ki.reduces.empty()) return KernelClass::Elementwise;
   if (ki.reduces.size() > 1) return KernelClass::Serial;
   GemmMatch g;
-  if (match_gemm(ki, &g)) return KernelClass::Gemm;
+  if (match_gemm(ki, &g)) {
+    NarrowPlan np;
+    return narrow_plan(g, &np) ? KernelClass::NarrowGemm : KernelClass::Gemm;
+  }
   const UOp& R = ki.reduces[0];
   // A reduction nested in another reduction's value renders serially.
   for (auto& n : R.src(0).toposort())
@@ -1734,7 +2057,7 @@ RenderedKernel render_hip(const UOp& kernel, const std::string& name, int force_
   KernelClass k = force_class >= 0 ? static_cast<KernelClass>(force_class) : classify_kernel(kernel);
   if (!ki.reduces.empty() && k == KernelClass::Elementwise) k = KernelClass::Serial;
   // The symbol carries the lowering class so profiles name what ran.
-  static const char* suffix[] = {"_gemm", "_ew", "_rowred", "_colred", "_serial"};
+  static const char* suffix[] = {"_gemm", "_ew", "_rowred", "_colred", "_serial", "_ngemm"};
   const std::string sym = name + suffix[static_cast<int>(k)];
   std::vector<std::pair<int, DType>> params;
   for (auto& [slot, p] : ki.params) params.emplace_back(slot, p.dtype());
@@ -1744,6 +2067,13 @@ RenderedKernel render_hip(const UOp& kernel, const std::string& name, int force_
       GemmMatch g;
       FG_CHECK(match_gemm(ki, &g), "kernel does not match the MFMA GEMM pattern");
       rk = render_gemm(ki, g, sym);
+      break;
+    }
+    case KernelClass::NarrowGemm: {
+      GemmMatch g;
+      NarrowPlan np;
+      FG_CHECK(match_gemm(ki, &g) && narrow_plan(g, &np), "kernel does not match the narrow GEMM pattern");
+      rk = np.rows ? render_narrow_rows(ki, g, np, sym) : render_narrow_cols(ki, g, np, sym);
       break;
     }
     case KernelClass::Elementwise: rk = render_elementwise(ki, sym); break;

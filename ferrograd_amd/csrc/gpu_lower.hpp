@@ -35,7 +35,7 @@ KernelInfo analyze_kernel(const UOp& sink);
 int64_t range_extent(const UOp& r);
 
 // Lowering classes, in the order they are tried.
-enum class KernelClass { Gemm, Elementwise, RowReduce, ColumnReduce, Serial };
+enum class KernelClass { Gemm, Elementwise, RowReduce, ColumnReduce, Serial, NarrowGemm };
 const char* kernel_class_name(KernelClass k);
 
 // Symbolic cleanup plus the GPU range retagging (size-1 reduce ranges become

@@ -66,8 +66,8 @@ def test_c3_is_one_mfma_gemm_reading_w_directly(fg, cpu):
     compile_only(fg, src, items[0]["name"])
 
 
-@pytest.mark.parametrize("mnk,split", [((256, 128, 784), True), ((4096, 10, 2048), True), ((10, 4096, 2048), True),
-                                       ((4096, 4096, 64), False), ((256, 10, 128), False)])
+@pytest.mark.parametrize("mnk,split", [((256, 128, 784), True), ((100, 20, 8192), True), ((4096, 4096, 64), False),
+                                       ((256, 10, 128), False)])
 def test_short_grid_and_narrow_gemms_split_k(fg, cpu, mnk, split):
     m, n, k = mnk
     x = fg.Tensor.new(np.ones((m, k), np.float32), [m, k], cpu)
@@ -151,3 +151,25 @@ def test_float_literals_match_reference_text(fg, cpu):
     items = hip_plan(fg, [x.exp()])
     # LOG2_E as f32 (tensor.rs:697-700) is a loaded scalar; exp2 runs in double.
     assert "(float)exp2((double)" in items[0]["source"]
+
+
+@pytest.mark.parametrize("m,n,k,layout", [(8192, 10, 4096, "rows"), (10, 4096, 2048, "rows"), (2048, 12, 1024, "rows"),
+                                           (4096, 10, 2048, "rows")])
+def test_narrow_products_lower_to_the_narrow_class(fg, cpu, m, n, k, layout):
+    # x·Wᵀ with 16 or fewer outputs on one side: the VALU narrow kernel, not a
+    # 32-wide MFMA tile.
+    x = fg.Tensor.new(np.ones((m, k), np.float32), [m, k], cpu)
+    w = fg.Tensor.new(np.ones((n, k), np.float32), [n, k], cpu)
+    (it,) = fg.debug_plan([x.matmul(w.permute([1, 0]))], fuse=True, render_hip=True)["items"]
+    assert it["class"] == "gemm_narrow_f32" and it["name"].endswith("_ngemm")
+    # The rows layout sums its per-wave totals through the fg_nt LDS array.
+    assert ("fg_nt[" in it["source"]) == (layout == "rows")
+
+
+def test_narrow_weight_gradient_lowers_to_split_cols(fg, cpu):
+    g = fg.Tensor.new(np.ones((8192, 10), np.float32), [8192, 10], cpu)
+    h = fg.Tensor.new(np.ones((8192, 4096), np.float32), [8192, 4096], cpu)
+    w = fg.Tensor.new(np.ones((10, 4096), np.float32), [10, 4096], cpu).with_requires_grad(True)
+    (dw,) = h.matmul(w.permute([1, 0])).mul(g).sum([0, 1]).gradient([w])
+    (it,) = fg.debug_plan([dw], fuse=True, render_hip=True)["items"]
+    assert it["class"] == "gemm_narrow_f32" and "_ngemm_part" in it["source"] and "_ngemm_fin" in it["source"]

@@ -319,3 +319,45 @@ def test_requested_identity_contiguous_is_a_snapshot(fg, cpu):
     assert r_cpu and r_hip
     assert np.array_equal(c_cpu, ws) and np.array_equal(c_hip, ws)
     assert np.array_equal(w_hip, ws + np.float32(1.0)) and np.array_equal(w_cpu, w_hip)
+
+
+# ── narrow products: one output side of at most 16 (the class axis) ────────
+# They run as VALU kernels that stream the wide operand once: "rows" when it
+# is contiguous along k (the forward x·Wᵀ), "cols" when it is contiguous along
+# the wide output (the weight gradient dZᵀ·H, split over k into partials).
+@pytest.mark.parametrize("m,n,k", [(8192, 10, 4096), (1000, 16, 1000), (300, 3, 260), (10, 4096, 2048),
+                                   (4097, 7, 1024), (513, 1, 64)])
+def test_narrow_forward_rows(fg, cpu, m, n, k):
+    r = seeded(23)
+    x = r.standard_normal((m, k)).astype(np.float32)
+    w = r.uniform(-1 / 32, 1 / 32, (n, k)).astype(np.float32)
+    b = r.standard_normal(n).astype(np.float32)
+    want, got = both(lambda d: c3(fg, d, x, w, b), cpu)
+    x64, w64 = x.astype(np.float64), w.astype(np.float64)
+    scale = np.abs(x64) @ np.abs(w64).T + np.abs(b)
+    assert rel_err_bound(got, want, scale, 1e-4) <= 1.0
+    assert rel_err_bound(got, x64 @ w64.T + b, scale, 1e-4) <= 1.0
+
+
+@pytest.mark.parametrize("bsz,nn,w", [(8192, 10, 4096), (256, 10, 1000), (4096, 16, 258), (1000, 1, 4099),
+                                      (64, 10, 512)])
+def test_narrow_weight_gradient_cols_with_sgd(fg, cpu, bsz, nn, w):
+    r = seeded(29)
+    g = (r.standard_normal((bsz, nn)) / bsz).astype(np.float32)
+    h = np.maximum(r.standard_normal((bsz, w)), 0).astype(np.float32)
+    w0 = r.standard_normal((nn, w)).astype(np.float32)
+
+    def run(dev):
+        th, tg = fg.Tensor.new(h, [bsz, w], dev), fg.Tensor.new(g, [bsz, nn], dev)
+        wt = fg.Tensor.new(w0, [nn, w], dev).with_requires_grad(True)
+        (dw,) = th.matmul(wt.permute([1, 0])).mul(tg).sum([0, 1]).gradient([wt])
+        wt.assign(wt.detach().sub(dw.mul(fg.Tensor.scalar(0.01, dev))))
+        fg.Tensor.realize_many([wt])
+        return wt.numpy().reshape(nn, w)
+
+    w_cpu, w_hip = both(run, cpu)
+    import f64ref
+
+    g64, h64 = g.astype(np.float64), h.astype(np.float64)
+    assert f64ref.sgd_effective_gradient_err(w0, w_hip, g64.T @ h64, np.abs(g64).T @ np.abs(h64)) <= 1.0
+    assert f64ref.sgd_effective_gradient_err(w0, w_cpu, g64.T @ h64, np.abs(g64).T @ np.abs(h64)) <= 1.0
