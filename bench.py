@@ -136,6 +136,7 @@ def bench_c2(fg, ctx, steps, warmup):
     check = {"against": "float32 numpy, each op rounded once; relu as Where(0 < t, t, 0)",
              "elements": n, "bit_exact": bool(np.array_equal(got.view(np.uint32), want.view(np.uint32)))}
     return {"ms_per_step": ms, "gbs": alg / (ms / 1e3) / 1e9, "kernels": kern, "dominant": name, "check": check,
+            "host_ms_per_step": timed.host_ms,
             "roofline": {"bound": "hbm", "achieved": alg / (dk["avg_ms"] / 1e3) / 1e9, "peak": HBM_PEAK_GBS,
                          "unit": "GB/s", "frac": alg / (dk["avg_ms"] / 1e3) / 1e9 / HBM_PEAK_GBS,
                          "traffic": pmc_traffic(name), "kernel": name, "algorithmic_bytes": alg,
@@ -194,7 +195,10 @@ def bench_c1(fg, ctx, steps, warmup):
     want = np.maximum(x0.astype(np.float64) * 0.5 + 1.0, 0.0).sum(axis=1)
     rel = float(np.max(np.abs(got - want) / np.maximum(want, 1e-30)))
     check = {"against": "float64 row sums", "max_rel_err": rel, "tol": 1e-4, "ok": rel <= 1e-4}
+    # Host pipeline phases per step (schedule key, plan lookup, launch, ...):
+    # the gap between the kernel's rate and the per-realise rate.
     return {"ms_per_step": ms, "gbs": alg / (ms / 1e3) / 1e9, "kernels": kern, "check": check,
+            "host_ms_per_step": timed.host_ms, "kernel_ms_per_step": dk["total_ms_per_step"],
             "roofline": {"bound": "hbm", "achieved": ach, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                          "frac": ach / HBM_PEAK_GBS, "traffic": pmc_traffic(name), "kernel": name,
                          "algorithmic_bytes": alg, "kernel_avg_ms": dk["avg_ms"]}}
@@ -229,6 +233,7 @@ def bench_c3(fg, ctx, steps, warmup):
     worst = float(np.max(np.abs(got - x64 @ w64.T) / bound))
     check = {"against": "float64, 64 sampled rows", "max_err_over_bound": worst, "ok": worst <= 1.0}
     return {"ms_per_step": ms, "tflops_step": flops / (ms / 1e3) / 1e12, "kernels": kern, "check": check,
+            "host_ms_per_step": timed.host_ms,
             "roofline": {"bound": "mfma", "achieved": tf, "peak": FP32_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
                          "frac": tf / FP32_MFMA_PEAK_TFLOPS, "kernel": gemm[0] if gemm else None,
                          "traffic": pmc_traffic(gemm[0]) if gemm else None, "algorithmic_flops": flops,
@@ -506,7 +511,7 @@ def main():
                        "elements": 1 << 26, "algorithmic_bytes_per_step": 4 * (1 << 26) * 4},
             "roofline": c2["roofline"], "check": c2["check"],
             "cpu_baseline": ({"value": c2cpu["value"], "unit": "GB/s", "cores": c2cpu["cores"], "kind": c2cpu["kind"],
-                              "sample": c2cpu["sample"]} if c2cpu else None),
+                              "sample": c2cpu["sample"], "host": c2cpu.get("host")} if c2cpu else None),
             "device": info, "secondary": sec,
         }
     else:

@@ -91,6 +91,8 @@ def _declare(l: ctypes.CDLL) -> None:
         "fg_mlp_train_steps": (c_int, [P, c_int, P, P, P, c_int, ctypes.POINTER(ctypes.c_float)]),
         "fg_sgd_free": (c_int, [P]),
         "fg_synchronize": (c_int, [c_int]),
+        "fg_default_device": (c_int, [ctypes.POINTER(c_int)]),
+        "fg_gpu_passes": (c_int, [ctypes.POINTER(c_int)] * 4),
         "fg_stats": (c_int, [ctypes.POINTER(ctypes.c_uint64)] * 3),
         "fg_graph_stats": (c_int, [ctypes.POINTER(ctypes.c_uint64)] * 2),
         "fg_step_capture_stats": (c_int, [ctypes.POINTER(ctypes.c_uint64)] * 2),
@@ -118,6 +120,12 @@ def _i64(xs: Iterable[int]):
 
 
 def _dev(device) -> int:
+    """Device code of a name ("hip", "cpu"), a code, or None: the default
+    device, which the DEVICE environment variable selects ("hip" unless set)."""
+    if device is None:
+        code = ctypes.c_int()
+        _check(lib().fg_default_device(ctypes.byref(code)))
+        return code.value
     if isinstance(device, int):
         return device
     try:
@@ -168,7 +176,7 @@ class Tensor:
 
     # ── construction (tensor.rs:260-312) ─────────────────────────────────
     @staticmethod
-    def new(data, shape: Sequence[int] | None = None, device="hip", dtype=None) -> "Tensor":
+    def new(data, shape: Sequence[int] | None = None, device=None, dtype=None) -> "Tensor":
         """Tensor::new — copy host data into a new device buffer."""
         if dtype is None:
             # ndarrays keep int32/bool; everything else (lists, float64) is f32
@@ -190,21 +198,21 @@ class Tensor:
                            arr.nbytes, s, n)
 
     @staticmethod
-    def zeros(shape: Sequence[int], device="hip", dtype=None) -> "Tensor":
+    def zeros(shape: Sequence[int], device=None, dtype=None) -> "Tensor":
         s, n = _i64(shape)
         return Tensor._out(lib().fg_tensor_zeros, _dev(device), _dtype_code(dtype), s, n)
 
     @staticmethod
-    def ones(shape: Sequence[int], device="hip", dtype=None) -> "Tensor":
+    def ones(shape: Sequence[int], device=None, dtype=None) -> "Tensor":
         s, n = _i64(shape)
         return Tensor._out(lib().fg_tensor_ones, _dev(device), _dtype_code(dtype), s, n)
 
     @staticmethod
-    def full(shape: Sequence[int], value: float, device="hip") -> "Tensor":
+    def full(shape: Sequence[int], value: float, device=None) -> "Tensor":
         return Tensor.new(np.full(int(np.prod(shape)) if len(shape) else 1, value, dtype=np.float32), shape, device)
 
     @staticmethod
-    def scalar(value: float, device="hip") -> "Tensor":
+    def scalar(value: float, device=None) -> "Tensor":
         return Tensor.new(np.array([value], dtype=np.float32), [1], device)
 
     # ── metadata ─────────────────────────────────────────────────────────
@@ -391,7 +399,7 @@ class Tensor:
 class Linear:
     """nn::Linear (nn.rs:67-104): weight [out, in], Kaiming-normal seeded init, zero bias."""
 
-    def __init__(self, in_features: int, out_features: int, device="hip", bias: bool = True):
+    def __init__(self, in_features: int, out_features: int, device=None, bias: bool = True):
         h = ctypes.c_void_p()
         _check(lib().fg_linear_new(_dev(device), in_features, out_features, int(bias), ctypes.byref(h)))
         self._h = h
@@ -451,8 +459,24 @@ def reset_init_seed(seed: int = 42) -> None:
     _check(lib().fg_reset_init_seed(seed))
 
 
-def synchronize(device="hip") -> None:
+def synchronize(device=None) -> None:
     _check(lib().fg_synchronize(_dev(device)))
+
+
+def default_device() -> str:
+    """The device used where a program names none: DEVICE=hip (default) or
+    DEVICE=cpu (the test oracle's device). The reference's tensor::cpu()
+    (tensor.rs:1122-1127) with the choice moved to the environment."""
+    return {v: k for k, v in _DEVICES.items()}[_dev(None)]
+
+
+def gpu_passes() -> dict:
+    """The HIP path's optional passes as OPT selected them for this process
+    (reference grammar, src/optimize/mod.rs:85-112; names symbolic, mfma,
+    narrow, fuse)."""
+    v = [ctypes.c_int() for _ in range(4)]
+    _check(lib().fg_gpu_passes(*[ctypes.byref(x) for x in v]))
+    return dict(zip(("symbolic", "mfma", "narrow", "fuse"), (bool(x.value) for x in v)))
 
 
 def stats() -> dict:

@@ -1,6 +1,7 @@
 // C-ABI of the tensor front end (include/ferrograd.h).
 #include "../../include/ferrograd.h"
 
+#include <cstdlib>
 #include <cstring>
 #include <sstream>
 #include <string>
@@ -362,6 +363,21 @@ int fg_sgd_free(fg_sgd* s) {
 
 int fg_synchronize(int device) {
   return guard([&] { fg::get_device(to_dev(device)).synchronize(); });
+}
+
+int fg_default_device(int* device) {
+  return guard([&] { *device = fg::default_device() == fg::DeviceId::Cpu ? FG_DEV_CPU : FG_DEV_HIP; });
+}
+
+int fg_gpu_passes(int* symbolic, int* mfma, int* narrow, int* fuse) {
+  return guard([&] {
+    const fg::GpuPasses& p = fg::gpu_passes();
+    const char* e = std::getenv("FG_FUSE");
+    *symbolic = p.symbolic;
+    *mfma = p.mfma;
+    *narrow = p.narrow;
+    *fuse = p.fuse && !(e && std::strcmp(e, "0") == 0);
+  });
 }
 
 int fg_device_context(int device, void** ctx) {

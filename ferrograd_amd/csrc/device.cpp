@@ -2,6 +2,7 @@
 #include "device.hpp"
 
 #include <atomic>
+#include <cstdlib>
 
 namespace fg {
 
@@ -77,5 +78,16 @@ Device& get_device(DeviceId id) {
 }
 
 void register_device(DeviceId id, Device* dev) { g_devices[static_cast<int>(id)] = dev; }
+
+DeviceId default_device() {
+  static const std::string raw = [] {
+    const char* e = std::getenv("DEVICE");
+    return std::string(e ? e : "");
+  }();
+  if (raw.empty() || raw == "hip") return DeviceId::Hip;
+  if (raw == "cpu") return DeviceId::Cpu;
+  FG_CHECK(false, "DEVICE must be 'hip' or 'cpu'; got '" + raw + "'");
+  return DeviceId::Hip;
+}
 
 }  // namespace fg

@@ -148,6 +148,11 @@ class Device {
 // provided by the test oracle, which registers itself at load time.
 Device& get_device(DeviceId id);
 bool has_device(DeviceId id);
+// The device programs use when they name none: the reference's tensor::cpu()
+// (tensor.rs:1122-1127) with the choice moved to the DEVICE environment
+// variable, "hip" (the default, MI355X) or "cpu" (registered only by the test
+// oracle). Read once per process; any other value is an error.
+DeviceId default_device();
 void register_device(DeviceId id, Device* dev);
 Device* make_hip_device();
 // Replayed launch sequences of at least this many launches run as one HIP

@@ -131,9 +131,41 @@ KernelInfo analyze_kernel(const UOp& sink) {
   return ki;
 }
 
+// ── OPT: pass selection (src/optimize/mod.rs:85-112) ───────────────────────
+GpuPasses parse_gpu_passes(const char* raw) {
+  GpuPasses all;
+  if (!raw) return all;
+  auto trim = [](const std::string& x) {
+    size_t a = x.find_first_not_of(" \t\n"), b = x.find_last_not_of(" \t\n");
+    return a == std::string::npos ? std::string() : x.substr(a, b - a + 1);
+  };
+  const std::string s = trim(raw);
+  if (s.empty() || s == "1" || s == "on" || s == "all") return all;
+  GpuPasses some{false, false, false, false};
+  if (s == "0" || s == "off" || s == "none") return some;
+  size_t p = 0;
+  while (p <= s.size()) {
+    size_t q = s.find(',', p);
+    const std::string name = trim(s.substr(p, q == std::string::npos ? std::string::npos : q - p));
+    if (name == "symbolic") some.symbolic = true;
+    else if (name == "mfma") some.mfma = true;
+    else if (name == "narrow") some.narrow = true;
+    else if (name == "fuse") some.fuse = true;
+    if (q == std::string::npos) break;
+    p = q + 1;
+  }
+  return some;
+}
+
+const GpuPasses& gpu_passes() {
+  static const GpuPasses on = parse_gpu_passes(std::getenv("OPT"));
+  return on;
+}
+
 // ── optimize: symbolic + size-1 reduce ranges ───────────────────────────────
 UOp gpu_optimize(const UOp& rangeified) {
-  UOp k = graph_rewrite(rangeified, symbolic_simple);
+  const bool symbolic = gpu_passes().symbolic;
+  UOp k = symbolic ? graph_rewrite(rangeified, symbolic_simple) : rangeified;
   // A reduce range of extent 1 iterates once at index 0: substitute 0 and
   // drop it from the Reduce (the accumulation itself is kept).
   auto drop_unit = [](const UOp& n) -> UOp {
@@ -151,7 +183,7 @@ UOp gpu_optimize(const UOp& rangeified) {
     return UOp::make_new(Op::Reduce, n.dtype(), srcs, n.arg());
   };
   k = graph_rewrite(k, drop_unit);
-  k = graph_rewrite(k, symbolic_simple);
+  if (symbolic) k = graph_rewrite(k, symbolic_simple);
   // Output ranges map to the launch grid: retag LOOP as GLOBAL.
   auto retag = [](const UOp& n) -> UOp {
     if (n.op() != Op::Range || n.arg().range_kind() != AxisKind::Loop) return UOp();
@@ -2013,9 +2045,11 @@ KernelClass classify_kernel(const UOp& kernel) {
   if (ki.reduces.empty()) return KernelClass::Elementwise;
   if (ki.reduces.size() > 1) return KernelClass::Serial;
   GemmMatch g;
-  if (match_gemm(ki, &g)) {
+  const GpuPasses& on = gpu_passes();
+  if ((on.mfma || on.narrow) && match_gemm(ki, &g)) {
     NarrowPlan np;
-    return narrow_plan(g, &np) ? KernelClass::NarrowGemm : KernelClass::Gemm;
+    if (on.narrow && narrow_plan(g, &np)) return KernelClass::NarrowGemm;
+    if (on.mfma) return KernelClass::Gemm;
   }
   const UOp& R = ki.reduces[0];
   // A reduction nested in another reduction's value renders serially.

@@ -38,8 +38,26 @@ int64_t range_extent(const UOp& r);
 enum class KernelClass { Gemm, Elementwise, RowReduce, ColumnReduce, Serial, NarrowGemm };
 const char* kernel_class_name(KernelClass k);
 
-// Symbolic cleanup plus the GPU range retagging (size-1 reduce ranges become
-// the constant 0; output ranges become GLOBAL).
+// The HIP path's optional passes, selected by the OPT environment variable
+// with the reference's grammar (src/optimize/mod.rs:85-112): unset, empty,
+// "1", "on" or "all" enable every pass; "0", "off" or "none" disable them
+// all; otherwise a comma-separated list enables the passes it names. Names
+// the HIP path does not know (the CPU backend's "upcast", "unroll") are
+// ignored here, as the reference ignores unknown names. With a pass off, the
+// kernels it would have produced are lowered by the generic classes instead
+// (row/column reductions, serial loops; the reference's kernel partition).
+struct GpuPasses {
+  bool symbolic = true;  // constant and identity folding before lowering
+  bool mfma = true;      // MUL-over-broadcast + REDUCE as fp32 MFMA tiles
+  bool narrow = true;    // products with a side of 16 or fewer as VALU row/column kernels
+  bool fuse = true;      // schedule-time value-preserving fusion (also off with FG_FUSE=0)
+};
+GpuPasses parse_gpu_passes(const char* raw);
+// OPT as read once per process.
+const GpuPasses& gpu_passes();
+
+// Symbolic cleanup (when enabled) plus the GPU range retagging (size-1 reduce
+// ranges become the constant 0; output ranges become GLOBAL).
 UOp gpu_optimize(const UOp& rangeified);
 
 // Render a gfx950 HIP kernel (source + launch geometry) for an optimized

@@ -267,11 +267,12 @@ class HipDevice : public Device {
     if (ctx_) check(fg_hip_sync(ctx_), "fg_hip_sync");
   }
 
-  // FG_FUSE=0 keeps the reference's kernel partition (read once per process).
+  // FG_FUSE=0, or an OPT list without "fuse", keeps the reference's kernel
+  // partition (read once per process).
   bool fuse_elementwise() const override {
     static const bool on = [] {
       const char* e = std::getenv("FG_FUSE");
-      return !(e && std::strcmp(e, "0") == 0);
+      return !(e && std::strcmp(e, "0") == 0) && gpu_passes().fuse;
     }();
     return on;
   }

@@ -20,7 +20,7 @@ def one_hot(labels: np.ndarray, num_classes: int) -> np.ndarray:
 class Mlp:
     """Linear -> ReLU -> ... -> Linear (mnist.rs:30-54 is dims = (784, 128, 10))."""
 
-    def __init__(self, dims: Sequence[int], device="hip"):
+    def __init__(self, dims: Sequence[int], device=None):
         self.layers = [Linear(dims[i], dims[i + 1], device) for i in range(len(dims) - 1)]
 
     def forward(self, x: Tensor) -> Tensor:
@@ -101,7 +101,7 @@ def predictions(logits: np.ndarray) -> np.ndarray:
     return logits.shape[1] - 1 - np.argmax(flipped, axis=1)
 
 
-def train_mnist(dataset, device="hip", epochs: int = 5, batch_size: int = 256, lr: float = 0.01,
+def train_mnist(dataset, device=None, epochs: int = 5, batch_size: int = 256, lr: float = 0.01,
                 max_batches: int | None = None, log=print) -> dict:
     """examples/mnist.rs:59-126 on `device`: Linear(784,128) -> ReLU ->
     Linear(128,10), cross-entropy, SGD; batches are narrow()ed views of the

@@ -124,6 +124,15 @@ int fg_sgd_free(fg_sgd* s);
  * fg_ctx (include/ferrograd_hip.h) — the stream every realised kernel runs
  * on — for event timing and launch profiling. */
 int fg_synchronize(int device);
+/* The device a program uses when it names none: the reference's
+ * tensor::cpu() (tensor.rs:1122-1127), chosen here by the DEVICE environment
+ * variable, "hip" (default) or "cpu" (only with the test oracle loaded). */
+int fg_default_device(int* device);
+/* The HIP path's optional passes as OPT selects them, read once per process
+ * with the reference's grammar (src/optimize/mod.rs:85-112): symbolic
+ * folding, MFMA GEMM tiles, narrow VALU products, schedule-time fusion (the
+ * last also off with FG_FUSE=0). 1 = enabled. */
+int fg_gpu_passes(int* symbolic, int* mfma, int* narrow, int* fuse);
 int fg_device_context(int device, void** ctx);
 int fg_stats(uint64_t* kernels_launched, uint64_t* programs_compiled, uint64_t* lowering_hits);
 /* Replayed realisation plans that ran as one HIP graph launch, and the

@@ -13,6 +13,7 @@ import argparse
 import json
 import os
 import statistics
+import subprocess
 import sys
 import time
 
@@ -32,6 +33,34 @@ def _time(fn, runs: int, warmup: int = 1) -> float:
     return statistics.median(ts)
 
 
+def host_cpu(core: int) -> dict:
+    """The host CPU the baseline ran on: lscpu's model, CPU count and clock
+    fields, nproc (CPUs this process may use) and the pinned core's current
+    clock from /proc/cpuinfo."""
+    info = {"nproc": len(os.sched_getaffinity(0)), "cpu_count": os.cpu_count(), "pinned_core": core}
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=20).stdout
+        fields = dict(line.split(":", 1) for line in out.splitlines() if ":" in line)
+        for key, name in (("Model name", "model"), ("CPU(s)", "lscpu_cpus"), ("Socket(s)", "sockets"),
+                          ("Thread(s) per core", "threads_per_core"), ("CPU max MHz", "max_mhz"),
+                          ("CPU min MHz", "min_mhz"), ("Hypervisor vendor", "hypervisor")):
+            if key in fields:
+                info[name] = fields[key].strip()
+    except (OSError, subprocess.SubprocessError):
+        pass
+    try:
+        with open("/proc/cpuinfo") as f:
+            blocks = f.read().split("\n\n")
+        for b in blocks:
+            kv = dict((k.strip(), v.strip()) for k, v in (ln.split(":", 1) for ln in b.splitlines() if ":" in ln))
+            if kv.get("processor") == str(core):
+                info["core_mhz"] = float(kv.get("cpu MHz", "nan"))
+                info.setdefault("model", kv.get("model name"))
+    except OSError:
+        pass
+    return info
+
+
 def main() -> None:
     ap = argparse.ArgumentParser()
     ap.add_argument("config")
@@ -49,7 +78,7 @@ def main() -> None:
 
     oracle.load()
     dev = "cpu"
-    out = {"cores": 1, "kind": "port", "core": core}
+    out = {"cores": 1, "kind": "port", "core": core, "host": host_cpu(core)}
     if args.config == "c2":
         n = 1 << 26
         r = np.random.default_rng(2)
