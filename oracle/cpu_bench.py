@@ -33,11 +33,11 @@ def _time(fn, runs: int, warmup: int = 1) -> float:
     return statistics.median(ts)
 
 
-def host_cpu(core: int) -> dict:
+def host_cpu(core: int, nproc: int) -> dict:
     """The host CPU the baseline ran on: lscpu's model, CPU count and clock
-    fields, nproc (CPUs this process may use) and the pinned core's current
-    clock from /proc/cpuinfo."""
-    info = {"nproc": len(os.sched_getaffinity(0)), "cpu_count": os.cpu_count(), "pinned_core": core}
+    fields, nproc (CPUs this process could use before pinning itself to one
+    core) and the pinned core's current clock from /proc/cpuinfo."""
+    info = {"nproc": nproc, "cpu_count": os.cpu_count(), "pinned_core": core}
     try:
         out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=20).stdout
         fields = dict(line.split(":", 1) for line in out.splitlines() if ":" in line)
@@ -78,7 +78,7 @@ def main() -> None:
 
     oracle.load()
     dev = "cpu"
-    out = {"cores": 1, "kind": "port", "core": core, "host": host_cpu(core)}
+    out = {"cores": 1, "kind": "port", "core": core, "host": host_cpu(core, len(cores))}
     if args.config == "c2":
         n = 1 << 26
         r = np.random.default_rng(2)
