@@ -92,7 +92,7 @@ def _declare(l: ctypes.CDLL) -> None:
         "fg_sgd_free": (c_int, [P]),
         "fg_synchronize": (c_int, [c_int]),
         "fg_default_device": (c_int, [ctypes.POINTER(c_int)]),
-        "fg_gpu_passes": (c_int, [ctypes.POINTER(c_int)] * 4),
+        "fg_gpu_passes": (c_int, [ctypes.POINTER(c_int)] * 6),
         "fg_stats": (c_int, [ctypes.POINTER(ctypes.c_uint64)] * 3),
         "fg_graph_stats": (c_int, [ctypes.POINTER(ctypes.c_uint64)] * 2),
         "fg_step_capture_stats": (c_int, [ctypes.POINTER(ctypes.c_uint64)] * 2),
@@ -473,10 +473,10 @@ def default_device() -> str:
 def gpu_passes() -> dict:
     """The HIP path's optional passes as OPT selected them for this process
     (reference grammar, src/optimize/mod.rs:85-112; names symbolic, mfma,
-    narrow, fuse)."""
-    v = [ctypes.c_int() for _ in range(4)]
+    narrow, fuse, block, batch)."""
+    v = [ctypes.c_int() for _ in range(6)]
     _check(lib().fg_gpu_passes(*[ctypes.byref(x) for x in v]))
-    return dict(zip(("symbolic", "mfma", "narrow", "fuse"), (bool(x.value) for x in v)))
+    return dict(zip(("symbolic", "mfma", "narrow", "fuse", "block", "batch"), (bool(x.value) for x in v)))
 
 
 def stats() -> dict:

@@ -369,7 +369,7 @@ int fg_default_device(int* device) {
   return guard([&] { *device = fg::default_device() == fg::DeviceId::Cpu ? FG_DEV_CPU : FG_DEV_HIP; });
 }
 
-int fg_gpu_passes(int* symbolic, int* mfma, int* narrow, int* fuse) {
+int fg_gpu_passes(int* symbolic, int* mfma, int* narrow, int* fuse, int* block, int* batch) {
   return guard([&] {
     const fg::GpuPasses& p = fg::gpu_passes();
     const char* e = std::getenv("FG_FUSE");
@@ -377,6 +377,8 @@ int fg_gpu_passes(int* symbolic, int* mfma, int* narrow, int* fuse) {
     *mfma = p.mfma;
     *narrow = p.narrow;
     *fuse = p.fuse && !(e && std::strcmp(e, "0") == 0);
+    *block = p.block;
+    *batch = p.batch;
   });
 }
 
@@ -493,7 +495,8 @@ int fg_debug_plan(fg_tensor** roots, int n, int fuse, int render, char* buf, siz
           os << ", \"kernel\": \"" << json_escape(fg::kernel_to_text(rangeified)) << "\"";
           fg::UOp k = fg::gpu_optimize(rangeified);
           auto rk = fg::render_hip_stable(k);
-          os << ", \"name\": \"" << rk.name << "\", \"class\": \"" << rk.kind << "\", \"grid\": [" << rk.grid[0] << ", " << rk.grid[1] << ", "
+          os << ", \"name\": \"" << rk.name << "\", \"class\": \"" << rk.kind << "\", \"base_class\": \""
+             << fg::kernel_class_name(fg::base_class(k)) << "\", \"grid\": [" << rk.grid[0] << ", " << rk.grid[1] << ", "
              << rk.grid[2] << "], \"block\": [" << rk.block[0] << ", " << rk.block[1] << ", " << rk.block[2]
              << "], \"source\": \"" << json_escape(rk.source) << "\"";
         }

@@ -77,6 +77,11 @@ struct RenderedKernel {
   // launch (partial results between passes; nothing needs zeroing).
   std::vector<LaunchSpec> launches;
   size_t scratch_bytes = 0;
+  // Block kernels (one workgroup): the device function the kernel calls, its
+  // parameter types in slot order, and its source, so a device can run a run
+  // of them as one launch (render_block_batch).
+  std::string stage_fn, stage_src;
+  std::vector<std::string> stage_types;
 };
 
 struct Program {

@@ -100,6 +100,7 @@ const char* kernel_class_name(KernelClass k) {
     case KernelClass::ColumnReduce: return "column_reduce";
     case KernelClass::Serial: return "serial";
     case KernelClass::NarrowGemm: return "gemm_narrow_f32";
+    case KernelClass::Block: return "block";
   }
   return "?";
 }
@@ -141,7 +142,7 @@ GpuPasses parse_gpu_passes(const char* raw) {
   };
   const std::string s = trim(raw);
   if (s.empty() || s == "1" || s == "on" || s == "all") return all;
-  GpuPasses some{false, false, false, false};
+  GpuPasses some{false, false, false, false, false, false};
   if (s == "0" || s == "off" || s == "none") return some;
   size_t p = 0;
   while (p <= s.size()) {
@@ -151,6 +152,8 @@ GpuPasses parse_gpu_passes(const char* raw) {
     else if (name == "mfma") some.mfma = true;
     else if (name == "narrow") some.narrow = true;
     else if (name == "fuse") some.fuse = true;
+    else if (name == "block") some.block = true;
+    else if (name == "batch") some.batch = true;
     if (q == std::string::npos) break;
     p = q + 1;
   }
@@ -441,6 +444,9 @@ class Emitter {
     } else {
       std::vector<std::string> s;
       for (auto& x : n.srcs()) s.push_back(val(x, lane));
+      // Placed after its sources are emitted: a source reduction may have
+      // pinned itself to the scope it ran in.
+      si = scope_of(n);
       std::string e;
       switch (n.op()) {
         case Op::Neg: e = "(-" + s[0] + ")"; break;
@@ -469,6 +475,9 @@ class Emitter {
     cache_[key] = name;
     scopes_[si]->keys.push_back(key);
   }
+  // Treat `n` as defined by the current scope, so nodes that depend on it
+  // (a reduction's epilogue inside a loop over outputs) are placed in it.
+  void pin_here(const UOp& n) { scopes_.back()->ranges.insert(n.get()); }
   void remember_here(const UOp& n, int lane, const std::string& name) {
     bool lane_dep = lane_range_ && depends_on(n, lane_range_);
     remember(scopes_.size() - 1, std::make_pair(n.get(), lane_dep ? lane : -1), name);
@@ -1728,6 +1737,225 @@ RenderedKernel render_gemm(const KernelInfo& ki, const GemmMatch& g, const std::
   return rk;
 }
 
+// ── Block: a small kernel in one workgroup ──────────────────────────────────
+// A kernel with few outputs and little work per output (an MLP's class-axis
+// softmax pieces and loss, small bias and weight gradients) is bound by its
+// launch, not by the chip: in a graph each launch costs about 2 us of device
+// time whatever it does. Such a kernel runs as one 1024-thread workgroup
+// whose body is a device function, so a replayed sequence can run several of
+// them back to back in one launch (render_block_batch), separated by
+// workgroup barriers. The body has three forms:
+// - one output per thread, reductions serial in the reference's order
+//   (elementwise and serial kernels, and reductions of at most 32 elements);
+// - row reductions: G consecutive lanes per output stride the reduce range,
+//   then a DPP/swizzle tree over the G lanes;
+// - column reductions: consecutive lanes take consecutive outputs, TR row
+//   groups split the reduce range, and LDS folds the groups in order.
+// The reduction forms walk their outputs in rounds of a fixed trip count, so
+// their barriers and lane exchanges run in uniform control flow. A kernel computes the same bits
+// whether it runs alone or in a batch: the body is the same code.
+// One workgroup has one CU's memory parallelism: a body is cheap only while
+// each thread folds few terms. Measured on the C4 train step: a run of five
+// [256, 10] kernels whose first computed 2560 outputs of 128 terms each took
+// 48 us in one workgroup, against about 15 us as five launches; the loss
+// kernels (256 outputs of 10 terms) take well under a launch's cost.
+constexpr int kBlockThreads = 1024;
+constexpr int64_t kBlockMaxOutputs = 4096;
+constexpr int64_t kBlockMaxReduce = 1024;
+constexpr int64_t kBlockMaxWork = int64_t(1) << 16;  // terms folded, all outputs: 64 per thread
+
+// Terms a reduction folds per output: its extent, times the terms of any
+// reduction recomputed inside its value.
+int64_t reduce_terms(const UOp& R) {
+  int64_t l = 1;
+  for (size_t i = 1; i < R.srcs().size(); i++) l *= range_extent(R.src(i));
+  int64_t inner = 0;
+  for (auto& n : R.src(0).toposort())
+    if (n.op() == Op::Reduce) {
+      int64_t m = 1;
+      for (size_t i = 1; i < n.srcs().size(); i++) m *= range_extent(n.src(i));
+      inner += m;
+    }
+  return l * (1 + inner);
+}
+
+bool block_eligible(const KernelInfo& ki, KernelClass base) {
+  if (base == KernelClass::Gemm || base == KernelClass::NarrowGemm) return false;
+  const int64_t T = total_outputs(ki);
+  if (T > kBlockMaxOutputs) return false;
+  std::set<const UOpInner*> nested;
+  for (auto& R : ki.reduces)
+    for (auto& n : R.src(0).toposort())
+      if (n.op() == Op::Reduce) nested.insert(n.get());
+  int64_t terms = 0;
+  for (auto& R : ki.reduces) {
+    int64_t l = 1;
+    for (size_t i = 1; i < R.srcs().size(); i++) l *= range_extent(R.src(i));
+    if (l > kBlockMaxReduce) return false;
+    if (!nested.count(R.get())) terms += reduce_terms(R);
+  }
+  return T * std::max<int64_t>(terms, 1) <= kBlockMaxWork;
+}
+
+// Parameter list of a block body: no __restrict__, since a batched launch
+// passes a buffer one stage writes to a later stage that reads it.
+std::string block_params(const KernelInfo& ki, std::vector<std::string>* types, std::vector<std::string>* names) {
+  std::ostringstream os;
+  bool first = true;
+  for (auto& [slot, p] : ki.params) {
+    std::string t = p.op() == Op::ParamBuffer ? std::string(p == ki.out_param ? "" : "const ") + ctype(p.dtype()) + "*"
+                                              : std::string(ctype(p.dtype()));
+    os << (first ? "" : ", ") << t << " data" << slot;
+    first = false;
+    types->push_back(t);
+    names->push_back("data" + std::to_string(slot));
+  }
+  return os.str();
+}
+
+RenderedKernel render_block(const KernelInfo& ki, KernelClass base, const std::string& name) {
+  const int64_t T = total_outputs(ki);
+  const std::string NT = std::to_string(kBlockThreads);
+  Emitter em;
+  const UOp* R = ki.reduces.size() == 1 ? &ki.reduces[0] : nullptr;
+  int64_t Lin = 1;
+  if (R) Lin = range_extent(R->srcs().back());
+  const bool serial_form = !R || base == KernelClass::Serial || base == KernelClass::Elementwise || Lin <= 32;
+  auto store = [&](const std::string& guard) {
+    std::string v = em.val(ki.value, 0);
+    em.line(guard + pname(ki.out_param) + "[" + em.idx(ki.out_index, 0) + "] = " + v + ";");
+  };
+  if (serial_form) {
+    em.open_scope("for (long gid = threadIdx.x; gid < " + std::to_string(T) + "L; gid += " + NT + ") {", "}");
+    decode_outputs(em, ki, "gid", UOp());
+    em.reduce_cb_ = [&](const UOp& RR, int lane) {
+      std::string acc = emit_serial_reduce(em, RR, lane);
+      em.pin_here(RR);
+      em.remember_here(RR, lane, acc);
+      return acc;
+    };
+    store("");
+    em.close_scope();
+  } else if (base == KernelClass::ColumnReduce && R->srcs().size() == 2) {
+    // Consecutive lanes take consecutive outputs (the memory's fast axis), TR
+    // row groups split the reduce range (unrolled, loads in flight together),
+    // and the TR partials are folded through LDS in row-group order.
+    // TR ~ sqrt(L) balances the loads and the fold.
+    const UOp r = R->src(1);
+    int TR = 2;
+    while (TR < 32 && static_cast<int64_t>(TR) * TR < Lin) TR *= 2;
+    const int TX = kBlockThreads / TR;
+    const int64_t rounds = (T + TX - 1) / TX, trips = (Lin + TR - 1) / TR;
+    const Op rop = R->arg().rop;
+    const DType dt = R->dtype();
+    em.line("const int tx = threadIdx.x % " + std::to_string(TX) + ", tr = threadIdx.x / " + std::to_string(TX) + ";");
+    em.line(std::string("__shared__ ") + ctype(dt) + " fg_blk[" + std::to_string(TR) + "][" + std::to_string(TX) + "];");
+    em.open_scope("for (int rnd = 0; rnd < " + std::to_string(rounds) + "; rnd++) {", "}");
+    em.line("const long oid = (long)rnd * " + std::to_string(TX) + " + tx;");
+    em.line("const bool active = oid < " + std::to_string(T) + "L;");
+    em.line("const long ocl = active ? oid : 0;");
+    decode_outputs(em, ki, "ocl", UOp());
+    em.reduce_cb_ = [&](const UOp& RR, int lane) -> std::string {
+      FG_CHECK(RR == *R, "block column reduce renders exactly one reduction");
+      std::string acc = em.fresh("bacc");
+      em.line(std::string(ctype(dt)) + " " + acc + " = " + init_lit(rop, dt) + ";");
+      size_t opened = 0;
+      em.open_scope("if (active) {", "}");
+      opened++;
+      em.open_scope("#pragma unroll\nfor (int bit = 0; bit < " + std::to_string(trips) + "; bit++) {", "}");
+      opened++;
+      em.line("const int rr = tr + bit * " + std::to_string(TR) + ";");
+      if (Lin % TR != 0) {
+        em.open_scope("if (rr < " + std::to_string(Lin) + ") {", "}");
+        opened++;
+      }
+      em.define_range(r, "rr");
+      em.line(acc + " = " + combine(rop, acc, em.val(R->src(0), 0)) + ";");
+      for (size_t i = 0; i < opened; i++) em.close_scope();
+      em.line("fg_blk[tr][tx] = " + acc + ";");
+      em.line("__syncthreads();");
+      em.line(acc + " = fg_blk[0][tx];");
+      em.line("#pragma unroll");
+      em.line("for (int q = 1; q < " + std::to_string(TR) + "; q++) " + acc + " = " + combine(rop, acc, "fg_blk[q][tx]") +
+              ";");
+      em.line("__syncthreads();");
+      em.pin_here(RR);
+      em.remember_here(RR, lane, acc);
+      return acc;
+    };
+    store("if (active && tr == 0) ");
+    em.close_scope();
+  } else {
+    // Row reductions: G consecutive lanes per output stride the innermost
+    // reduce range (outer reduce ranges loop serially), fully unrolled so a
+    // lane's loads are in flight together, then a DPP/swizzle tree over the G
+    // lanes. G ~ sqrt(L) balances the two.
+    std::vector<UOp> ranges(R->srcs().begin() + 1, R->srcs().end());
+    const UOp r_in = ranges.back();
+    int G = 2;
+    while (G < 64 && static_cast<int64_t>(G) * G < Lin) G *= 2;
+    const int64_t per_round = kBlockThreads / G, rounds = (T + per_round - 1) / per_round;
+    const int64_t trips = (Lin + G - 1) / G;
+    const Op rop = R->arg().rop;
+    const DType dt = R->dtype();
+    em.line("const int lg = threadIdx.x % " + std::to_string(G) + ";");
+    em.open_scope("for (int rnd = 0; rnd < " + std::to_string(rounds) + "; rnd++) {", "}");
+    em.line("const long oid = (long)rnd * " + std::to_string(per_round) + " + threadIdx.x / " + std::to_string(G) + ";");
+    em.line("const bool active = oid < " + std::to_string(T) + "L;");
+    em.line("const long ocl = active ? oid : 0;");
+    decode_outputs(em, ki, "ocl", UOp());
+    em.reduce_cb_ = [&](const UOp& RR, int lane) -> std::string {
+      FG_CHECK(RR == *R, "block reduction renders exactly one reduction");
+      std::string acc = em.fresh("bacc");
+      em.line(std::string(ctype(dt)) + " " + acc + " = " + init_lit(rop, dt) + ";");
+      size_t opened = 0;
+      em.open_scope("if (active) {", "}");
+      opened++;
+      for (size_t i = 0; i + 1 < ranges.size(); i++) {
+        std::string v = "bro" + std::to_string(i);
+        em.open_scope("for (int " + v + " = 0; " + v + " < " + std::to_string(range_extent(ranges[i])) + "; " + v + "++) {",
+                      "}");
+        em.define_range(ranges[i], v);
+        opened++;
+      }
+      em.open_scope("#pragma unroll\nfor (int bit = 0; bit < " + std::to_string(trips) + "; bit++) {", "}");
+      opened++;
+      em.line("const int rj = lg + bit * " + std::to_string(G) + ";");
+      if (Lin % G != 0) {
+        em.open_scope("if (rj < " + std::to_string(Lin) + ") {", "}");
+        opened++;
+      }
+      em.define_range(r_in, "rj");
+      em.line(acc + " = " + combine(rop, acc, em.val(R->src(0), 0)) + ";");
+      for (size_t i = 0; i < opened; i++) em.close_scope();
+      std::string wr = wave_reduce(acc, G, rop, dt);
+      std::istringstream is(wr);
+      std::string l;
+      while (std::getline(is, l)) em.line(l);
+      em.pin_here(RR);
+      em.remember_here(RR, lane, acc);
+      return acc;
+    };
+    store("if (active && lg == 0) ");
+    em.close_scope();
+  }
+  RenderedKernel rk;
+  std::vector<std::string> names;
+  const std::string params = block_params(ki, &rk.stage_types, &names);
+  rk.stage_fn = name + "_body";
+  rk.stage_src = "__device__ __forceinline__ void " + rk.stage_fn + "(" + params + ") {\n" + em.code() + "}\n";
+  std::string call = rk.stage_fn + "(";
+  for (size_t i = 0; i < names.size(); i++) call += (i ? ", " : "") + names[i];
+  call += ");";
+  rk.name = name;
+  rk.kind = kernel_class_name(KernelClass::Block);
+  rk.source = std::string(kPrelude) + rk.stage_src + "extern \"C\" __global__ void __launch_bounds__(" + NT + ") " + name +
+              "(" + params + ") {\n  " + call + "\n}\n";
+  rk.block[0] = kBlockThreads;
+  rk.grid[0] = 1;
+  return rk;
+}
+
 // ── Narrow GEMM (VALU, HBM-bound) ───────────────────────────────────────────
 // A product with one output side of at most kNarrow elements (the 10 classes
 // of an MLP's last layer) streams its wide operand once and does only
@@ -2040,7 +2268,8 @@ bool reads_dest_elsewhere(const KernelInfo& ki) {
 
 }  // namespace
 
-KernelClass classify_kernel(const UOp& kernel) {
+// The class a kernel would have on its own size (no block promotion).
+KernelClass base_class(const UOp& kernel) {
   KernelInfo ki = analyze_kernel(kernel);
   if (ki.reduces.empty()) return KernelClass::Elementwise;
   if (ki.reduces.size() > 1) return KernelClass::Serial;
@@ -2071,6 +2300,12 @@ KernelClass classify_kernel(const UOp& kernel) {
   return KernelClass::Serial;
 }
 
+KernelClass classify_kernel(const UOp& kernel) {
+  const KernelClass base = base_class(kernel);
+  if (gpu_passes().block && block_eligible(analyze_kernel(kernel), base)) return KernelClass::Block;
+  return base;
+}
+
 RenderedKernel render_hip(const UOp& kernel, const std::string& name, int force_class) {
   KernelInfo ki = analyze_kernel(kernel);
   // Kernel indexes are int32, as rangeify builds them (schedule/indexing.rs:
@@ -2091,7 +2326,7 @@ RenderedKernel render_hip(const UOp& kernel, const std::string& name, int force_
   KernelClass k = force_class >= 0 ? static_cast<KernelClass>(force_class) : classify_kernel(kernel);
   if (!ki.reduces.empty() && k == KernelClass::Elementwise) k = KernelClass::Serial;
   // The symbol carries the lowering class so profiles name what ran.
-  static const char* suffix[] = {"_gemm", "_ew", "_rowred", "_colred", "_serial", "_ngemm"};
+  static const char* suffix[] = {"_gemm", "_ew", "_rowred", "_colred", "_serial", "_ngemm", "_blk"};
   const std::string sym = name + suffix[static_cast<int>(k)];
   std::vector<std::pair<int, DType>> params;
   for (auto& [slot, p] : ki.params) params.emplace_back(slot, p.dtype());
@@ -2114,6 +2349,12 @@ RenderedKernel render_hip(const UOp& kernel, const std::string& name, int force_
     case KernelClass::RowReduce: rk = render_row_reduce(ki, sym); break;
     case KernelClass::ColumnReduce: rk = render_column_reduce(ki, sym); break;
     case KernelClass::Serial: rk = render_serial(ki, sym); break;
+    case KernelClass::Block: {
+      const KernelClass base = base_class(kernel);
+      FG_CHECK(block_eligible(ki, base), "kernel is too large for one workgroup");
+      rk = render_block(ki, base, sym);
+      break;
+    }
   }
   rk.params = params;
   return rk;
@@ -2137,7 +2378,47 @@ RenderedKernel render_hip_stable(const UOp& kernel) {
   };
   replace_all(rk.source);
   replace_all(rk.name);
+  replace_all(rk.stage_fn);
+  replace_all(rk.stage_src);
   for (auto& l : rk.launches) replace_all(l.func);
+  return rk;
+}
+
+RenderedKernel render_block_batch(const std::vector<const RenderedKernel*>& stages) {
+  FG_CHECK(stages.size() >= 2, "a batch runs at least two block kernels");
+  static const std::string kPlaceholder = "FGBATCHNAME";
+  std::ostringstream src, params, body;
+  src << kPrelude;
+  std::set<std::string> defined;
+  size_t n = 0;
+  for (size_t i = 0; i < stages.size(); i++) {
+    const RenderedKernel& st = *stages[i];
+    FG_CHECK(!st.stage_fn.empty(), "kernel " + st.name + " is not a block kernel");
+    if (defined.insert(st.stage_fn).second) src << st.stage_src;
+    if (i) body << "  __syncthreads();\n";
+    body << "  " << st.stage_fn << "(";
+    for (size_t j = 0; j < st.stage_types.size(); j++, n++) {
+      params << (n ? ", " : "") << st.stage_types[j] << " a" << n;
+      body << (j ? ", " : "") << "a" << n;
+    }
+    body << ");\n";
+  }
+  src << "extern \"C\" __global__ void __launch_bounds__(" << kBlockThreads << ") " << kPlaceholder << "("
+      << params.str() << ") {\n" << body.str() << "}\n";
+  RenderedKernel rk;
+  rk.source = src.str();
+  uint64_t h = 1469598103934665603ULL;
+  for (unsigned char c : rk.source) {
+    h ^= c;
+    h *= 1099511628211ULL;
+  }
+  char hex[40];
+  std::snprintf(hex, sizeof(hex), "k%012llx_batch", static_cast<unsigned long long>(h & 0xffffffffffffULL));
+  for (size_t p = rk.source.find(kPlaceholder); p != std::string::npos; p = rk.source.find(kPlaceholder, p))
+    rk.source.replace(p, kPlaceholder.size(), hex);
+  rk.name = hex;
+  rk.kind = "block_batch";
+  rk.block[0] = kBlockThreads;
   return rk;
 }
 

@@ -35,7 +35,7 @@ KernelInfo analyze_kernel(const UOp& sink);
 int64_t range_extent(const UOp& r);
 
 // Lowering classes, in the order they are tried.
-enum class KernelClass { Gemm, Elementwise, RowReduce, ColumnReduce, Serial, NarrowGemm };
+enum class KernelClass { Gemm, Elementwise, RowReduce, ColumnReduce, Serial, NarrowGemm, Block };
 const char* kernel_class_name(KernelClass k);
 
 // The HIP path's optional passes, selected by the OPT environment variable
@@ -51,6 +51,8 @@ struct GpuPasses {
   bool mfma = true;      // MUL-over-broadcast + REDUCE as fp32 MFMA tiles
   bool narrow = true;    // products with a side of 16 or fewer as VALU row/column kernels
   bool fuse = true;      // schedule-time value-preserving fusion (also off with FG_FUSE=0)
+  bool block = true;     // small kernels as one 1024-thread workgroup ("_blk")
+  bool batch = true;     // consecutive block kernels of a replayed sequence in one launch
 };
 GpuPasses parse_gpu_passes(const char* raw);
 // OPT as read once per process.
@@ -66,5 +68,13 @@ RenderedKernel render_hip(const UOp& kernel, const std::string& name, int force_
 // render_hip with the symbol named by a hash of the source ("k<hash>_<class>").
 RenderedKernel render_hip_stable(const UOp& kernel);
 KernelClass classify_kernel(const UOp& kernel);
+// The class a kernel has before a small one is promoted to KernelClass::Block.
+KernelClass base_class(const UOp& kernel);
+
+// One launch for a run of block kernels (KernelClass::Block) that a replayed
+// sequence launches back to back: their bodies, in order, separated by
+// workgroup barriers, taking every stage's arguments concatenated in stage
+// order. Each stage computes exactly what its own kernel computes.
+RenderedKernel render_block_batch(const std::vector<const RenderedKernel*>& stages);
 
 }  // namespace fg

@@ -200,29 +200,48 @@ class HipDevice : public Device {
       int uses = 0;
       bool failed = false;
       fg_graph* graph = nullptr;
+      // Runs of consecutive block kernels that launch as one batch: (first
+      // program, count) and the batch program of each.
+      std::vector<std::pair<size_t, size_t>> groups;
+      std::vector<std::shared_ptr<Program>> batches;
       ~Replay() { fg_hip_graph_free(graph); }
     };
     if (!state) state = std::make_shared<Replay>();
     auto* r = static_cast<Replay*>(state.get());
     r->uses++;
+    if (r->uses == 1 && gpu_passes().batch) group_blocks(progs, args, r->groups, r->batches);
     std::vector<fg_prog*> lp;
     std::vector<unsigned> grids, blocks, lds;
     std::vector<int> nargs;
     std::vector<fg_arg> all;
+    auto add = [&](fg_prog* fp, const unsigned* g, const unsigned* b, unsigned l, const std::vector<fg_arg>& a) {
+      lp.push_back(fp);
+      grids.insert(grids.end(), g, g + 3);
+      blocks.insert(blocks.end(), b, b + 3);
+      lds.push_back(l);
+      nargs.push_back(static_cast<int>(a.size()));
+      all.insert(all.end(), a.begin(), a.end());
+    };
+    size_t next_group = 0;
     for (size_t i = 0; i < progs.size(); i++) {
+      if (next_group < r->groups.size() && r->groups[next_group].first == i) {
+        const size_t n = r->groups[next_group].second;
+        std::vector<fg_arg> a;
+        for (size_t j = i; j < i + n; j++) {
+          std::vector<fg_arg> aj = marshal(static_cast<HipProgram&>(*progs[j]), args[j]);
+          a.insert(a.end(), aj.begin(), aj.end());
+        }
+        auto& bp = static_cast<HipProgram&>(*r->batches[next_group]);
+        add(bp.prog, bp.meta.grid, bp.meta.block, bp.meta.lds_bytes, a);
+        next_group++;
+        i += n - 1;
+        continue;
+      }
       auto& p = static_cast<HipProgram&>(*progs[i]);
       std::vector<fg_arg> a = marshal(p, args[i]);
-      auto add = [&](fg_prog* fp, const unsigned* g, const unsigned* b, unsigned l) {
-        lp.push_back(fp);
-        grids.insert(grids.end(), g, g + 3);
-        blocks.insert(blocks.end(), b, b + 3);
-        lds.push_back(l);
-        nargs.push_back(static_cast<int>(a.size()));
-        all.insert(all.end(), a.begin(), a.end());
-      };
-      if (p.passes.empty()) add(p.prog, p.meta.grid, p.meta.block, p.meta.lds_bytes);
+      if (p.passes.empty()) add(p.prog, p.meta.grid, p.meta.block, p.meta.lds_bytes, a);
       for (size_t k = 0; k < p.passes.size(); k++)
-        add(p.passes[k], p.meta.launches[k].grid, p.meta.launches[k].block, p.meta.launches[k].lds_bytes);
+        add(p.passes[k], p.meta.launches[k].grid, p.meta.launches[k].block, p.meta.launches[k].lds_bytes, a);
     }
     if (graphs_enabled() && !r->failed && !r->graph && r->uses >= 2 &&
         lp.size() >= static_cast<size_t>(graph_min_launches())) {
@@ -244,6 +263,39 @@ class HipDevice : public Device {
       check(fg_hip_launch(ctx(), lp[i], all.data() + off, nargs[i], &grids[3 * i], &blocks[3 * i], lds[i]),
             "execution failed");
       off += static_cast<size_t>(nargs[i]);
+    }
+  }
+
+  // Runs of two or more consecutive block kernels (one workgroup each, no
+  // scratch) in a sequence: each becomes one launch of a batch program that
+  // runs the kernels' bodies in order behind workgroup barriers. At most
+  // kMaxBatch kernels per batch. The batch's code object is cached by its
+  // source like any other.
+  void group_blocks(const std::vector<Program*>& progs, std::vector<std::vector<KernelArg>>& args,
+                    std::vector<std::pair<size_t, size_t>>& groups, std::vector<std::shared_ptr<Program>>& batches) {
+    constexpr size_t kMaxBatch = 16;
+    auto is_block = [&](size_t i) {
+      auto& p = static_cast<HipProgram&>(*progs[i]);
+      return !p.meta.stage_fn.empty() && p.passes.empty() && !p.scratch;
+    };
+    for (size_t i = 0; i < progs.size();) {
+      if (!is_block(i)) {
+        i++;
+        continue;
+      }
+      size_t n = 1;
+      while (i + n < progs.size() && n < kMaxBatch && is_block(i + n)) n++;
+      if (n >= 2) {
+        std::vector<const RenderedKernel*> stages;
+        size_t total = 0;
+        for (size_t j = i; j < i + n; j++) {
+          stages.push_back(&progs[j]->meta);
+          total += args[j].size();
+        }
+        batches.push_back(compile(render_block_batch(stages), total));
+        groups.emplace_back(i, n);
+      }
+      i += n;
     }
   }
 

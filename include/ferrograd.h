@@ -130,9 +130,10 @@ int fg_synchronize(int device);
 int fg_default_device(int* device);
 /* The HIP path's optional passes as OPT selects them, read once per process
  * with the reference's grammar (src/optimize/mod.rs:85-112): symbolic
- * folding, MFMA GEMM tiles, narrow VALU products, schedule-time fusion (the
- * last also off with FG_FUSE=0). 1 = enabled. */
-int fg_gpu_passes(int* symbolic, int* mfma, int* narrow, int* fuse);
+ * folding, MFMA GEMM tiles, narrow VALU products, schedule-time fusion (also
+ * off with FG_FUSE=0), small kernels as one workgroup, and consecutive such
+ * kernels of a replayed sequence batched into one launch. 1 = enabled. */
+int fg_gpu_passes(int* symbolic, int* mfma, int* narrow, int* fuse, int* block, int* batch);
 int fg_device_context(int device, void** ctx);
 int fg_stats(uint64_t* kernels_launched, uint64_t* programs_compiled, uint64_t* lowering_hits);
 /* Replayed realisation plans that ran as one HIP graph launch, and the

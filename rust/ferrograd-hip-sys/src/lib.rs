@@ -235,7 +235,8 @@ extern "C" {
     pub fn fg_sgd_free(s: *mut fg_sgd) -> i32;
     pub fn fg_synchronize(device: i32) -> i32;
     pub fn fg_default_device(device: *mut i32) -> i32;
-    pub fn fg_gpu_passes(symbolic: *mut i32, mfma: *mut i32, narrow: *mut i32, fuse: *mut i32) -> i32;
+    pub fn fg_gpu_passes(symbolic: *mut i32, mfma: *mut i32, narrow: *mut i32, fuse: *mut i32, block: *mut i32,
+                         batch: *mut i32) -> i32;
     pub fn fg_device_context(device: i32, ctx: *mut *mut c_void) -> i32;
     pub fn fg_stats(kernels_launched: *mut u64, programs_compiled: *mut u64, lowering_hits: *mut u64) -> i32;
     pub fn fg_graph_stats(replays: *mut u64, updated_launches: *mut u64) -> i32;

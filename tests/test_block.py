@@ -1,0 +1,161 @@
+"""Small kernels as one 1024-thread workgroup (the `block` class) and runs of
+them batched into one launch (the `batch` pass).
+
+A block kernel's body is a device function; alone it is launched as one
+workgroup, in a batch several bodies run back to back behind workgroup
+barriers. The values are the oracle's within the reduction tolerance
+(1e-4·Σ|terms|; max and elementwise bit for bit), and a batched sequence
+gives the same bits as the same kernels launched one by one.
+"""
+from __future__ import annotations
+
+import json
+import os
+import subprocess
+import sys
+
+import numpy as np
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def plan(fg, roots):
+    return fg.debug_plan(roots, fuse=True, render_hip=True)["items"]
+
+
+def rnd(shape, seed):
+    return np.random.default_rng(seed).standard_normal(shape).astype(np.float32)
+
+
+# (name, builder over (device, arrays), arrays, expected base class)
+CASES = {
+    "row_sum_L128": (lambda fg, d, a: fg.Tensor.new(a[0], list(a[0].shape), d).sum([1]), [rnd((40, 128), 1)], "row_reduce"),
+    "row_max_L64": (lambda fg, d, a: fg.Tensor.new(a[0], list(a[0].shape), d).max([1]), [rnd((100, 64), 2)], "row_reduce"),
+    "row_sum_L1000_one_output": (lambda fg, d, a: fg.Tensor.new(a[0], list(a[0].shape), d).sum([0]),
+                                 [rnd((1000,), 3)], "row_reduce"),
+    "col_sum_T64": (lambda fg, d, a: fg.Tensor.new(a[0], list(a[0].shape), d).sum([0]), [rnd((300, 64), 4)], "column_reduce"),
+    "col_sum_T1000": (lambda fg, d, a: fg.Tensor.new(a[0], list(a[0].shape), d).sum([0]), [rnd((64, 1000), 5)],
+                      "column_reduce"),
+    "col_sum_T10_relu_product": (lambda fg, d, a: fg.Tensor.new(a[0], list(a[0].shape), d).relu()
+                                 .mul(fg.Tensor.new(a[1], list(a[1].shape), d)).sum([0]),
+                                 [rnd((256, 10), 6), rnd((256, 10), 7)], "column_reduce"),
+    "log_softmax_32x10": (lambda fg, d, a: fg.Tensor.new(a[0], list(a[0].shape), d).log_softmax(1), [rnd((32, 10), 8)],
+                          None),
+    "elementwise_1000": (lambda fg, d, a: fg.Tensor.new(a[0], [1000], d).mul(fg.Tensor.new(a[1], [1000], d)).relu(),
+                         [rnd((1000,), 9), rnd((1000,), 10)], "elementwise"),
+}
+
+
+@pytest.mark.parametrize("name", sorted(CASES))
+def test_small_kernels_plan_as_one_workgroup(fg, cpu, name):
+    build, arrays, base = CASES[name]
+    items = plan(fg, [build(fg, cpu, arrays)])
+    assert all(it["class"] == "block" for it in items), [(it["class"], it["base_class"]) for it in items]
+    assert all(it["grid"] == [1, 1, 1] and it["block"] == [1024, 1, 1] for it in items)
+    if base:
+        assert items[-1]["base_class"] == base
+    assert all("_body(" in it["source"] and "__restrict__" not in it["source"].split("_body(")[1].split(")")[0]
+               for it in items)
+
+
+def test_kernels_past_the_workgroup_limits_keep_their_class(fg, cpu):
+    # More than 4096 outputs, a reduction longer than 1024, or more than 2^16
+    # terms folded in all (64 per thread): the ordinary multi-workgroup classes.
+    big_out = fg.Tensor.new(np.ones((5000,), np.float32), [5000], cpu).relu()
+    long_red = fg.Tensor.new(np.ones((8, 2048), np.float32), [8, 2048], cpu).sum([1])
+    much_work = fg.Tensor.new(np.ones((512, 256), np.float32), [512, 256], cpu).sum([0])
+    for t, cls in ((big_out, "elementwise"), (long_red, "row_reduce"), (much_work, "column_reduce")):
+        (it,) = plan(fg, [t])
+        assert it["class"] == cls and it["base_class"] == cls
+
+
+def compile_all(src):
+    import ctypes
+    import re
+
+    from ferrograd_amd.hip import api
+
+    for fn in re.findall(r"extern \"C\" __global__ void __launch_bounds__\(\d+\) (\w+)\(", src):
+        h = ctypes.c_void_p()
+        assert api().fg_hip_compile(None, src.encode(), fn.encode(), 16, ctypes.byref(h)) == 0, api().fg_hip_last_error()
+
+
+def test_block_sources_compile(fg, cpu):
+    for name, (build, arrays, _) in CASES.items():
+        for it in plan(fg, [build(fg, cpu, arrays)]):
+            compile_all(it["source"])
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("name", sorted(CASES))
+def test_block_kernels_match_the_oracle(fg, cpu, hip, name):
+    build, arrays, _ = CASES[name]
+    print(f"block case {name}", flush=True)
+    got = build(fg, hip, arrays).numpy().astype(np.float64)
+    want = build(fg, cpu, arrays).numpy().astype(np.float64)
+    if name.startswith(("row_max", "elementwise")):
+        assert np.array_equal(got, want)
+        return
+    a = arrays[0].astype(np.float64)
+    if name == "col_sum_T10_relu_product":
+        scale = (np.maximum(a, 0) * np.abs(arrays[1])).sum(0)
+    elif name.startswith("col_sum") or name == "row_sum_L1000_one_output":
+        scale = np.abs(a).sum(0)
+    elif name.startswith("row_sum"):
+        scale = np.abs(a).sum(1)
+    else:  # log_softmax: max-shifted log of a 10-term sum of exponentials
+        scale = np.abs(want) + np.log(np.exp(a - a.max(1, keepdims=True)).sum(1, keepdims=True)) + 1.0
+    assert np.all(np.abs(got - want).reshape(-1) <= 1e-4 * np.asarray(scale).reshape(-1) + 1e-30)
+
+
+# C4-sized train steps in a child process with the given OPT: losses and every
+# parameter, and the launches per step seen by the launch profiler.
+STEPS_SCRIPT = r"""
+import json, sys
+import numpy as np
+sys.path.insert(0, %r)
+import ferrograd_amd as fg
+from ferrograd_amd.hip import Context
+from ferrograd_amd.mlp import Mlp, synthetic_batch, train_step, train_steps_native
+fg.reset_init_seed(42)
+model = Mlp((784, 128, 10), "hip")
+opt = fg.Sgd(model.parameters(), 0.01)
+xs, ts = synthetic_batch(256, 784, 10, 7, 8)
+x = fg.Tensor.new(xs, list(xs.shape), "hip")
+t = fg.Tensor.new(ts, list(ts.shape), "hip")
+losses = [train_step(model, opt, x, t).to_vec()[0] for _ in range(4)]
+ctx = Context.of_device()
+ctx.profile_read()
+ctx.profile(True)
+losses += [train_step(model, opt, x, t).to_vec()[0]]
+fg.synchronize()
+ctx.profile(False)
+launches = len(ctx.profile_read())
+losses += train_steps_native(model, opt, x, t, 6)
+print(json.dumps({"passes": fg.gpu_passes(), "losses": losses, "launches": launches,
+                  "params": [p.numpy().tolist() for p in model.parameters()]}))
+"""
+
+
+def run_steps(opt):
+    env = {k: v for k, v in os.environ.items() if k != "OPT"}
+    if opt is not None:
+        env["OPT"] = opt
+    print(f"C4 steps with OPT={opt}", flush=True)
+    p = subprocess.run([sys.executable, "-u", "-c", STEPS_SCRIPT % ROOT], env=env, capture_output=True, text=True,
+                       timeout=110)
+    assert p.returncode == 0, p.stderr[-3000:]
+    return json.loads(p.stdout.strip().splitlines()[-1])
+
+
+@pytest.mark.gpu
+def test_batched_launches_give_the_same_bits_as_one_by_one(fg, hip):
+    batched = run_steps(None)
+    single = run_steps("symbolic,mfma,narrow,fuse,block")
+    assert batched["passes"]["batch"] and not single["passes"]["batch"]
+    assert batched["losses"] == single["losses"]
+    for a, b in zip(batched["params"], single["params"]):
+        assert np.array_equal(np.asarray(a, np.float32), np.asarray(b, np.float32))
+    # The C4 step's two runs of small kernels each became one launch.
+    assert batched["launches"] <= single["launches"] - 6, (batched["launches"], single["launches"])

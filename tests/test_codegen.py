@@ -21,7 +21,7 @@ def compile_only(fg, source: str, name: str):
 
 
 def test_c2_is_one_vectorised_elementwise_kernel(fg, cpu):
-    a, b, c = (fg.Tensor.new(np.ones(1 << 12, np.float32), [1 << 12], cpu) for _ in range(3))
+    a, b, c = (fg.Tensor.new(np.ones(1 << 16, np.float32), [1 << 16], cpu) for _ in range(3))
     items = hip_plan(fg, [a.mul(b).add(c).relu()])
     assert [it["class"] for it in items] == ["elementwise"]
     src = items[0]["source"]
@@ -75,7 +75,8 @@ def test_short_grid_and_narrow_gemms_split_k(fg, cpu, mnk, split):
     items = hip_plan(fg, [x.matmul(w.permute([1, 0]))])
     gemm = [it for it in items if it["class"] == "gemm_mfma_f32"]
     if (m, n, k) == (256, 10, 128):
-        # Too small a grid for a 32-wide tile: stays a row reduction.
+        # Too small a grid for a 32-wide tile: stays a row reduction (2560
+        # outputs of 128 terms are too much work for one workgroup).
         assert not gemm and items[-1]["class"] == "row_reduce"
         return
     assert len(gemm) == 1

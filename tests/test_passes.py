@@ -69,7 +69,7 @@ def classes(report, prog):
 
 def test_opt_unset_enables_every_gpu_pass():
     rep = json.loads(run_child({}).stdout)
-    assert rep["passes"] == {"symbolic": True, "mfma": True, "narrow": True, "fuse": True}
+    assert rep["passes"] == {"symbolic": True, "mfma": True, "narrow": True, "fuse": True, "block": True, "batch": True}
     assert rep["default_device"] == "hip"
     assert "gemm_mfma_f32" in classes(rep, "matmul")
     assert "gemm_narrow_f32" in classes(rep, "narrow")
@@ -78,10 +78,11 @@ def test_opt_unset_enables_every_gpu_pass():
 @pytest.mark.parametrize("value", ["0", "off", "none", " none "])
 def test_opt_off_disables_every_gpu_pass_and_still_lowers(value):
     rep = json.loads(run_child({"OPT": value}).stdout)
-    assert rep["passes"] == {"symbolic": False, "mfma": False, "narrow": False, "fuse": False}
+    assert rep["passes"] == {"symbolic": False, "mfma": False, "narrow": False, "fuse": False, "block": False,
+                             "batch": False}
     for prog, rows in rep["programs"].items():
         for r in rows:
-            assert r["class"] not in ("gemm_mfma_f32", "gemm_narrow_f32"), (prog, r)
+            assert r["class"] not in ("gemm_mfma_f32", "gemm_narrow_f32", "block"), (prog, r)
             assert r["compiles"] and r["functions"] >= 1, (prog, r)
 
 
@@ -95,7 +96,8 @@ def test_opt_list_selects_named_passes_and_ignores_cpu_pass_names():
     # "upcast" and "unroll" are the CPU backend's passes: ignored by the HIP
     # path, as the reference ignores names it does not know.
     rep = json.loads(run_child({"OPT": "symbolic, mfma,upcast,unroll,bogus"}).stdout)
-    assert rep["passes"] == {"symbolic": True, "mfma": True, "narrow": False, "fuse": False}
+    assert rep["passes"] == {"symbolic": True, "mfma": True, "narrow": False, "fuse": False, "block": False,
+                             "batch": False}
     assert "gemm_mfma_f32" in classes(rep, "matmul")
     # Without the narrow pass the 10-wide product is no longer a narrow kernel.
     assert "gemm_narrow_f32" not in classes(rep, "narrow")
@@ -105,7 +107,8 @@ def test_opt_list_selects_named_passes_and_ignores_cpu_pass_names():
 
 def test_opt_narrow_without_mfma():
     rep = json.loads(run_child({"OPT": "narrow"}).stdout)
-    assert rep["passes"] == {"symbolic": False, "mfma": False, "narrow": True, "fuse": False}
+    assert rep["passes"] == {"symbolic": False, "mfma": False, "narrow": True, "fuse": False, "block": False,
+                             "batch": False}
     assert "gemm_narrow_f32" in classes(rep, "narrow")
     assert "gemm_mfma_f32" not in classes(rep, "matmul")
 

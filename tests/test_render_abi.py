@@ -68,7 +68,7 @@ def test_kernel_text_round_trip_reproduces_the_rendering(fg, cpu):
 
     fg.reset_init_seed(42)
     m = Mlp((64, 48, 10), cpu)
-    xs, ts = synthetic_batch(32, 64, 10, 1, 2)
+    xs, ts = synthetic_batch(512, 64, 10, 1, 2)
     loss = m.forward(fg.Tensor.new(xs, list(xs.shape), cpu)).cross_entropy(fg.Tensor.new(ts, list(ts.shape), cpu))
     loss.backward()
     params = m.parameters()
@@ -76,6 +76,9 @@ def test_kernel_text_round_trip_reproduces_the_rendering(fg, cpu):
         p.assign(p.detach().sub(p.grad().mul(fg.Tensor.scalar(0.01, cpu))))
     items = [it for root, _ in roots.values() for it in plan(fg, root)]
     items += fg.debug_plan(params + [loss], fuse=True, render_hip=True)["items"]
+    # A column sum too long for one workgroup: split into partials and a finishing pass.
+    cols = fg.Tensor.new(np.ones((4096, 512), np.float32), [4096, 512], cpu)
+    items += fg.debug_plan([cols.sum([0])], fuse=True, render_hip=True)["items"]
     kinds = set()
     for it in items:
         r = Rendered(it["kernel"])
@@ -84,7 +87,7 @@ def test_kernel_text_round_trip_reproduces_the_rendering(fg, cpu):
         assert len(r.params) == len(it["inputs"]) + (1 if it["output"] is not None else 0)
         kinds.add((r.kind, len(r.launches), r.scratch_bytes > 0))
     assert ("gemm_mfma_f32", 2, True) in kinds and ("column_reduce", 2, True) in kinds
-    assert {"elementwise", "row_reduce", "serial"} <= {k[0] for k in kinds}
+    assert {"elementwise", "row_reduce", "serial", "block"} <= {k[0] for k in kinds}
 
 
 def test_parameter_kinds_follow_the_slots(fg, cpu):

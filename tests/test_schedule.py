@@ -163,7 +163,7 @@ def test_fusion_runs_linear_bias_as_reduce_epilogue_and_recomputes_relu_mask(fg,
     assert not any("bool* __restrict__ data0" in it["source"] for it in fused)  # no mask buffer
     # Every [16, 64] / [16, 48] pre-activation is written by a reduction kernel.
     pre = [it for it in fused if it.get("out_shape") in ([16, 64], [16, 48])]
-    assert pre and all(it["class"] != "elementwise" for it in pre)
+    assert pre and all(it["base_class"] != "elementwise" for it in pre)
 
 
 def test_cheap_node_with_scalar_inputs_is_recomputed(fg, cpu):
@@ -257,7 +257,7 @@ def test_reduce_read_through_broadcast_stays_materialised(fg, cpu):
     y = x.sum([1]).mul(fg.Tensor.scalar(2.0, cpu))
     z = y.expand([4, 64]).add(x)
     items = plan(fg, [z], fuse=True, render=True)
-    assert [it["class"] for it in items] == ["row_reduce", "elementwise"]
+    assert [it["base_class"] for it in items] == ["row_reduce", "elementwise"]
 
 
 def test_small_reduce_is_recomputed_by_its_consumer(fg, cpu):
@@ -267,7 +267,7 @@ def test_small_reduce_is_recomputed_by_its_consumer(fg, cpu):
     x = fg.Tensor.new(np.ones((4, 8), np.float32), [4, 8], cpu)
     z = x.sum([1]).mul(fg.Tensor.scalar(2.0, cpu)).expand([4, 8]).add(x)
     items = plan(fg, [z], fuse=True, render=True)
-    assert [it["class"] for it in items] == ["row_reduce"]
+    assert [it["base_class"] for it in items] == ["row_reduce"]
     assert items[0]["out_shape"] == [4, 8]
     assert len(plan(fg, [z], fuse=False)) == 2
 
@@ -278,7 +278,7 @@ def test_small_reduce_broadcast_far_stays_materialised(fg, cpu):
     y = x.sum([1]).mul(fg.Tensor.scalar(2.0, cpu))
     z = y.expand([4, 200]).add(fg.Tensor.new(np.ones((4, 200), np.float32), [4, 200], cpu))
     items = plan(fg, [z], fuse=True, render=True)
-    assert [it["class"] for it in items] == ["row_reduce", "elementwise"]
+    assert [it["base_class"] for it in items] == ["row_reduce", "elementwise"]
 
 
 def test_small_reduce_feeding_a_reduce_stays_materialised(fg, cpu):
@@ -287,7 +287,7 @@ def test_small_reduce_feeding_a_reduce_stays_materialised(fg, cpu):
     x = fg.Tensor.new(np.ones((64, 8), np.float32), [64, 8], cpu)
     z = x.sum([1]).mul(fg.Tensor.scalar(2.0, cpu)).sum([0])
     items = plan(fg, [z], fuse=True, render=True)
-    assert len(items) == 2 and "serial" not in [it["class"] for it in items]
+    assert len(items) == 2 and "serial" not in [it["base_class"] for it in items]
 
 
 def test_two_reduces_into_one_consumer_keep_one_per_kernel(fg, cpu):
@@ -296,7 +296,7 @@ def test_two_reduces_into_one_consumer_keep_one_per_kernel(fg, cpu):
     w = fg.Tensor.new(np.ones((4, 64), np.float32), [4, 64], cpu)
     z = x.sum([1]).add(w.max([1]))
     items = plan(fg, [z], fuse=True, render=True)
-    assert len(items) == 2 and all(it["class"] == "row_reduce" for it in items)
+    assert len(items) == 2 and all(it["base_class"] == "row_reduce" for it in items)
 
 
 def test_reduce_read_after_an_in_place_store_is_materialised_first(fg, cpu):
