@@ -2357,6 +2357,7 @@ RenderedKernel render_hip(const UOp& kernel, const std::string& name, int force_
     }
   }
   rk.params = params;
+  rk.out_slot = static_cast<int>(ki.out_param.arg().a);
   return rk;
 }
 

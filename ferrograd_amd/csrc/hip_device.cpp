@@ -3,6 +3,7 @@
 // gpu_lower.cpp as its optimize/render stages.
 #include <cstdlib>
 #include <cstring>
+#include <set>
 
 #include "../../include/ferrograd_hip.h"
 #include "device.hpp"
@@ -204,12 +205,25 @@ class HipDevice : public Device {
       // program, count) and the batch program of each.
       std::vector<std::pair<size_t, size_t>> groups;
       std::vector<std::shared_ptr<Program>> batches;
+      std::vector<size_t> order;  // launch order of the programs (empty: as given)
       ~Replay() { fg_hip_graph_free(graph); }
     };
     if (!state) state = std::make_shared<Replay>();
     auto* r = static_cast<Replay*>(state.get());
     r->uses++;
-    if (r->uses == 1 && gpu_passes().batch) group_blocks(progs, args, r->groups, r->batches);
+    if (r->uses == 1 && gpu_passes().batch) {
+      r->order = sink_blocks(progs, args);
+      std::vector<Program*> ordered;
+      std::vector<std::vector<KernelArg>> ordered_args;
+      for (size_t i = 0; i < progs.size(); i++) {
+        const size_t k = r->order.empty() ? i : r->order[i];
+        ordered.push_back(progs[k]);
+        ordered_args.push_back(args[k]);
+      }
+      group_blocks(ordered, ordered_args, r->groups, r->batches);
+    }
+    auto prog_at = [&](size_t i) -> Program* { return r->order.empty() ? progs[i] : progs[r->order[i]]; };
+    auto args_at = [&](size_t i) -> std::vector<KernelArg>& { return r->order.empty() ? args[i] : args[r->order[i]]; };
     std::vector<fg_prog*> lp;
     std::vector<unsigned> grids, blocks, lds;
     std::vector<int> nargs;
@@ -228,7 +242,7 @@ class HipDevice : public Device {
         const size_t n = r->groups[next_group].second;
         std::vector<fg_arg> a;
         for (size_t j = i; j < i + n; j++) {
-          std::vector<fg_arg> aj = marshal(static_cast<HipProgram&>(*progs[j]), args[j]);
+          std::vector<fg_arg> aj = marshal(static_cast<HipProgram&>(*prog_at(j)), args_at(j));
           a.insert(a.end(), aj.begin(), aj.end());
         }
         auto& bp = static_cast<HipProgram&>(*r->batches[next_group]);
@@ -237,8 +251,8 @@ class HipDevice : public Device {
         i += n - 1;
         continue;
       }
-      auto& p = static_cast<HipProgram&>(*progs[i]);
-      std::vector<fg_arg> a = marshal(p, args[i]);
+      auto& p = static_cast<HipProgram&>(*prog_at(i));
+      std::vector<fg_arg> a = marshal(p, args_at(i));
       if (p.passes.empty()) add(p.prog, p.meta.grid, p.meta.block, p.meta.lds_bytes, a);
       for (size_t k = 0; k < p.passes.size(); k++)
         add(p.passes[k], p.meta.launches[k].grid, p.meta.launches[k].block, p.meta.launches[k].lds_bytes, a);
@@ -264,6 +278,56 @@ class HipDevice : public Device {
             "execution failed");
       off += static_cast<size_t>(nargs[i]);
     }
+  }
+
+  // A launch order in which block kernels sit next to each other where the
+  // data allow: a block kernel moves later, past kernels it shares no buffer
+  // with (neither reads what the other writes, nor both write one buffer),
+  // when that brings it up to the next block kernel. Buffers are told apart by
+  // their device addresses in this first call: within one sequence every
+  // output is a fresh allocation and every input is live, so equal addresses
+  // are the same buffer in every later call too. Empty when nothing moves.
+  std::vector<size_t> sink_blocks(const std::vector<Program*>& progs, std::vector<std::vector<KernelArg>>& args) {
+    const size_t n = progs.size();
+    auto is_block = [&](size_t i) {
+      auto& p = static_cast<HipProgram&>(*progs[i]);
+      return !p.meta.stage_fn.empty() && p.passes.empty() && !p.scratch;
+    };
+    std::vector<std::set<void*>> reads(n), writes(n);
+    for (size_t i = 0; i < n; i++) {
+      const RenderedKernel& m = progs[i]->meta;
+      for (size_t j = 0; j < args[i].size(); j++) {
+        if (args[i][j].kind != KernelArg::Kind::Buffer || !args[i][j].buffer->realized) continue;
+        void* ptr = args[i][j].buffer->storage;
+        const bool out = j < m.params.size() && m.params[j].first == m.out_slot;
+        (out ? writes : reads)[i].insert(ptr);
+        if (out) reads[i].insert(ptr);  // an in-place update also reads its destination
+      }
+    }
+    auto independent = [&](size_t a, size_t b) {
+      for (void* w : writes[a])
+        if (reads[b].count(w) || writes[b].count(w)) return false;
+      for (void* w : writes[b])
+        if (reads[a].count(w)) return false;
+      return true;
+    };
+    std::vector<size_t> order(n);
+    for (size_t i = 0; i < n; i++) order[i] = i;
+    bool moved = false;
+    for (size_t pos = 0; pos < n; pos++) {
+      const size_t k = order[pos];
+      if (!is_block(k) || (pos + 1 < n && is_block(order[pos + 1]))) continue;
+      size_t q = pos + 1;
+      while (q < n && !is_block(order[q]) && independent(k, order[q])) q++;
+      if (q == pos + 1 || q == n || !is_block(order[q])) continue;
+      // Move k from pos to just before q (after the kernels it passed).
+      order.erase(order.begin() + static_cast<long>(pos));
+      order.insert(order.begin() + static_cast<long>(q - 1), k);
+      moved = true;
+      pos--;  // re-examine the kernel that slid into pos
+    }
+    if (!moved) order.clear();
+    return order;
   }
 
   // Runs of two or more consecutive block kernels (one workgroup each, no

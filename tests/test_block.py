@@ -157,5 +157,7 @@ def test_batched_launches_give_the_same_bits_as_one_by_one(fg, hip):
     assert batched["losses"] == single["losses"]
     for a, b in zip(batched["params"], single["params"]):
         assert np.array_equal(np.asarray(a, np.float32), np.asarray(b, np.float32))
-    # The C4 step's two runs of small kernels each became one launch.
-    assert batched["launches"] <= single["launches"] - 6, (batched["launches"], single["launches"])
+    # The C4 update plan's class-axis kernels became one launch, b1's
+    # gradient moved past dW2's (no shared buffer) to join b2's in another, and
+    # the loss plan's four kernels one more: 7 launches fewer.
+    assert batched["launches"] <= single["launches"] - 7, (batched["launches"], single["launches"])
