@@ -132,6 +132,13 @@ class Device {
     (void)state;
     for (size_t i = 0; i < progs.size(); i++) execute(*progs[i], args[i]);
   }
+  // execute_sequence, then `result` read back into `slot` as read_async
+  // does. A device may fold the copy into the sequence itself.
+  virtual void execute_sequence_read(const std::vector<Program*>& progs, std::vector<std::vector<KernelArg>>& args,
+                                     std::shared_ptr<void>& state, const Buffer& result, int slot) {
+    execute_sequence(progs, args, state);
+    read_async(result, slot);
+  }
   virtual void synchronize() {}
   // Whether schedule-time value-preserving fusion (shared elementwise
   // subexpressions inlined into one kernel, zero buffers folded) is enabled.

@@ -360,6 +360,31 @@ int fg_hip_read_async(fg_ctx* c, int slot, const void* src, size_t n) {
   return FG_OK;
 }
 
+int fg_hip_read_slot(fg_ctx* c, int slot, void** device_ptr) {
+  if (!c || !device_ptr) return set_err(FG_ERR_INVALID, "fg_hip_read_slot: null argument");
+  if (slot < 0 || slot >= FG_READ_SLOTS)
+    return set_err(FG_ERR_INVALID, "fg_hip_read_slot: slot " + std::to_string(slot) + " outside 0.." +
+                                       std::to_string(FG_READ_SLOTS - 1));
+  if (c->async_pending[slot]) HIP_TRY(hipEventSynchronize(c->async_events[slot]));  // its last read landed
+  c->async_pending[slot] = false;
+  HIP_TRY(hipHostGetDevicePointer(device_ptr, c->async_read + static_cast<size_t>(slot) * FG_READ_SLOT_BYTES, 0));
+  return FG_OK;
+}
+
+int fg_hip_read_queued(fg_ctx* c, int slot, size_t n) {
+  if (!c) return set_err(FG_ERR_INVALID, "fg_hip_read_queued: null context");
+  if (slot < 0 || slot >= FG_READ_SLOTS)
+    return set_err(FG_ERR_INVALID, "fg_hip_read_queued: slot " + std::to_string(slot) + " outside 0.." +
+                                       std::to_string(FG_READ_SLOTS - 1));
+  if (n > FG_READ_SLOT_BYTES)
+    return set_err(FG_ERR_INVALID, "fg_hip_read_queued: " + std::to_string(n) + " bytes exceed a slot's " +
+                                       std::to_string(FG_READ_SLOT_BYTES));
+  HIP_TRY(hipEventRecord(c->async_events[slot], c->stream));
+  c->async_bytes[slot] = n;
+  c->async_pending[slot] = true;
+  return FG_OK;
+}
+
 int fg_hip_read_wait(fg_ctx* c, int slot, void* dst, size_t n) {
   if (!c || (!dst && n)) return set_err(FG_ERR_INVALID, "fg_hip_read_wait: null argument");
   if (slot < 0 || slot >= FG_READ_SLOTS || !c->async_pending[slot])

@@ -912,8 +912,9 @@ std::unique_ptr<CapturedStep> capture_step(const std::vector<ReplayRecord>& prev
 }
 
 // Launches every kernel of a captured step as one sequence (a single HIP
-// graph from its second run on) and returns the step's result buffer.
-Buffer replay_step(Device& backend, CapturedStep& cap) {
+// graph from its second run on), with the step's result (the loss) read back
+// into `slot` (Device::read_async) behind it.
+void replay_step(Device& backend, CapturedStep& cap, int slot) {
   const size_t n = cap.kernels.size();
   std::vector<Buffer> outs(n);
   std::vector<Program*> progs(n);
@@ -938,11 +939,10 @@ Buffer replay_step(Device& backend, CapturedStep& cap) {
   }
   uint64_t l1 = now_ns();
   realize_stats().ns_lower += l1 - l0;
-  backend.execute_sequence(progs, args, cap.device_state);
+  backend.execute_sequence_read(progs, args, cap.device_state, outs[cap.result_kernel], slot);
   realize_stats().ns_launch += now_ns() - l1;
   realize_stats().kernels_launched += n;
   realize_stats().lowering_cache_hits += n;
-  return outs[cap.result_kernel];
 }
 
 bool step_capture_enabled() {
@@ -1343,7 +1343,7 @@ std::vector<float> train_steps(const std::vector<const Linear*>& layers, const S
   bool prev_valid = false;
   for (int i = 0; i < steps; i++) {
     if (cap && i + 1 < steps) {
-      dev.read_async(replay_step(dev, *cap), i % 2);
+      replay_step(dev, *cap, i % 2);
       realize_stats().steps_replayed++;
       if (i > 0) collect(i - 1);
       continue;

@@ -93,6 +93,15 @@ int fg_hip_copy_d2d(fg_ctx* ctx, void* dst, const void* src, size_t nbytes);
 #define FG_READ_SLOT_BYTES ((size_t)65536)
 int fg_hip_read_async(fg_ctx* ctx, int slot, const void* src, size_t nbytes);
 int fg_hip_read_wait(fg_ctx* ctx, int slot, void* dst, size_t nbytes);
+/* The same read-back done by a kernel of the caller's own launches (the last
+ * node of a replayed sequence's graph), so no separate copy is queued.
+ * fg_hip_read_slot waits until `slot` is free (its previous read landed) and
+ * gives the device address of its pinned landing area, which a kernel may
+ * store up to FG_READ_SLOT_BYTES into. After queuing that kernel,
+ * fg_hip_read_queued marks the slot as holding `nbytes` that land behind the
+ * work on the stream; fg_hip_read_wait then waits for them as above. */
+int fg_hip_read_slot(fg_ctx* ctx, int slot, void** device_ptr);
+int fg_hip_read_queued(fg_ctx* ctx, int slot, size_t nbytes);
 
 /* Compile HIP source for gfx950 with hiprtc and load kernel `func`. The code
  * object is cached on disk keyed by a hash of source, options and target. */

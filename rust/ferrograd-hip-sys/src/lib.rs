@@ -110,6 +110,8 @@ extern "C" {
     pub fn fg_hip_copy_d2d(ctx: *mut fg_ctx, dst: *mut c_void, src: *const c_void, nbytes: usize) -> i32;
     pub fn fg_hip_read_async(ctx: *mut fg_ctx, slot: i32, src: *const c_void, nbytes: usize) -> i32;
     pub fn fg_hip_read_wait(ctx: *mut fg_ctx, slot: i32, dst: *mut c_void, nbytes: usize) -> i32;
+    pub fn fg_hip_read_slot(ctx: *mut fg_ctx, slot: i32, device_ptr: *mut *mut c_void) -> i32;
+    pub fn fg_hip_read_queued(ctx: *mut fg_ctx, slot: i32, nbytes: usize) -> i32;
     pub fn fg_hip_compile(ctx: *mut fg_ctx, source: *const c_char, func: *const c_char, num_args: i32,
                           out: *mut *mut fg_prog) -> i32;
     pub fn fg_hip_program_free(prog: *mut fg_prog) -> i32;
