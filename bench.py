@@ -255,9 +255,13 @@ def mlp_gemm_flops(batch, dims):
 def bench_mlp(fg, ctx, steps, warmup, batch, dims, native_steps=None):
     from ferrograd_amd.mlp import mlp_setup, train_steps_native
 
-    # Step 1 schedules and compiles, step 2 replays the plan, step 3 records
-    # its HIP graph: all three stay out of the timed region.
-    warmup = max(warmup, 3)
+    # The first step runs while the biases still hold allocate()'s zeros (a
+    # plan of its own); the steady-state plan then schedules and compiles, is
+    # replayed once (its block kernels batched and compiled), and is recorded
+    # as a HIP graph on its second replay. Six steps keep all of that out of
+    # the timed region, and the native warm-up call also captures its step
+    # and replays it, compiling the captured sequence's batches.
+    warmup = max(warmup, 6)
     step, (model, opt, x, t) = mlp_setup(fg, "hip", batch=batch, dims=dims, with_state=True)
     losses = []
     ms, prof = timed(fg, ctx, lambda: losses.append(step()), steps, warmup)
