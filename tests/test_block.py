@@ -161,3 +161,23 @@ def test_batched_launches_give_the_same_bits_as_one_by_one(fg, hip):
     # gradient moved past dW2's (no shared buffer) to join b2's in another, and
     # the loss plan's four kernels one more: 7 launches fewer.
     assert batched["launches"] <= single["launches"] - 7, (batched["launches"], single["launches"])
+
+
+def test_reference_partition_small_kernels_compile_as_blocks(fg, cpu):
+    # Without the schedule-time fusions the relu masks are materialised as
+    # bool buffers: small ones become block kernels with a bool output.
+    from ferrograd_amd.mlp import Mlp, synthetic_batch
+
+    fg.reset_init_seed(42)
+    m = Mlp((64, 32, 10), cpu)
+    xs, ts = synthetic_batch(16, 64, 10, 1, 2)
+    loss = m.forward(fg.Tensor.new(xs, list(xs.shape), cpu)).cross_entropy(fg.Tensor.new(ts, list(ts.shape), cpu))
+    loss.backward()
+    params = m.parameters()
+    for p in params:
+        p.assign(p.detach().sub(p.grad().mul(fg.Tensor.scalar(0.01, cpu))))
+    items = fg.debug_plan(params + [loss], fuse=False, render_hip=True)["items"]
+    blocks = [it for it in items if it["class"] == "block"]
+    assert blocks and any("void " in it["source"] and "bool* data0" in it["source"] for it in blocks)
+    for it in items:
+        compile_all(it["source"])

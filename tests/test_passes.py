@@ -183,8 +183,11 @@ print(json.dumps(rep))
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("opt", ["0", "symbolic,fuse"])
+@pytest.mark.parametrize("opt", ["0", "symbolic,fuse", "symbolic,mfma,narrow,block,batch"])
 def test_hip_with_gpu_passes_off_matches_oracle(opt):
+    # The third leaves out only the schedule-time fusion: the reference
+    # partition, whose materialised relu masks are small bool kernels that
+    # run (and batch) as one-workgroup block kernels.
     env = {k: v for k, v in os.environ.items() if k not in ("OPT", "DEVICE", "FG_FUSE")}
     env["OPT"] = opt
     print(f"OPT={opt}: child process", flush=True)
@@ -192,7 +195,8 @@ def test_hip_with_gpu_passes_off_matches_oracle(opt):
                        text=True, timeout=110)
     assert p.returncode == 0, p.stderr[-3000:]
     rep = json.loads(p.stdout.strip().splitlines()[-1])
-    assert not rep["passes"]["mfma"] and not rep["passes"]["narrow"]
+    names = opt.split(",")
+    assert all(rep["passes"][k] == (k in names) for k in ("fuse", "mfma", "narrow", "block", "batch"))
     assert max(rep["err_over_bound"]) <= 1.0, rep
     assert rep["max_bit_exact"], rep
     assert rep["loss_rel"] <= 1e-4, rep
