@@ -167,6 +167,21 @@ def test_narrow_products_lower_to_the_narrow_class(fg, cpu, m, n, k, layout):
     assert ("fg_nt[" in it["source"]) == (layout == "rows")
 
 
+@pytest.mark.parametrize("m,n,k,cached", [(8192, 10, 4096, True), (1500, 10, 2000, True), (1537, 16, 1500, True),
+                                           (300, 10, 4096, True), (602, 12, 4000, False), (4096, 10, 8192, False)])
+def test_narrow_rows_hold_the_narrow_operand_in_registers_when_it_fits(fg, cpu, m, n, k, cached):
+    # N x ceil(K/1024) x 4 floats of the narrow operand per thread: at most
+    # 160 (two waves per SIMD), else the row-group layout that re-reads it.
+    x = fg.Tensor.new(np.ones((m, k), np.float32), [m, k], cpu)
+    w = fg.Tensor.new(np.ones((n, k), np.float32), [n, k], cpu)
+    (it,) = fg.debug_plan([x.matmul(w.permute([1, 0]))], fuse=True, render_hip=True)["items"]
+    assert it["class"] == "gemm_narrow_f32"
+    assert ("nb0_0[" in it["source"]) == cached
+    if cached:
+        rows = -(-m // min(512, m))
+        assert it["grid"] == [-(-m // rows), 1, 1] and it["block"] == [256, 1, 1]
+
+
 def test_narrow_weight_gradient_lowers_to_split_cols(fg, cpu):
     g = fg.Tensor.new(np.ones((8192, 10), np.float32), [8192, 10], cpu)
     h = fg.Tensor.new(np.ones((8192, 4096), np.float32), [8192, 4096], cpu)

@@ -153,10 +153,13 @@ def test_c1_row_reduce(fg, cpu, shape):
 # (BK 8) and 256x256 (BK 16, 8 waves), with ragged M/N edges and K not a
 # multiple of the k-tile; split K (partials summed by a second pass) on a
 # short grid, on narrow 32-wide tiles for N or M of 10, and with a ragged
-# last column group.
+# last column group. The narrow rows layout with its operand in registers:
+# k not a multiple of 1024, an odd or ragged count of rows per workgroup,
+# fewer rows than workgroups.
 @pytest.mark.parametrize("mnk", [(64, 64, 64), (256, 128, 784), (128, 10, 128), (512, 512, 512), (100, 70, 30),
                                  (4100, 4000, 100), (4096, 2100, 72), (2100, 4096, 40), (4096, 10, 2048),
-                                 (10, 4096, 2048), (1000, 70, 3000), (12, 602, 4000)])
+                                 (10, 4096, 2048), (1000, 70, 3000), (12, 602, 4000), (1500, 10, 2000),
+                                 (1537, 16, 1500), (300, 10, 4096)])
 def test_c3_linear_forward(fg, cpu, mnk):
     m, n, k = mnk
     r = seeded(5)
