@@ -349,6 +349,18 @@ typedef float fg_probe_f4 __attribute__((ext_vector_type(4)));
 extern "C" __global__ void __launch_bounds__(256) fg_copy_probe_nt(fg_probe_f4* __restrict__ dst, const fg_probe_f4* __restrict__ src, int n4) {
   const int i = blockIdx.x * 256 + threadIdx.x;
   if (i < n4) __builtin_nontemporal_store(__builtin_nontemporal_load(src + i), dst + i);
+}
+extern "C" __global__ void __launch_bounds__(256) fg_read_probe(float* __restrict__ dst, const fg_probe_f4* __restrict__ src, int n4) {
+  // 16 non-temporal 16-byte loads per thread, all issued before the sum; one float written per thread.
+  const int base = blockIdx.x * 4096 + threadIdx.x;
+  fg_probe_f4 v[16];
+  #pragma unroll
+  for (int j = 0; j < 16; j++)
+    v[j] = base + 256 * j < n4 ? __builtin_nontemporal_load(src + base + 256 * j) : fg_probe_f4{0.f, 0.f, 0.f, 0.f};
+  float s = 0.f;
+  #pragma unroll
+  for (int j = 0; j < 16; j++) s += v[j].x + v[j].y + v[j].z + v[j].w;
+  dst[blockIdx.x * 256 + threadIdx.x] = s;
 }"""
 
 
@@ -356,9 +368,10 @@ def copy_probe(nbytes: int = 1 << 30, reps: int = 5) -> None:
     """Launch a plain copy of `nbytes` (read + write) `reps` times: the
     reference kernel whose FETCH_SIZE / WRITE_SIZE counters calibrate the
     byte counts of the generated kernels under rocprofv3 --pmc. Also times it,
-    and a non-temporal copy, with events: the practical streaming ceiling the
-    HBM-bound kernels are compared with (3 source/destination pairs rotate so
-    the 256 MB Infinity Cache cannot hold a launch's data)."""
+    a non-temporal copy and a non-temporal read of `nbytes` with events: the
+    practical streaming ceilings the HBM-bound kernels are compared with (3
+    source/destination pairs rotate so the 256 MB Infinity Cache cannot hold a
+    launch's data)."""
     from ferrograd_amd.hip import Arg, Context
 
     ctx = Context(0)
@@ -371,17 +384,22 @@ def copy_probe(nbytes: int = 1 << 30, reps: int = 5) -> None:
         ctx.launch(prog, [Arg.ptr(dst), Arg.ptr(src), Arg.i32(n4)], grid=grid, block=block)
     ctx.sync()
     rates = {}
-    for name in ("fg_copy_probe", "fg_copy_probe_nt"):
+    for name in ("fg_copy_probe", "fg_copy_probe_nt", "fg_read_probe"):
         p = ctx.compile(COPY_SRC, name, 3)
+        # The read probe's grid covers 16 float4 per thread; it writes one float
+        # per thread (1/64 of the bytes read) into the destination.
+        g = ((n4 + 4095) // 4096, 1, 1) if name == "fg_read_probe" else grid
+        moved = nbytes if name == "fg_read_probe" else 2 * nbytes
         ms = []
         for i in range(3 + 20):
             src, dst = pairs[i % 3]
             ctx.record(0)
-            ctx.launch(p, [Arg.ptr(dst), Arg.ptr(src), Arg.i32(n4)], grid=grid, block=block)
+            ctx.launch(p, [Arg.ptr(dst), Arg.ptr(src), Arg.i32(n4)], grid=g, block=block)
             ctx.record(1)
             if i >= 3:
                 ms.append(ctx.elapsed_ms(0, 1))
-        rates[name + "_gbs"] = 2 * nbytes / (float(np.mean(ms)) / 1e3) / 1e9
+        rates[name + "_us"] = float(np.mean(ms)) * 1e3
+        rates[name + "_gbs"] = moved / (float(np.mean(ms)) / 1e3) / 1e9
     print(json.dumps({"copy_probe_bytes_read": nbytes, "copy_probe_bytes_written": nbytes, "launches": reps, **rates}))
 
 
@@ -444,12 +462,13 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--kernels", action="store_true", help="include per-kernel tables")
     ap.add_argument("--copy-probe", action="store_true", help="only run the 1 GiB copy calibration kernel")
+    ap.add_argument("--probe-mib", type=int, default=1024, help="bytes the copy probe copies, in MiB")
     ap.add_argument("--library-compare", action="store_true", help="only time torch's fp32 mm and add for reference")
     ap.add_argument("--shard-sweep", action="store_true",
                     help="only time the C5 step at the per-GPU batch of 1, 2, 4 and 8-way data parallelism")
     args = ap.parse_args()
     if args.copy_probe:
-        copy_probe()
+        copy_probe(args.probe_mib << 20)
         return
     if args.library_compare:
         library_compare()
