@@ -2564,8 +2564,8 @@ RenderedKernel render_hip_stable(const UOp& kernel) {
   return rk;
 }
 
-RenderedKernel render_block_batch(const std::vector<const RenderedKernel*>& stages) {
-  FG_CHECK(stages.size() >= 2, "a batch runs at least two block kernels");
+RenderedKernel render_block_batch(const std::vector<const RenderedKernel*>& stages, bool read_back) {
+  FG_CHECK(stages.size() >= (read_back ? 1u : 2u), "a batch runs at least two block kernels");
   static const std::string kPlaceholder = "FGBATCHNAME";
   std::ostringstream src, params, body;
   src << kPrelude;
@@ -2582,6 +2582,11 @@ RenderedKernel render_block_batch(const std::vector<const RenderedKernel*>& stag
       body << (j ? ", " : "") << "a" << n;
     }
     body << ");\n";
+  }
+  if (read_back) {
+    params << ", unsigned int* rb_dst, const unsigned int* rb_src, int rb_words";
+    body << "  __syncthreads();\n"
+         << "  for (int i = threadIdx.x; i < rb_words; i += " << kBlockThreads << ") rb_dst[i] = rb_src[i];\n";
   }
   src << "extern \"C\" __global__ void __launch_bounds__(" << kBlockThreads << ") " << kPlaceholder << "("
       << params.str() << ") {\n" << body.str() << "}\n";

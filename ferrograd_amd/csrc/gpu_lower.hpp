@@ -74,7 +74,11 @@ KernelClass base_class(const UOp& kernel);
 // One launch for a run of block kernels (KernelClass::Block) that a replayed
 // sequence launches back to back: their bodies, in order, separated by
 // workgroup barriers, taking every stage's arguments concatenated in stage
-// order. Each stage computes exactly what its own kernel computes.
-RenderedKernel render_block_batch(const std::vector<const RenderedKernel*>& stages);
+// order. Each stage computes exactly what its own kernel computes. With
+// `read_back` (one stage or more), three more arguments follow (rb_dst,
+// rb_src, rb_words) and a last stage, after a barrier, copies rb_words 32-bit
+// words from rb_src to rb_dst: the sequence's result read back by the launch
+// that computed it.
+RenderedKernel render_block_batch(const std::vector<const RenderedKernel*>& stages, bool read_back = false);
 
 }  // namespace fg

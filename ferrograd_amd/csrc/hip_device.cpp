@@ -254,6 +254,11 @@ class HipDevice : public Device {
       std::vector<std::pair<size_t, size_t>> groups;
       std::vector<std::shared_ptr<Program>> batches;
       std::vector<size_t> order;  // launch order of the programs (empty: as given)
+      // The sequence's last launch with the read-back as its last stage, when
+      // that launch is a block kernel or a batch of them: from program
+      // rb_first (in launch order) to the end.
+      std::shared_ptr<Program> rb_batch;
+      size_t rb_first = 0;
       ~Replay() { fg_hip_graph_free(graph); }
     };
     if (!state) state = std::make_shared<Replay>();
@@ -278,6 +283,38 @@ class HipDevice : public Device {
     }
     auto prog_at = [&](size_t i) -> Program* { return r->order.empty() ? progs[i] : progs[r->order[i]]; };
     auto args_at = [&](size_t i) -> std::vector<KernelArg>& { return r->order.empty() ? args[i] : args[r->order[i]]; };
+    if (rb && gpu_passes().batch && !r->rb_batch && !progs.empty()) {
+      size_t first = progs.size(), count = 0;
+      if (!r->groups.empty() && r->groups.back().first + r->groups.back().second == progs.size()) {
+        first = r->groups.back().first;
+        count = r->groups.back().second;
+      } else if (is_block_program(*prog_at(progs.size() - 1))) {
+        first = progs.size() - 1;
+        count = 1;
+      }
+      if (count) {
+        std::vector<const RenderedKernel*> stages;
+        size_t total = 3;
+        for (size_t j = first; j < first + count; j++) {
+          stages.push_back(&prog_at(j)->meta);
+          total += args_at(j).size();
+        }
+        r->rb_batch = compile(render_block_batch(stages, true), total);
+        r->rb_first = first;
+      }
+    }
+    const bool fold_rb = rb && r->rb_batch;
+    auto rb_args = [&]() {
+      std::vector<fg_arg> a(3);
+      std::memset(a.data(), 0, a.size() * sizeof(fg_arg));
+      a[0].kind = FG_ARG_PTR;
+      a[0].v.p = rb->dst;
+      a[1].kind = FG_ARG_PTR;
+      a[1].v.p = const_cast<void*>(rb->src);
+      a[2].kind = FG_ARG_I32;
+      a[2].v.i = rb->words;
+      return a;
+    };
     std::vector<fg_prog*> lp;
     std::vector<unsigned> grids, blocks, lds;
     std::vector<int> nargs;
@@ -292,6 +329,18 @@ class HipDevice : public Device {
     };
     size_t next_group = 0;
     for (size_t i = 0; i < progs.size(); i++) {
+      if (fold_rb && i == r->rb_first) {
+        std::vector<fg_arg> a;
+        for (size_t j = i; j < progs.size(); j++) {
+          std::vector<fg_arg> aj = marshal(static_cast<HipProgram&>(*prog_at(j)), args_at(j));
+          a.insert(a.end(), aj.begin(), aj.end());
+        }
+        std::vector<fg_arg> ra = rb_args();
+        a.insert(a.end(), ra.begin(), ra.end());
+        auto& bp = static_cast<HipProgram&>(*r->rb_batch);
+        add(bp.prog, bp.meta.grid, bp.meta.block, bp.meta.lds_bytes, a);
+        break;
+      }
       if (next_group < r->groups.size() && r->groups[next_group].first == i) {
         const size_t n = r->groups[next_group].second;
         std::vector<fg_arg> a;
@@ -311,17 +360,9 @@ class HipDevice : public Device {
       for (size_t k = 0; k < p.passes.size(); k++)
         add(p.passes[k], p.meta.launches[k].grid, p.meta.launches[k].block, p.meta.launches[k].lds_bytes, a);
     }
-    if (rb) {
+    if (rb && !fold_rb) {
       HipProgram& p = readback_program();
-      std::vector<fg_arg> a(3);
-      std::memset(a.data(), 0, a.size() * sizeof(fg_arg));
-      a[0].kind = FG_ARG_PTR;
-      a[0].v.p = rb->dst;
-      a[1].kind = FG_ARG_PTR;
-      a[1].v.p = const_cast<void*>(rb->src);
-      a[2].kind = FG_ARG_I32;
-      a[2].v.i = rb->words;
-      add(p.prog, p.meta.grid, p.meta.block, 0, a);
+      add(p.prog, p.meta.grid, p.meta.block, 0, rb_args());
     }
     if (graphs_enabled() && !r->failed && !r->graph && r->uses >= 2 &&
         lp.size() >= static_cast<size_t>(graph_min_launches())) {
@@ -347,6 +388,13 @@ class HipDevice : public Device {
     }
   }
 
+  // A block kernel: one workgroup, a single launch, no scratch; its body can
+  // run as a stage of a batch.
+  static bool is_block_program(Program& prog) {
+    auto& p = static_cast<HipProgram&>(prog);
+    return !p.meta.stage_fn.empty() && p.passes.empty() && !p.scratch;
+  }
+
   // A launch order in which block kernels sit next to each other where the
   // data allow: a block kernel moves later, past kernels it shares no buffer
   // with (neither reads what the other writes, nor both write one buffer),
@@ -356,10 +404,7 @@ class HipDevice : public Device {
   // are the same buffer in every later call too. Empty when nothing moves.
   std::vector<size_t> sink_blocks(const std::vector<Program*>& progs, std::vector<std::vector<KernelArg>>& args) {
     const size_t n = progs.size();
-    auto is_block = [&](size_t i) {
-      auto& p = static_cast<HipProgram&>(*progs[i]);
-      return !p.meta.stage_fn.empty() && p.passes.empty() && !p.scratch;
-    };
+    auto is_block = [&](size_t i) { return is_block_program(*progs[i]); };
     std::vector<std::set<void*>> reads(n), writes(n);
     for (size_t i = 0; i < n; i++) {
       const RenderedKernel& m = progs[i]->meta;
@@ -405,10 +450,7 @@ class HipDevice : public Device {
   void group_blocks(const std::vector<Program*>& progs, std::vector<std::vector<KernelArg>>& args,
                     std::vector<std::pair<size_t, size_t>>& groups, std::vector<std::shared_ptr<Program>>& batches) {
     constexpr size_t kMaxBatch = 16;
-    auto is_block = [&](size_t i) {
-      auto& p = static_cast<HipProgram&>(*progs[i]);
-      return !p.meta.stage_fn.empty() && p.passes.empty() && !p.scratch;
-    };
+    auto is_block = [&](size_t i) { return is_block_program(*progs[i]); };
     for (size_t i = 0; i < progs.size();) {
       if (!is_block(i)) {
         i++;

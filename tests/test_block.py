@@ -110,7 +110,8 @@ def test_block_kernels_match_the_oracle(fg, cpu, hip, name):
 
 
 # C4-sized train steps in a child process with the given OPT: losses and every
-# parameter, and the launches per step seen by the launch profiler.
+# parameter, the launches of one Python-driven step and of a native-loop step
+# seen by the launch profiler.
 STEPS_SCRIPT = r"""
 import json, sys
 import numpy as np
@@ -133,7 +134,22 @@ fg.synchronize()
 ctx.profile(False)
 launches = len(ctx.profile_read())
 losses += train_steps_native(model, opt, x, t, 6)
+def native_kernels(steps):
+    fg.synchronize()
+    ctx.profile_read()
+    ctx.profile(True)
+    out = train_steps_native(model, opt, x, t, steps)
+    fg.synchronize()
+    ctx.profile(False)
+    return out, [p["kernel"] for p in ctx.profile_read()]
+# A call's first steps launch outside the step capture; the difference of two
+# calls counts captured steps alone.
+l1, n1 = native_kernels(5)
+l5, n5 = native_kernels(9)
+losses += l1 + l5
+native = n1 + n5
 print(json.dumps({"passes": fg.gpu_passes(), "losses": losses, "launches": launches,
+                  "native_launches": (len(n5) - len(n1)) / 4, "native_readback_kernels": native.count("fg_readback"),
                   "params": [p.numpy().tolist() for p in model.parameters()]}))
 """
 
@@ -161,6 +177,10 @@ def test_batched_launches_give_the_same_bits_as_one_by_one(fg, hip):
     # gradient moved past dW2's (no shared buffer) to join b2's in another, and
     # the loss plan's four kernels one more: 7 launches fewer.
     assert batched["launches"] <= single["launches"] - 7, (batched["launches"], single["launches"])
+    # In the native loop the loss read-back is the last stage of the step's
+    # last batch, not a kernel of its own.
+    assert batched["native_readback_kernels"] == 0 and single["native_readback_kernels"] > 0
+    assert batched["native_launches"] <= 10, batched["native_launches"]
 
 
 def test_reference_partition_small_kernels_compile_as_blocks(fg, cpu):
