@@ -1969,12 +1969,13 @@ RenderedKernel render_block(const KernelInfo& ki, KernelClass base, const std::s
 // MFMA tile is mostly padding. Two layouts, by which way the wide operand is
 // contiguous:
 // - rows: the wide operand is contiguous along k (out[w, n] = sum_k
-//   W[w, k] N[n, k], the forward x·Wᵀ). Each wave owns RW wide rows; its
-//   lanes stride k by four floats, so every load is a coalesced 16-byte load
-//   that streams the row once. The narrow operand's float4 at (n, k) serves
-//   all RW rows. Each accumulator is then summed across the wave by a fixed
-//   DPP/swizzle tree, and the totals go through LDS to the lanes that run the
-//   epilogue.
+//   W[w, k] N[n, k], the forward x·Wᵀ). The lanes of a workgroup stride k by
+//   four floats, so every load is a coalesced 16-byte load that streams a row
+//   once. The narrow operand's float4 at (n, k) is held in registers for the
+//   whole launch when it fits (render_narrow_rows_cached), else loaded once
+//   per group of 4 rows. Each accumulator is then summed across the wave by a
+//   fixed DPP/swizzle tree, and the totals go through LDS to the lanes that
+//   run the epilogue.
 // - cols: the wide operand is contiguous along the wide output (out[n, w] =
 //   sum_k N[k, n] W[k, w], the weight gradient dZᵀ·H). Lanes own V
 //   consecutive wide outputs and loop over k, where the narrow values are the
