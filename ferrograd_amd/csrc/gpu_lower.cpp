@@ -2031,8 +2031,11 @@ constexpr int kNarrowRowDepth = 2;
 bool narrow_rows_cached_fits(const NarrowPlan& np) {
   const int64_t JT = (np.K + 1023) / 1024;
   const int64_t nloads = static_cast<int64_t>(loads_in(np.wide.expr).size());
+  // The workgroup's sums stay in LDS until its last row: 4 x R x NN floats,
+  // at most 64 KB.
+  const int64_t rows = (np.W + kNarrowRowGroups - 1) / kNarrowRowGroups;
   // About 200 VGPRs in all keeps two waves per SIMD.
-  return np.NN * JT * 4 <= 160 && kNarrowRowDepth * nloads * JT * 4 <= 64;
+  return np.NN * JT * 4 <= 160 && kNarrowRowDepth * nloads * JT * 4 <= 64 && rows * np.NN <= 4096;
 }
 
 RenderedKernel render_narrow_rows_cached(const KernelInfo& ki, const GemmMatch& g, const NarrowPlan& np,

@@ -168,10 +168,12 @@ def test_narrow_products_lower_to_the_narrow_class(fg, cpu, m, n, k, layout):
 
 
 @pytest.mark.parametrize("m,n,k,cached", [(8192, 10, 4096, True), (1500, 10, 2000, True), (1537, 16, 1500, True),
-                                           (300, 10, 4096, True), (602, 12, 4000, False), (4096, 10, 8192, False)])
+                                           (300, 10, 4096, True), (602, 12, 4000, False), (4096, 10, 8192, False),
+                                           (140000, 16, 64, False)])
 def test_narrow_rows_hold_the_narrow_operand_in_registers_when_it_fits(fg, cpu, m, n, k, cached):
     # N x ceil(K/1024) x 4 floats of the narrow operand per thread: at most
-    # 160 (two waves per SIMD), else the row-group layout that re-reads it.
+    # 160 (two waves per SIMD), and the workgroup's sums (4 x rows x N) within
+    # 64 KB of LDS; else the row-group layout that re-reads it.
     x = fg.Tensor.new(np.ones((m, k), np.float32), [m, k], cpu)
     w = fg.Tensor.new(np.ones((n, k), np.float32), [n, k], cpu)
     (it,) = fg.debug_plan([x.matmul(w.permute([1, 0]))], fuse=True, render_hip=True)["items"]
