@@ -184,6 +184,18 @@ def test_narrow_rows_hold_the_narrow_operand_in_registers_when_it_fits(fg, cpu, 
         assert it["grid"] == [-(-m // rows), 1, 1] and it["block"] == [256, 1, 1]
 
 
+def test_narrow_rows_ring_holds_each_load_of_a_fused_operand(fg, cpu):
+    # relu(a*b)·Wᵀ: two loads per wide element, each with its own ring buffers
+    # (w<buffer>_<load>_<k block>), evaluated when the row is folded.
+    a = fg.Tensor.new(np.ones((4096, 2048), np.float32), [4096, 2048], cpu)
+    b = fg.Tensor.new(np.ones((4096, 2048), np.float32), [4096, 2048], cpu)
+    w = fg.Tensor.new(np.ones((10, 2048), np.float32), [10, 2048], cpu)
+    (it,) = fg.debug_plan([a.mul(b).relu().matmul(w.permute([1, 0]))], fuse=True, render_hip=True)["items"]
+    src = it["source"]
+    assert it["class"] == "gemm_narrow_f32" and "nb0_0[" in src
+    assert all(f"w{d}_{i}_{j}[4]" in src for d in (0, 1) for i in (0, 1) for j in (0, 1))
+
+
 def test_narrow_weight_gradient_lowers_to_split_cols(fg, cpu):
     g = fg.Tensor.new(np.ones((8192, 10), np.float32), [8192, 10], cpu)
     h = fg.Tensor.new(np.ones((8192, 4096), np.float32), [8192, 4096], cpu)

@@ -342,6 +342,27 @@ def test_narrow_forward_rows(fg, cpu, m, n, k):
     assert rel_err_bound(got, x64 @ w64.T + b, scale, 1e-4) <= 1.0
 
 
+@pytest.mark.parametrize("m,k", [(4096, 2048), (1537, 1500)])
+def test_narrow_rows_with_a_fused_two_input_operand(fg, cpu, m, k):
+    # relu(a*b)·Wᵀ: the elementwise producer is recomputed inside the narrow
+    # kernel, so its register ring holds the raw loads of both inputs.
+    r = seeded(31)
+    a = r.standard_normal((m, k)).astype(np.float32)
+    b = r.standard_normal((m, k)).astype(np.float32)
+    w = r.uniform(-1 / 32, 1 / 32, (10, k)).astype(np.float32)
+
+    def run(dev):
+        ta, tb = fg.Tensor.new(a, [m, k], dev), fg.Tensor.new(b, [m, k], dev)
+        tw = fg.Tensor.new(w, [10, k], dev)
+        return ta.mul(tb).relu().matmul(tw.permute([1, 0])).numpy().reshape(m, 10)
+
+    want, got = both(run, cpu)
+    h64 = np.maximum(a * b, np.float32(0)).astype(np.float64)
+    scale = np.abs(h64) @ np.abs(w.astype(np.float64)).T
+    assert rel_err_bound(got, want, scale, 1e-4) <= 1.0
+    assert rel_err_bound(got, h64 @ w.astype(np.float64).T, scale, 1e-4) <= 1.0
+
+
 @pytest.mark.parametrize("bsz,nn,w", [(8192, 10, 4096), (256, 10, 1000), (4096, 16, 258), (1000, 1, 4099),
                                       (64, 10, 512)])
 def test_narrow_weight_gradient_cols_with_sgd(fg, cpu, bsz, nn, w):
