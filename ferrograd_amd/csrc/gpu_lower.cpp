@@ -1153,6 +1153,7 @@ struct GemmTile {
   int BM = 256, BN = 256, BK = 32, WGM = 2, WGN = 2;
   int64_t S = 1;   // K splits (partials summed by a second pass)
   int64_t KC = 0;  // K per split, a multiple of BK
+  int nbuf = 2;    // LDS operand stages (3: the next stage's first fragments are read before the barrier)
   int nt() const { return 64 * WGM * WGN; }
   int tm() const { return BM / WGM / 32; }
   int tn() const { return BN / WGN / 32; }
@@ -1167,7 +1168,7 @@ constexpr int64_t kMinSplitK = 64;      // shortest K range a split workgroup ru
 // accumulators (16 VGPRs per 32x32 tile, about 128 more for staging and
 // addresses, 512 per SIMD lane).
 int64_t gemm_tile_residency(const GemmTile& t) {
-  const int64_t lds = 2 * 4 * static_cast<int64_t>(t.BM + t.BN + 8) * (t.BK + 4);
+  const int64_t lds = t.nbuf * 4 * static_cast<int64_t>(t.BM + t.BN + 8) * (t.BK + 4);
   const int64_t waves_per_simd = std::max<int64_t>(1, 512 / (16 * t.tm() * t.tn() + 128));
   const int64_t by_waves = std::max<int64_t>(1, waves_per_simd * 4 / (t.WGM * t.WGN));
   return std::max<int64_t>(1, std::min(kLdsPerCu / lds, by_waves));
@@ -1191,7 +1192,8 @@ int64_t gemm_tile_residency(const GemmTile& t) {
 //   operands. 64x64 tiles put many workgroups' loads and stores in flight:
 //   8192x4096 with K 10 took 91 us with 256x256 tiles, 54 with 128x128, 50 with
 //   64x64.
-// FG_GEMM_TILE="BM,BN,BK,WGM,WGN,S" fixes the tile and split count of every
+// FG_GEMM_TILE="BM,BN,BK,WGM,WGN,S[,NBUF]" fixes the tile, split count (and
+// LDS stage count, 2 or 3) of every
 // GEMM in the process: a tuning override for measuring alternatives to the
 // choice below on one box. Read once; a malformed value fails.
 bool gemm_tile_override(GemmTile* t) {
@@ -1206,12 +1208,13 @@ bool gemm_tile_override(GemmTile* t) {
       std::string f = s.substr(p, q == std::string::npos ? std::string::npos : q - p);
       char* end = nullptr;
       long long x = std::strtoll(f.c_str(), &end, 10);
-      FG_CHECK(!f.empty() && *end == '\0' && x > 0, "FG_GEMM_TILE must be BM,BN,BK,WGM,WGN,S; got '" + s + "'");
+      FG_CHECK(!f.empty() && *end == '\0' && x > 0, "FG_GEMM_TILE must be BM,BN,BK,WGM,WGN,S[,NBUF]; got '" + s + "'");
       out.push_back(x);
       if (q == std::string::npos) break;
       p = q + 1;
     }
-    FG_CHECK(out.size() == 6, "FG_GEMM_TILE must be BM,BN,BK,WGM,WGN,S; got '" + s + "'");
+    FG_CHECK(out.size() == 6 || (out.size() == 7 && (out[6] == 2 || out[6] == 3)),
+             "FG_GEMM_TILE must be BM,BN,BK,WGM,WGN,S[,NBUF]; got '" + s + "'");
     return out;
   }();
   if (v.empty()) return false;
@@ -1221,6 +1224,7 @@ bool gemm_tile_override(GemmTile* t) {
   t->WGM = static_cast<int>(v[3]);
   t->WGN = static_cast<int>(v[4]);
   t->S = v[5];
+  if (v.size() == 7) t->nbuf = static_cast<int>(v[6]);
   return true;
 }
 
@@ -1277,6 +1281,17 @@ GemmTile choose_gemm_tile(int64_t M, int64_t N, int64_t K) {
         best = t;
       }
     }
+  }
+  // A 16-wide k-tile runs with three LDS stages where they fit without costing
+  // a resident workgroup: its k-tiles are half as long, so the read of the next
+  // stage's first fragments after each barrier weighed twice as much. Measured
+  // on the 8192x4096 forward with K 784: 455-462 us against 463-464 us with two
+  // stages; 4096^3 with BK 16: 1054 against 1071 us (BK 32, two stages: 1034).
+  if (best.BK == 16) {
+    GemmTile t3 = best;
+    t3.nbuf = 3;
+    const int64_t lds3 = 3 * 4 * static_cast<int64_t>(t3.BM + t3.BN + 8) * (t3.BK + 4);
+    if (lds3 <= kLdsPerCu && gemm_tile_residency(t3) == gemm_tile_residency(best)) best = t3;
   }
   return best;
 }
@@ -1347,6 +1362,80 @@ __device__ __forceinline__ void fg_sched_k_tile() {
 }
 )";
 
+// The k loop with three LDS operand stages instead of two: the stage after
+// next is written while a stage is computed, so the next stage was complete
+// at the previous barrier and its first fragments are read during the last
+// group's MFMAs, before the barrier, instead of after it. One barrier per
+// k-tile still orders every write after the reads of the stage it replaces
+// (read during the k-tile before the last barrier) and before its own reads
+// (after the next barrier). Needs an even number of 8-k groups per k-tile, so
+// the fragment registers of the next k-tile's first group are free.
+std::string gemm_three_stages(std::string src) {
+  auto swap_once = [&](const std::string& from, const std::string& to) {
+    const size_t p = src.find(from);
+    FG_CHECK(p != std::string::npos && src.find(from, p + 1) == std::string::npos,
+             "three-stage GEMM: generated text not found once");
+    src.replace(p, from.size(), to);
+  };
+  swap_once("  // Operand stages, double-buffered, rows padded by 4 floats;",
+            "  // Operand stages, three of them, rows padded by 4 floats;");
+  swap_once("constexpr int SA = 2 * SA_R * SA_C, SB = 2 * SB_R * SB_C,",
+            "constexpr int SA = 3 * SA_R * SA_C, SB = 3 * SB_R * SB_C,");
+  swap_once("__device__ __forceinline__ void fg_sched_k_tile() {\n"
+            "  constexpr int nv = g == 0 ? NV : 0, nd = g + 1 < G ? ND : 0, nw = g == G - 1 ? NW : 0;",
+            "__device__ __forceinline__ void fg_sched_k_tile() {\n"
+            "  constexpr int nv = g == 0 ? NV : 0, nd = ND, nw = g == G - 1 ? NW : 0;");
+  swap_once(R"(  load_a(kbeg); load_b(kbeg);
+  store_a(0, kbeg); store_b(0, kbeg);
+  __syncthreads();
+  frag(0, 0, fa[0], fb[0]);
+  for (int kt = 0; kt < KT; kt++) {
+    const int cur = kt & 1;
+    // The last k-tile reloads itself, so the body is the same every time.
+    const int knext = kbeg + (kt + 1 < KT ? kt + 1 : kt) * BK;
+    load_a(knext); load_b(knext);
+    #pragma unroll
+    for (int g = 0; g < BK / 8; g++) {
+      if (g + 1 < BK / 8) frag(cur, g + 1, fa[(g + 1) & 1], fb[(g + 1) & 1]);
+)",
+            R"(  static_assert((BK / 8) % 2 == 0, "three stages need an even number of 8-k groups");
+  load_a(kbeg); load_b(kbeg);
+  store_a(0, kbeg); store_b(0, kbeg);
+  {
+    const int k1 = kbeg + (1 < KT ? 1 : 0) * BK;
+    load_a(k1); load_b(k1);
+    store_a(1, k1); store_b(1, k1);
+  }
+  __syncthreads();
+  frag(0, 0, fa[0], fb[0]);
+  int cur = 0;
+  for (int kt = 0; kt < KT; kt++) {
+    const int nxt = cur == 2 ? 0 : cur + 1, nn = nxt == 2 ? 0 : nxt + 1;
+    // The last k-tiles reload the last one, so the body is the same every time.
+    const int knext = kbeg + (kt + 2 < KT ? kt + 2 : KT - 1) * BK;
+    load_a(knext); load_b(knext);
+    #pragma unroll
+    for (int g = 0; g < BK / 8; g++) {
+      if (g + 1 < BK / 8) frag(cur, g + 1, fa[(g + 1) & 1], fb[(g + 1) & 1]);
+      else frag(nxt, 0, fa[0], fb[0]);
+)");
+  swap_once(R"(      if (g == BK / 8 - 1) { store_a(cur ^ 1, knext); store_b(cur ^ 1, knext); }
+    }
+    fg_sched_k_tile<BK / 8, 0, NV_, ND_, NW_, 4 * TM * TN>();
+    __syncthreads();
+    frag(cur ^ 1, 0, fa[0], fb[0]);
+  }
+)",
+            R"(      if (g == BK / 8 - 1) { store_a(nn, knext); store_b(nn, knext); }
+    }
+    fg_sched_k_tile<BK / 8, 0, NV_, ND_, NW_, 4 * TM * TN>();
+    __syncthreads();
+    cur = nxt;
+  }
+)");
+  return src;
+}
+
 RenderedKernel render_gemm(const KernelInfo& ki, const GemmMatch& g, const std::string& name) {
   const int64_t M = g.M, N = g.N, K = g.K;
   const GemmTile tile = choose_gemm_tile(M, N, K);
@@ -1356,6 +1445,7 @@ RenderedKernel render_gemm(const KernelInfo& ki, const GemmMatch& g, const std::
   const int64_t ntiles = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
   FG_CHECK(BM % (32 * WGM) == 0 && BN % (32 * WGN) == 0 && BK % 8 == 0, "gemm tile shape does not fit the wave grid");
   FG_CHECK((TM == 1 || TM == 2 || TM == 4) && (TN == 1 || TN == 2 || TN == 4), "gemm wave tile must be 32, 64 or 128 wide");
+  FG_CHECK(tile.nbuf == 2 || (tile.nbuf == 3 && (BK / 8) % 2 == 0), "three GEMM stages need an even number of 8-k groups");
   const std::string scratch_param = S > 1 ? ", float* __restrict__ fg_scratch" : "";
   const int waves_per_eu = static_cast<int>(std::max<int64_t>(1, gemm_tile_residency(tile) * NT / 256));
   auto sig = [&](const std::string& fn, int block, bool main) {
@@ -1727,6 +1817,7 @@ RenderedKernel render_gemm(const KernelInfo& ki, const GemmMatch& g, const std::
   rk.name = name;
   rk.kind = kernel_class_name(KernelClass::Gemm);
   rk.source = s.str();
+  if (tile.nbuf == 3) rk.source = gemm_three_stages(rk.source);
   rk.block[0] = static_cast<unsigned>(NT);
   rk.grid[0] = static_cast<unsigned>(ntiles * S);
   if (S > 1) {
