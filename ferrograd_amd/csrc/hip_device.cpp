@@ -200,10 +200,12 @@ class HipDevice : public Device {
     run_sequence(progs, args, state, nullptr);
   }
 
-  // The read-back of `result` as the sequence's last kernel, storing straight
-  // into the pinned slot: the captured train step then reads its loss with
-  // no separate copy behind its graph (that copy and the gap before it were
-  // about 12 us of a 55 us C4 step under the profiler).
+  // The read-back of `result` as part of the sequence, storing straight into
+  // the pinned slot: the captured train step then reads its loss with no
+  // separate copy behind its graph (that copy and the gap before it were
+  // about 12 us of a 55 us C4 step under the profiler). When the sequence
+  // ends in a block kernel or a batch of them, the copy is that launch's last
+  // stage; otherwise it is one more kernel.
   void execute_sequence_read(const std::vector<Program*>& progs, std::vector<std::vector<KernelArg>>& args,
                              std::shared_ptr<void>& state, const Buffer& result, int slot) override {
     const size_t nb = result->nbytes();
