@@ -1159,6 +1159,24 @@ struct GemmTile {
   int tn() const { return BN / WGN / 32; }
 };
 
+// A [k][row] operand stage interleaves the rows of a wave's T MFMA tiles so
+// one LDS read gives a lane its operand of several tiles. The tiles are cut
+// into chunks of 4, 2 or 1 (16-, 8- or 4-byte reads); in the chunk of s tiles
+// that starts at tile f, row r of tile f + i sits at wave-block row
+// 32f + s*r + i. T = 5 (a 160-wide wave block) is a chunk of 4 and one of 1.
+struct KmChunk {
+  int first, size;
+};
+std::vector<KmChunk> km_chunks(int T) {
+  std::vector<KmChunk> out;
+  for (int f = 0; f < T;) {
+    const int rest = T - f, sz = rest >= 4 ? 4 : rest >= 2 ? 2 : 1;
+    out.push_back({f, sz});
+    f += sz;
+  }
+  return out;
+}
+
 constexpr int64_t kComputeUnits = 256;  // MI355X
 constexpr int64_t kLdsPerCu = 163840;   // gfx950 LDS bytes per CU
 constexpr int64_t kMinSplitK = 64;      // shortest K range a split workgroup runs
@@ -1262,10 +1280,16 @@ GemmTile choose_gemm_tile(int64_t M, int64_t N, int64_t K) {
   // Each shape with BK 32 and BK 16. BK 16 pads a K that is not a multiple of
   // 32 less: the 8192x4096 forward with K 784 (49 k-tiles of 16) took 399 us
   // against 424 us with BK 32; for K 4096 BK 32 was about 2% faster.
+  // 256x160 (four waves of 64x160 stacked along M, five 32-wide MFMA columns
+  // each) pads a 784-wide side to 800 columns instead of 1024. C5's dW1
+  // (4096x784, K 8192), timed alone: 472 us with 3 splits (240 workgroups)
+  // against 526 us as 256x256 with 4; with BK 16 (two or three stages) 548 us.
   const Cand cands[] = {{{256, 256, 32, 2, 2}, 1.0},   {{256, 256, 16, 2, 2}, 0.99}, {{256, 128, 32, 2, 2}, 0.9},
                         {{256, 128, 16, 2, 2}, 0.89},  {{128, 256, 32, 2, 2}, 0.9},  {{128, 256, 16, 2, 2}, 0.89},
-                        {{128, 128, 32, 2, 2}, 0.92},  {{128, 128, 16, 2, 2}, 0.91}, {{64, 64, 32, 2, 2}, 0.6}};
-  GemmTile best = with_splits(cands[8].t, 1);
+                        {{128, 128, 32, 2, 2}, 0.92},  {{128, 128, 16, 2, 2}, 0.91}, {{64, 64, 32, 2, 2}, 0.6},
+                        {{256, 160, 32, 4, 1}, 0.97},  {{256, 160, 16, 4, 1}, 0.84}, {{160, 256, 32, 1, 4}, 0.97},
+                        {{160, 256, 16, 1, 4}, 0.84}};
+  GemmTile best = with_splits(GemmTile{64, 64, 32, 2, 2}, 1);
   double best_s = 1e30;
   for (const Cand& c : cands) {
     if (M < c.t.BM / 2 || N < c.t.BN / 2) continue;  // mostly padding
@@ -1444,7 +1468,7 @@ RenderedKernel render_gemm(const KernelInfo& ki, const GemmMatch& g, const std::
   const int64_t S = tile.S, KC = tile.KC, NP = (N + 3) / 4 * 4;
   const int64_t ntiles = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
   FG_CHECK(BM % (32 * WGM) == 0 && BN % (32 * WGN) == 0 && BK % 8 == 0, "gemm tile shape does not fit the wave grid");
-  FG_CHECK((TM == 1 || TM == 2 || TM == 4) && (TN == 1 || TN == 2 || TN == 4), "gemm wave tile must be 32, 64 or 128 wide");
+  FG_CHECK(TM >= 1 && TM <= 5 && TN >= 1 && TN <= 5, "gemm wave tile must be 32 to 160 wide");
   FG_CHECK(tile.nbuf == 2 || (tile.nbuf == 3 && (BK / 8) % 2 == 0), "three GEMM stages need an even number of 8-k groups");
   const std::string scratch_param = S > 1 ? ", float* __restrict__ fg_scratch" : "";
   const int waves_per_eu = static_cast<int>(std::max<int64_t>(1, gemm_tile_residency(tile) * NT / 256));
@@ -1488,7 +1512,8 @@ RenderedKernel render_gemm(const KernelInfo& ki, const GemmMatch& g, const std::
   };
   const Stage sa = plan(g.a, BM, M), sb = plan(g.b, BN, N);
   const int NV = sa.per * static_cast<int>(sa.lds.size()) + sb.per * static_cast<int>(sb.lds.size());
-  const int ND = (sa.km ? 4 : TM) + (sb.km ? 4 : TN);
+  const int ND = (sa.km ? 4 * static_cast<int>(km_chunks(TM).size()) : TM) +
+                 (sb.km ? 4 * static_cast<int>(km_chunks(TN).size()) : TN);
   const int NW = sa.per + sb.per;
 
   std::ostringstream s;
@@ -1644,17 +1669,48 @@ RenderedKernel render_gemm(const KernelInfo& ki, const GemmMatch& g, const std::
   };
   s << loader("a", g.a, sa, BM, M, "m");
   s << loader("b", g.b, sb, BN, N, "n");
+  // [k][row] stages: one LDS read of each chunk's interleaved rows per MFMA step.
+  auto km_frag = [&](const char* S, const char* w, const char* fr, int T) {
+    std::ostringstream f;
+    f << "    #pragma unroll\n    for (int t = 0; t < 4; t++) {\n";
+    for (const KmChunk& c : km_chunks(T)) {
+      f << "      {\n        const typename fg_vt<" << c.size << ">::t v = *(const typename fg_vt<" << c.size
+        << ">::t*)&" << S << "[buf][8 * g + 4 * h + t][" << w << " + " << 32 * c.first << " + " << c.size
+        << " * r32];\n";
+      f << "        #pragma unroll\n        for (int i = 0; i < " << c.size << "; i++) " << fr << "[" << c.first
+        << " + i][t] = ((const float*)&v)[i];\n      }\n";
+    }
+    f << "    }\n";
+    return f.str();
+  };
+  // Wave-block position of row r of tile i in a [k][row] stage.
+  auto km_pos = [&](int T, const std::string& i, const std::string& r) {
+    std::string e = "0";
+    const auto ch = km_chunks(T);
+    for (size_t c = ch.size(); c-- > 0;) {
+      const std::string here = std::to_string(32 * ch[c].first) + " + " + std::to_string(ch[c].size) + " * " + r +
+                               " + (" + i + " - " + std::to_string(ch[c].first) + ")";
+      e = c + 1 == ch.size() ? here : "(" + i + " < " + std::to_string(ch[c].first + ch[c].size) + " ? " + here + " : " + e + ")";
+    }
+    return e;
+  };
+  // Epilogue staging of a [k][row] B operand's columns: one LDS write per chunk.
+  auto km_stage = [&]() {
+    std::ostringstream f;
+    for (const KmChunk& c : km_chunks(TN)) {
+      f << "      {\n        typename fg_vt<" << c.size << ">::t v;\n";
+      f << "        #pragma unroll\n        for (int j = 0; j < " << c.size << "; j++) ((float*)&v)[j] = acc[i]["
+        << c.first << " + j][e];\n";
+      f << "        *(typename fg_vt<" << c.size << ">::t*)(wst + rr * EPS + " << 32 * c.first << " + " << c.size
+        << " * r32) = v;\n      }\n";
+    }
+    return f.str();
+  };
   s << R"(  // K schedule: in group g (8 k), MFMA step t, lane half h uses k = 8g + 4h + t.
   float fa[2][TM][4], fb[2][TN][4];
   auto frag = [&](int buf, int g, float (&fra)[TM][4], float (&frb)[TN][4]) {
 #if A_KM
-    #pragma unroll
-    for (int t = 0; t < 4; t++) {
-      const typename fg_vt<TM>::t v = *(const typename fg_vt<TM>::t*)&As[buf][8 * g + 4 * h + t][wm + TM * r32];
-      #pragma unroll
-      for (int i = 0; i < TM; i++) fra[i][t] = ((const float*)&v)[i];
-    }
-#else
+)" << km_frag("As", "wm", "fra", TM) << R"(#else
     #pragma unroll
     for (int i = 0; i < TM; i++) {
       const fg_f4 v = *(const fg_f4*)&As[buf][wm + 32 * i + r32][8 * g + 4 * h];
@@ -1662,13 +1718,7 @@ RenderedKernel render_gemm(const KernelInfo& ki, const GemmMatch& g, const std::
     }
 #endif
 #if B_KM
-    #pragma unroll
-    for (int t = 0; t < 4; t++) {
-      const typename fg_vt<TN>::t v = *(const typename fg_vt<TN>::t*)&Bs[buf][8 * g + 4 * h + t][wn + TN * r32];
-      #pragma unroll
-      for (int j = 0; j < TN; j++) frb[j][t] = ((const float*)&v)[j];
-    }
-#else
+)" << km_frag("Bs", "wn", "frb", TN) << R"(#else
     #pragma unroll
     for (int j = 0; j < TN; j++) {
       const fg_f4 v = *(const fg_f4*)&Bs[buf][wn + 32 * j + r32][8 * g + 4 * h];
@@ -1715,11 +1765,7 @@ RenderedKernel render_gemm(const KernelInfo& ki, const GemmMatch& g, const std::
     for (int e = 0; e < 16; e++) {
       const int rr = 8 * (e >> 2) + 4 * h + (e & 3);
 #if B_KM
-      typename fg_vt<TN>::t v;
-      #pragma unroll
-      for (int j = 0; j < TN; j++) ((float*)&v)[j] = acc[i][j][e];
-      *(typename fg_vt<TN>::t*)(wst + rr * EPS + TN * r32) = v;
-#else
+)" << km_stage() << R"(#else
       #pragma unroll
       for (int j = 0; j < TN; j++) wst[rr * EPS + 32 * j + r32] = acc[i][j][e];
 #endif
@@ -1730,7 +1776,7 @@ RenderedKernel render_gemm(const KernelInfo& ki, const GemmMatch& g, const std::
       const int ch = lane + 64 * q, rr = ch / (WN / 4), cc = (ch % (WN / 4)) * 4;
       const fg_f4 gv = *(const fg_f4*)(wst + rr * EPS + cc);
 #if A_KM
-      const int grow = m0 + wm + TM * rr + i;
+      const int grow = m0 + wm + )" << km_pos(TM, "i", "rr") << R"(;
 #else
       const int grow = m0 + wm + 32 * i + rr;
 #endif

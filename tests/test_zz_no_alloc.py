@@ -82,7 +82,7 @@ def test_noalloc_refuses_a_kernel_beyond_its_scratch(fg, hip):
     from ferrograd_amd.hip import FG_NOALLOC_SCRATCH_BYTES, Arg, Context, HipError, Kernel
 
     ctx = Context.of_device()
-    r, text, g, h = dw_kernel(fg, 4096, 3072, 3072, 3)
+    r, text, g, h = dw_kernel(fg, 8192, 2560, 2560, 3)  # 4 K splits of a 2560x2560 output: 125 MiB
     assert r.scratch_bytes > FG_NOALLOC_SCRATCH_BYTES
     k = Kernel(ctx, r)
     p = ctx.alloc(4)
