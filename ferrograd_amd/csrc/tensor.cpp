@@ -1328,8 +1328,13 @@ std::vector<float> train_steps(const std::vector<const Linear*>& layers, const S
   FG_CHECK(steps >= 0, "train_steps: negative step count");
   std::vector<float> losses(static_cast<size_t>(steps));
   Device& dev = get_device(x.device());
+  // Step i's loss lands in read-back slot i % kInFlight and is waited for
+  // kInFlight - 1 steps later, so the host queues up to that many steps
+  // ahead of the device and a slow host wake-up does not leave it idle.
+  constexpr int kInFlight = 4;  // read-back slots in use (the HIP device has 8)
+  auto slot = [](int step) { return step % kInFlight; };
   auto collect = [&](int step) {
-    std::vector<uint8_t> b = dev.read_wait(step % 2);
+    std::vector<uint8_t> b = dev.read_wait(slot(step));
     FG_CHECK(b.size() == sizeof(float), "train_steps: the loss must be one f32");
     std::memcpy(&losses[static_cast<size_t>(step)], b.data(), sizeof(float));
   };
@@ -1343,9 +1348,9 @@ std::vector<float> train_steps(const std::vector<const Linear*>& layers, const S
   bool prev_valid = false;
   for (int i = 0; i < steps; i++) {
     if (cap && i + 1 < steps) {
-      replay_step(dev, *cap, i % 2);
+      replay_step(dev, *cap, slot(i));
       realize_stats().steps_replayed++;
-      if (i > 0) collect(i - 1);
+      if (i >= kInFlight - 1) collect(i - (kInFlight - 1));
       continue;
     }
     StepRecorder rec;
@@ -1361,16 +1366,16 @@ std::vector<float> train_steps(const std::vector<const Linear*>& layers, const S
       loss.backward();
       opt.step();
       Buffer lb = loss.realized_buffer();
-      dev.read_async(lb, i % 2);  // the loss's read-back, queued behind the step
+      dev.read_async(lb, slot(i));  // the loss's read-back, queued behind the step
       if (capture && !cap) {
         if (rec.valid && prev_valid && (cap = capture_step(prev, rec.records, lb))) realize_stats().steps_captured++;
         prev = cap ? std::vector<ReplayRecord>() : std::move(rec.records);
         prev_valid = !cap && rec.valid;
       }
     }
-    if (i > 0) collect(i - 1);
+    if (i >= kInFlight - 1) collect(i - (kInFlight - 1));
   }
-  if (steps > 0) collect(steps - 1);
+  for (int i = std::max(0, steps - (kInFlight - 1)); i < steps; i++) collect(i);
   return losses;
 }
 

@@ -40,8 +40,10 @@ def test_native_loop_matches_python_loop_cpu(fg, cpu, dims):
     assert l_nat == l_py and l_nat[-1] < l_nat[0]
     for a, b in zip(p_nat, p_py):
         assert np.array_equal(a, b)
-    l_ch, p_ch = run(fg, cpu, dims, 8, 9, native=True, chunks=[4, 1, 4])
-    assert l_ch == l_py and all(np.array_equal(a, b) for a, b in zip(p_ch, p_py))
+    # Calls shorter and longer than the loop's four steps in flight.
+    for chunks in ([4, 1, 4], [2, 3, 4], [6, 3]):
+        l_ch, p_ch = run(fg, cpu, dims, 8, 9, native=True, chunks=chunks)
+        assert l_ch == l_py and all(np.array_equal(a, b) for a, b in zip(p_ch, p_py)), chunks
 
 
 def test_step_capture_off_matches(fg, cpu):
@@ -87,6 +89,8 @@ def test_native_loop_matches_python_loop_hip(fg, cpu, batch, dims):
     assert l_nat == l_py
     for a, b in zip(p_nat, p_py):
         assert np.array_equal(a, b)
+    l_ch, p_ch = run(fg, "hip", dims, batch, 9, native=True, chunks=[2, 7])
+    assert l_ch == l_py and all(np.array_equal(a, b) for a, b in zip(p_ch, p_py))
     # The loop's steps are the recorded steps' kernels: each step of the
     # Python-driven loop, product by product against float64 on the device's
     # own values, and the oracle's losses within 1e-4.
