@@ -1151,9 +1151,14 @@ bool gemm_operand(const UOp& e, const UOp& rk, const KernelInfo& ki, GemmOperand
 // owns a (BM/WGM) x (BN/WGN) block of 32x32 MFMA tiles: TM x TN of them.
 struct GemmTile {
   int BM = 256, BN = 256, BK = 32, WGM = 2, WGN = 2;
-  int64_t S = 1;   // K splits (partials summed by a second pass)
+  int64_t S = 1;   // K splits (partials summed by a second pass); with stream_k, the most segments of a tile
   int64_t KC = 0;  // K per split, a multiple of BK
   int nbuf = 2;    // LDS operand stages (3: the next stage's first fragments are read before the barrier)
+  // Stream-K: G workgroups each run an equal share of the (tile, k-tile)
+  // iterations, crossing tile boundaries; each tile's segments are partials
+  // that the second pass sums in k order.
+  bool stream_k = false;
+  int64_t G = 0;
   int nt() const { return 64 * WGM * WGN; }
   int tm() const { return BM / WGM / 32; }
   int tn() const { return BN / WGN / 32; }
@@ -1210,10 +1215,22 @@ int64_t gemm_tile_residency(const GemmTile& t) {
 //   operands. 64x64 tiles put many workgroups' loads and stores in flight:
 //   8192x4096 with K 10 took 91 us with 256x256 tiles, 54 with 128x128, 50 with
 //   64x64.
-// FG_GEMM_TILE="BM,BN,BK,WGM,WGN,S[,NBUF]" fixes the tile, split count (and
-// LDS stage count, 2 or 3) of every
+// FG_GEMM_TILE="BM,BN,BK,WGM,WGN,S[,NBUF]" fixes the tile, split count (0:
+// stream-K over the chip's CUs) and LDS stage count (2 or 3) of every
 // GEMM in the process: a tuning override for measuring alternatives to the
 // choice below on one box. Read once; a malformed value fails.
+// Stream-K over `iters` (tile, k-tile) iterations, tile-major with `kt`
+// k-tiles per tile, on G workgroups: workgroup w runs [w*iters/G,
+// (w+1)*iters/G), so iteration x belongs to workgroup ((x+1)*G - 1)/iters.
+// The most segments (workgroups) any tile is split into.
+int64_t stream_k_segments(int64_t ntiles, int64_t kt, int64_t G) {
+  const int64_t iters = ntiles * kt;
+  auto owner = [&](int64_t x) { return ((x + 1) * G - 1) / iters; };
+  int64_t most = 1;
+  for (int64_t t = 0; t < ntiles; t++) most = std::max(most, owner(t * kt + kt - 1) - owner(t * kt) + 1);
+  return most;
+}
+
 bool gemm_tile_override(GemmTile* t) {
   static const std::vector<int64_t> v = [] {
     std::vector<int64_t> out;
@@ -1226,7 +1243,8 @@ bool gemm_tile_override(GemmTile* t) {
       std::string f = s.substr(p, q == std::string::npos ? std::string::npos : q - p);
       char* end = nullptr;
       long long x = std::strtoll(f.c_str(), &end, 10);
-      FG_CHECK(!f.empty() && *end == '\0' && x > 0, "FG_GEMM_TILE must be BM,BN,BK,WGM,WGN,S[,NBUF]; got '" + s + "'");
+      FG_CHECK(!f.empty() && *end == '\0' && (x > 0 || (x == 0 && out.size() == 5)),
+               "FG_GEMM_TILE must be BM,BN,BK,WGM,WGN,S[,NBUF] (S 0: stream-K); got '" + s + "'");
       out.push_back(x);
       if (q == std::string::npos) break;
       p = q + 1;
@@ -1254,8 +1272,28 @@ GemmTile choose_gemm_tile(int64_t M, int64_t N, int64_t K) {
     t.S = (K + t.KC - 1) / t.KC;
     return t;
   };
+  // Stream-K on every resident workgroup slot of the chip.
+  auto as_stream_k = [&](GemmTile t) {
+    const int64_t kt = (K + t.BK - 1) / t.BK;
+    t.stream_k = true;
+    t.G = kComputeUnits * gemm_tile_residency(t);
+    t.S = stream_k_segments(tiles(t), kt, t.G);
+    t.KC = t.BK;
+    return t;
+  };
+  // Worth it when every workgroup runs at least 4 k-tiles and the shares do
+  // not fall on whole tiles anyway.
+  auto stream_k_fits = [&](const GemmTile& t) {
+    const int64_t kt = (K + t.BK - 1) / t.BK, G = kComputeUnits * gemm_tile_residency(t), iters = tiles(t) * kt;
+    return iters >= 4 * G && !(iters % G == 0 && (iters / G) % kt == 0);
+  };
   GemmTile forced;
-  if (gemm_tile_override(&forced)) return with_splits(forced, forced.S);
+  if (gemm_tile_override(&forced)) {
+    if (forced.S != 0) return with_splits(forced, forced.S);
+    FG_CHECK(tiles(forced) * ((K + forced.BK - 1) / forced.BK) >= kComputeUnits * gemm_tile_residency(forced),
+             "FG_GEMM_TILE: stream-K needs at least one k-tile per workgroup");
+    return as_stream_k(forced);
+  }
   if (M <= 32 || N <= 32) {
     GemmTile t;
     auto side = [](int64_t ext, int* b, int* w) {
@@ -1301,6 +1339,18 @@ GemmTile choose_gemm_tile(int64_t M, int64_t N, int64_t K) {
       const double mfma = static_cast<double>(rounds * res) * 2.0 * t.BM * t.BN * t.KC / (kCuFlops * c.eff);
       const double partials = t.S > 1 ? static_cast<double>(t.S + 1) * M * N * 4.0 / kHbmBytes : 0.0;
       if (mfma + partials < best_s * 0.999) {
+        best_s = mfma + partials;
+        best = t;
+      }
+    }
+    if (stream_k_fits(c.t)) {
+      // Each workgroup's share of the k-tiles, plus one more epilogue when it
+      // crosses into a second tile, plus the segments' partials.
+      const GemmTile t = as_stream_k(c.t);
+      const int64_t kt = (K + t.BK - 1) / t.BK, share = (nt * kt + t.G - 1) / t.G;
+      const double mfma = static_cast<double>(share + 1) * res * 2.0 * t.BM * t.BN * t.BK / (kCuFlops * c.eff);
+      const double partials = static_cast<double>(t.S + 1) * M * N * 4.0 / kHbmBytes;
+      if (mfma + partials < best_s * 0.98) {
         best_s = mfma + partials;
         best = t;
       }
@@ -1460,6 +1510,45 @@ std::string gemm_three_stages(std::string src) {
   return src;
 }
 
+// The main pass as stream-K: instead of one (split, tile) pair per
+// workgroup, each of the G workgroups runs its share of the (tile, k-tile)
+// iterations as segments of consecutive k-tiles of one tile, computing and
+// storing each segment's partial sums as a split-K workgroup would. Shares
+// differ by at most one k-tile, so no CU is left without work when the tiles
+// do not divide into rounds.
+std::string gemm_stream_k(std::string src) {
+  const std::string from = R"(  int bid = blockIdx.x;
+  // Blocks are dispatched round-robin over the 8 XCDs; give each XCD a
+  // contiguous run of (split, tile) pairs so neighbouring tiles of one K
+  // range share its L2.
+  if ((NTILES_ * S_) % 8 == 0) bid = (bid % 8) * (NTILES_ * S_ / 8) + bid / 8;
+#if S_ > 1
+  const int ks = bid / NTILES_;
+  bid = bid % NTILES_;
+  const int kbeg = ks * KC_, kend = (kbeg + KC_ < K_) ? kbeg + KC_ : K_;
+#else
+  constexpr int kbeg = 0, kend = K_;
+#endif
+)";
+  const std::string to = R"(  // Consecutive shares (which share tiles) run on one XCD.
+  int wv = blockIdx.x;
+  if (G_ % 8 == 0) wv = (wv % 8) * (G_ / 8) + wv / 8;
+  const long it_end = (long)(wv + 1) * ITERS_ / G_;
+  for (long it = (long)wv * ITERS_ / G_; it < it_end;) {
+  int bid = (int)(it / KTT_);
+  const int kt0 = (int)(it % KTT_);
+  const int kt1 = (it_end - it < (long)(KTT_ - kt0)) ? kt0 + (int)(it_end - it) : KTT_;
+  it += kt1 - kt0;
+  const int ks = wv - fg_sk_owner((long)bid * KTT_);  // the segment's place in its tile, in k order
+  const int kbeg = kt0 * BK, kend = (kt1 * BK < K_) ? kt1 * BK : K_;
+)";
+  const size_t p = src.find(from);
+  FG_CHECK(p != std::string::npos && src.find(from, p + 1) == std::string::npos,
+           "stream-K GEMM: generated text not found once");
+  src.replace(p, from.size(), to);
+  return src;
+}
+
 RenderedKernel render_gemm(const KernelInfo& ki, const GemmMatch& g, const std::string& name) {
   const int64_t M = g.M, N = g.N, K = g.K;
   const GemmTile tile = choose_gemm_tile(M, N, K);
@@ -1470,7 +1559,9 @@ RenderedKernel render_gemm(const KernelInfo& ki, const GemmMatch& g, const std::
   FG_CHECK(BM % (32 * WGM) == 0 && BN % (32 * WGN) == 0 && BK % 8 == 0, "gemm tile shape does not fit the wave grid");
   FG_CHECK(TM >= 1 && TM <= 5 && TN >= 1 && TN <= 5, "gemm wave tile must be 32 to 160 wide");
   FG_CHECK(tile.nbuf == 2 || (tile.nbuf == 3 && (BK / 8) % 2 == 0), "three GEMM stages need an even number of 8-k groups");
-  const std::string scratch_param = S > 1 ? ", float* __restrict__ fg_scratch" : "";
+  const bool split = S > 1 || tile.stream_k;  // partials in scratch, summed by _fin
+  const int64_t KTT = (K + BK - 1) / BK;       // k-tiles per tile
+  const std::string scratch_param = split ? ", float* __restrict__ fg_scratch" : "";
   const int waves_per_eu = static_cast<int>(std::max<int64_t>(1, gemm_tile_residency(tile) * NT / 256));
   auto sig = [&](const std::string& fn, int block, bool main) {
     std::string s = signature(ki, fn, block);
@@ -1482,7 +1573,7 @@ RenderedKernel render_gemm(const KernelInfo& ki, const GemmMatch& g, const std::
     }
     return s;
   };
-  const std::string main_name = S > 1 ? name + "_part" : name;
+  const std::string main_name = split ? name + "_part" : name;
 
   // How each operand reaches LDS. Mode 0: 4 consecutive k per thread (unit
   // stride along k: 16-byte loads), staged [row][k]. Mode 1: 4 consecutive rows
@@ -1524,6 +1615,11 @@ RenderedKernel render_gemm(const KernelInfo& ki, const GemmMatch& g, const std::
   s << "#define NT " << NT << "\n#define WGN " << WGN << "\n#define TM " << TM << "\n#define TN " << TN << "\n";
   s << "#define A_KM " << (sa.km ? 1 : 0) << "\n#define B_KM " << (sb.km ? 1 : 0) << "\n";
   s << "#define NV_ " << NV << "\n#define ND_ " << ND << "\n#define NW_ " << NW << "\n";
+  if (tile.stream_k) {
+    s << "#define G_ " << tile.G << "\n#define KTT_ " << KTT << "\n#define ITERS_ " << ntiles * KTT << "L\n";
+    s << "// Stream-K: the workgroup that runs (tile, k-tile) iteration x.\n"
+         "__device__ __forceinline__ int fg_sk_owner(long x) { return (int)(((x + 1) * G_ - 1) / ITERS_); }\n";
+  }
   s << sig(main_name, NT, true) << " {\n";
   s << R"(  // Operand stages, double-buffered, rows padded by 4 floats; then per-wave
   // 32 x WN staging tiles for the epilogue.
@@ -1835,22 +1931,38 @@ RenderedKernel render_gemm(const KernelInfo& ki, const GemmMatch& g, const std::
     while (std::getline(is, l)) o << pre << l << "\n";
     return o.str();
   };
-  if (S == 1) {
+  if (!split) {
     s << indent(epilogue(), "        ");
   } else {
     // Raw partial sums of this K range; the epilogue runs after they are summed.
     s << "        *(fg_f4*)(fg_scratch + ((long)ks * M_ + grow) * NP_ + gcol) = gv;\n";
   }
-  s << "      }\n    }\n    __syncthreads();\n  }\n}\n";
-  if (S > 1) {
-    // Second pass: one thread per 4 columns of a row sums the S partials in
-    // split order, then runs the epilogue.
+  s << "      }\n    }\n    __syncthreads();\n  }\n";
+  if (tile.stream_k) s << "  }\n";  // the workgroup's next segment
+  s << "}\n";
+  if (split) {
+    // Second pass: one thread per 4 columns of a row sums the partials in
+    // split order (stream-K: the tile's segments, in k order), then runs the
+    // epilogue.
     s << sig(name + "_fin", 256, false) << " {\n";
     s << R"(  const long gid = (long)blockIdx.x * 256 + threadIdx.x;
   if (gid >= (long)M_ * (NP_ / 4)) return;
   const int grow = (int)(gid / (NP_ / 4)), gcol = (int)(gid % (NP_ / 4)) * 4;
   fg_f4 gv = *(const fg_f4*)(fg_scratch + (long)grow * NP_ + gcol);
-  for (int ks = 1; ks < S_; ks++) {
+)";
+    if (tile.stream_k) {
+      // The tile's block index (the inverse of the main pass's grouped
+      // order), then how many workgroups its k-tiles were split over.
+      s << R"(  const int nbm = (M_ + BM - 1) / BM, nbn = (N_ + BN - 1) / BN, GM = 8;
+  const int tm = grow / BM, tn = gcol / BN, group = tm / GM, first_m = group * GM;
+  const int gsz = (nbm - first_m) < GM ? (nbm - first_m) : GM;
+  const long t0 = (long)(group * GM * nbn + tn * gsz + (tm - first_m)) * KTT_;
+  const int nseg = fg_sk_owner(t0 + KTT_ - 1) - fg_sk_owner(t0) + 1;
+  for (int ks = 1; ks < nseg; ks++) {)";
+    } else {
+      s << "  for (int ks = 1; ks < S_; ks++) {";
+    }
+    s << R"(
     const fg_f4 p = *(const fg_f4*)(fg_scratch + ((long)ks * M_ + grow) * NP_ + gcol);
     gv.x = gv.x + p.x; gv.y = gv.y + p.y; gv.z = gv.z + p.z; gv.w = gv.w + p.w;
   }
@@ -1865,8 +1977,9 @@ RenderedKernel render_gemm(const KernelInfo& ki, const GemmMatch& g, const std::
   rk.source = s.str();
   if (tile.nbuf == 3) rk.source = gemm_three_stages(rk.source);
   rk.block[0] = static_cast<unsigned>(NT);
-  rk.grid[0] = static_cast<unsigned>(ntiles * S);
-  if (S > 1) {
+  rk.grid[0] = static_cast<unsigned>(tile.stream_k ? tile.G : ntiles * S);
+  if (tile.stream_k) rk.source = gemm_stream_k(rk.source);
+  if (split) {
     LaunchSpec a, b;
     a.func = name + "_part";
     a.grid[0] = rk.grid[0];

@@ -7,9 +7,11 @@ K = 8192) pads to 1024 columns in 256-wide tiles; a 256x160 workgroup tile
 four (16-byte LDS reads) and one of one. These shapes are ones the tile model
 gives a 160-wide tile, in all three orientations of a Linear's products
 (forward x·Wᵀ, dX = G·W, dW = Gᵀ·X: gradient.rs:100-105, 165-176), with
-ragged edges, split K, 16-wide k-tiles (three LDS stages) and a 160-row
-tile (the chunked layout on the A side). Each product is checked per element
-within 1e-4·Σ|terms| of float64 on sampled output rows."""
+ragged edges, split K, stream-K (each workgroup an equal share of the
+(tile, k-tile) iterations, crossing tile boundaries; C5's dW1 runs so),
+16-wide k-tiles (three LDS stages) and a 160-row tile (the chunked layout on
+the A side). Each product is checked per element within 1e-4·Σ|terms| of
+float64 on sampled output rows."""
 from __future__ import annotations
 
 import re
@@ -19,12 +21,12 @@ import pytest
 
 from conftest import rel_err_bound
 
-# (B, in, out) -> the tile (BM, BN) each product gets, from the tile model.
+# (B, in, out) -> the tile (BM, BN, stream-K) each product gets, from the tile model.
 CASES = {
-    (3000, 800, 600): {"fwd": (256, 160), "dx": (256, 160)},
-    (4096, 4096, 784): {"fwd": (256, 160), "dw": (160, 256)},
-    (2048, 784, 1000): {"dx": (256, 160), "dw": (256, 160)},
-    (8192, 784, 4096): {"dx": (256, 160), "dw": (256, 160)},
+    (3000, 800, 600): {"fwd": (256, 160, False), "dx": (256, 160, False)},
+    (4096, 4096, 784): {"fwd": (256, 160, True), "dw": (160, 256, True)},
+    (2048, 784, 1000): {"dx": (256, 160, False), "dw": (256, 160, False)},
+    (8192, 784, 4096): {"dx": (256, 160, True), "dw": (256, 160, True)},
 }
 
 
@@ -41,7 +43,8 @@ def gemm_tile(fg, t):
     src = [it["source"] for it in fg.debug_plan([t], fuse=True, render_hip=True)["items"]
            if it["class"] == "gemm_mfma_f32"]
     assert len(src) == 1
-    return tuple(int(re.search(r"#define %s (\d+)" % k, src[0]).group(1)) for k in ("BM", "BN"))
+    return tuple(int(re.search(r"#define %s (\d+)" % k, src[0]).group(1)) for k in ("BM", "BN")) + (
+        "#define ITERS_" in src[0],)
 
 
 @pytest.mark.parametrize("shape", sorted(CASES))
@@ -101,11 +104,13 @@ sys.exit(0 if max(errs.values()) <= 1.0 else 1)
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("tile", ["256,160,16,4,1,3,3", "160,256,32,1,4,2"])
+@pytest.mark.parametrize("tile", ["256,160,16,4,1,3,3", "160,256,32,1,4,2", "256,160,16,4,1,0,3", "128,128,32,2,2,0"])
 def test_forced_160_wide_tiles_against_float64(tile):
     # Tiles the model rarely picks (16-wide k-tiles with three LDS stages; a
-    # 160-row tile on every orientation), fixed with the FG_GEMM_TILE tuning
-    # override in a process of their own, as it holds for every GEMM.
+    # 160-row tile on every orientation; stream-K, split count 0, with those
+    # stages and with two workgroups per CU on ragged 128x128 tiles), fixed
+    # with the FG_GEMM_TILE tuning override in a process of their own, as it
+    # holds for every GEMM.
     import os
     import subprocess
     import sys
