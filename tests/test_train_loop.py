@@ -40,8 +40,8 @@ def test_native_loop_matches_python_loop_cpu(fg, cpu, dims):
     assert l_nat == l_py and l_nat[-1] < l_nat[0]
     for a, b in zip(p_nat, p_py):
         assert np.array_equal(a, b)
-    # Calls shorter and longer than the loop's four steps in flight.
-    for chunks in ([4, 1, 4], [2, 3, 4], [6, 3]):
+    # Calls shorter and longer than the loop's steps in flight (8 by default).
+    for chunks in ([4, 1, 4], [2, 3, 4], [6, 3], [9]):
         l_ch, p_ch = run(fg, cpu, dims, 8, 9, native=True, chunks=chunks)
         assert l_ch == l_py and all(np.array_equal(a, b) for a, b in zip(p_ch, p_py)), chunks
 
