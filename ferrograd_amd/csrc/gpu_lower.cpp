@@ -1204,9 +1204,11 @@ int64_t gemm_tile_residency(const GemmTile& t) {
 //   128x128 at 127. The shape, k-tile and split count are chosen by estimated time:
 //   rounds of resident workgroups times the MFMA time of one tile's K range
 //   (padding included, at each shape's measured efficiency), plus the traffic
-//   of split-K partials. For dW1 of the C5 MLP (4096x784, K 8192) that picks
-//   256x256 with 4 splits (477 us), one full round of 256 workgroups, over
-//   256x128 with 2 or 4 splits (513, 521 us) or 128x128 (511 us).
+//   of split-K partials; or, for stream-K, each workgroup's share of the
+//   k-tiles plus one more epilogue. For dW1 of the C5 MLP (4096x784, K 8192)
+//   that picks 256x160 tiles as stream-K (410 + 13 us in the train step), over
+//   256x160 with 3 splits on 240 CUs (430 + 10 us) and 256x256 with 4 splits
+//   (484 + 14 us).
 // - A side of at most 32 (N = 10 classes): one operand is streamed once, so the
 //   kernel is HBM-bound. BK 16 (less LDS, more resident workgroups) and splits
 //   up to about two workgroups per CU: the 8192x10 (K 4096) forward took 59 us
