@@ -79,6 +79,30 @@ def test_native_loop_errors_cross_the_abi(fg, cpu):
         fg.train_steps_native(model.layers, opt, x, x, -1)
 
 
+@pytest.mark.parametrize("depth,ok", [("1", True), ("3", True), ("0", False), ("9", False), ("x", False)])
+def test_steps_in_flight_setting(fg, cpu, depth, ok):
+    # FG_STEPS_IN_FLIGHT (read once per process) sets how many steps the
+    # native loop queues ahead; any depth gives the same bits, and a value
+    # outside 1..8 fails with a message naming the setting.
+    import json
+    import os
+    import subprocess
+    import sys
+
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    code = ("import sys, json; sys.path.insert(0, %r); sys.path.insert(0, %r); import ferrograd_amd as fg, oracle; "
+            "oracle.load(); from test_train_loop import run; l, p = run(fg, 'cpu', (16, 8, 4), 8, 7, True); "
+            "print(json.dumps(l))") % (root, os.path.join(root, "tests"))
+    r = subprocess.run([sys.executable, "-c", code], env=dict(os.environ, FG_STEPS_IN_FLIGHT=depth),
+                       capture_output=True, text=True)
+    if ok:
+        assert r.returncode == 0, r.stderr[-2000:]
+        l_py, _ = run(fg, cpu, (16, 8, 4), 8, 7, native=False)
+        assert json.loads(r.stdout.strip().splitlines()[-1]) == l_py
+    else:
+        assert r.returncode != 0 and "FG_STEPS_IN_FLIGHT must be 1 to 8" in r.stderr
+
+
 @pytest.mark.gpu
 @pytest.mark.parametrize("batch,dims", [(256, (784, 128, 10)), (64, (96, 64, 32, 10))])
 def test_native_loop_matches_python_loop_hip(fg, cpu, batch, dims):
