@@ -1768,12 +1768,12 @@ RenderedKernel render_gemm(const KernelInfo& ki, const GemmMatch& g, const std::
   s << loader("a", g.a, sa, BM, M, "m");
   s << loader("b", g.b, sb, BN, N, "n");
   // [k][row] stages: one LDS read of each chunk's interleaved rows per MFMA step.
-  auto km_frag = [&](const char* S, const char* w, const char* fr, int T) {
+  auto km_frag = [&](const char* stage, const char* w, const char* fr, int T) {
     std::ostringstream f;
     f << "    #pragma unroll\n    for (int t = 0; t < 4; t++) {\n";
     for (const KmChunk& c : km_chunks(T)) {
       f << "      {\n        const typename fg_vt<" << c.size << ">::t v = *(const typename fg_vt<" << c.size
-        << ">::t*)&" << S << "[buf][8 * g + 4 * h + t][" << w << " + " << 32 * c.first << " + " << c.size
+        << ">::t*)&" << stage << "[buf][8 * g + 4 * h + t][" << w << " + " << 32 * c.first << " + " << c.size
         << " * r32];\n";
       f << "        #pragma unroll\n        for (int i = 0; i < " << c.size << "; i++) " << fr << "[" << c.first
         << " + i][t] = ((const float*)&v)[i];\n      }\n";
