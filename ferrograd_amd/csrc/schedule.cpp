@@ -680,13 +680,17 @@ UOp rewrite_index_movement(const UOp& inner, const std::vector<UOp>& idxs) {
   const UOp& src = inner.src(0);
   std::vector<UOp> ni;
   // A reshape that is not a squeeze flattens to one index (indexing.rs:167);
-  // only a flat buffer can consume it. The reference indexes out of bounds
-  // (a panic) when a permuted view follows: report it instead.
+  // only a one-dimensional buffer can consume it. Any view of rank > 1 under
+  // such a reshape (a permute, or the Reshape(Buffer, shape) that every
+  // created or realised tensor is, tensor.rs:260-284, schedule.rs:340-353)
+  // receives one index for several dimensions, and the reference's
+  // flat_index assertion panics (indexing.rs:42-46): report it instead.
   Shape inner_shape;
   if (inner.op() != Op::Contiguous && inner.shape_opt(&inner_shape) && idxs.size() != inner_shape.size())
     fail(std::string("rangeify: ") + op_name(inner.op()) + " of rank " + std::to_string(inner_shape.size()) +
          " indexed with " + std::to_string(idxs.size()) +
-         " indices (reshape of a non-contiguous view needs contiguous() first)");
+         " indices (a reshape that is not a squeeze reaches a view of several dimensions; the reference's index "
+         "rules support it only over a one-dimensional buffer)");
   switch (inner.op()) {
     case Op::Shrink:
       for (size_t ax = 0; ax < idxs.size(); ax++) {

@@ -136,8 +136,27 @@ def test_in_place_update_reading_other_indices_is_rejected(fg, cpu):
 
 def test_reshape_of_permuted_view_is_an_error_not_a_crash(fg, cpu):
     w = fg.Tensor.new(np.arange(4, dtype=np.float32), [2, 2], cpu)
-    with pytest.raises(fg.FerrogradError, match="non-contiguous view"):
+    with pytest.raises(fg.FerrogradError, match="reshape that is not a squeeze reaches a view of several dimensions"):
         hip_plan(fg, [w.permute([1, 0]).reshape([4]).add(fg.Tensor.new(np.ones(4, np.float32), [4], cpu))])
+
+
+def test_reshape_index_rules_follow_the_reference(fg, cpu):
+    # indexing.rs:143-169: a reshape that only adds or drops size-1 dims maps
+    # indices one to one; any other reshape flattens to one index, which only
+    # a one-dimensional buffer takes. A created tensor is Reshape(Buffer,
+    # shape) (tensor.rs:260-284), so [6, 8] -> [48] reaches a two-dimensional
+    # view with one index: the reference's flat_index assertion panics there
+    # (indexing.rs:42-46), and this build reports it.
+    import numpy as np
+
+    a = np.arange(48, dtype=np.float32)
+    flat = fg.Tensor.new(a, [48], cpu)
+    assert np.array_equal(flat.reshape([6, 8]).add(flat.reshape([6, 8])).numpy(), (a + a).reshape(6, 8))
+    mat = fg.Tensor.new(a.reshape(6, 8), [6, 8], cpu)
+    sq = mat.reshape([6, 1, 8]).reshape([1, 6, 8, 1]).add(mat.reshape([1, 6, 8, 1]))
+    assert np.array_equal(sq.numpy().reshape(6, 8), (a + a).reshape(6, 8))
+    with pytest.raises(fg.FerrogradError, match="reshape that is not a squeeze reaches a view of several dimensions"):
+        fg.Tensor.realize_many([mat.reshape([48]).add(flat)])
 
 
 def test_kernels_beyond_int32_indexing_are_refused(fg, cpu):

@@ -312,3 +312,27 @@ def test_reduce_read_after_an_in_place_store_is_materialised_first(fg, cpu):
     assert {"buffer": items[0]["output"]} in items[2]["inputs"]
     # Read before any store, the sum stays the root's epilogue.
     assert [it["out_shape"] for it in plan(fg, [y, w], fuse=True)] == [[1, 3], []]
+
+
+def test_roots_are_compiled_in_the_order_given(fg, cpu):
+    # schedule.rs:118-133 compiles the roots in the order given and replaces
+    # each with its buffer only after compiling it; a root is never
+    # materialised in phase 1 (schedule.rs:294-296). Listed after a root
+    # that reads it, a reduction root is therefore inlined into that root's
+    # kernel, a reduction nested inside another (the reference's CPU
+    # renderer cannot emit it: the oracle reports it). Listed first, it is a
+    # buffer the other root reads.
+    r = np.random.default_rng(3)
+    x = fg.Tensor.new(r.uniform(-1, 1, (8, 16)).astype(np.float32), [8, 16], cpu)
+    w = fg.Tensor.new(r.uniform(-1, 1, (16, 8)).astype(np.float32), [16, 8], cpu)
+    s = x.sum([0])
+    m = s.matmul(w)
+    # (Phase 1 first copies W for matmul's permute().contiguous(), tensor.rs:771-777.)
+    producer_first = plan(fg, [s, m])
+    assert [it["out_shape"] for it in producer_first] == [[8, 16], [1, 16], [1, 8]]
+    assert {"buffer": producer_first[1]["output"]} in producer_first[2]["inputs"]
+    consumer_first = plan(fg, [m, s])
+    assert [it["out_shape"] for it in consumer_first] == [[8, 16], [1, 8], [1, 16]]
+    assert {"buffer": consumer_first[2]["output"]} not in consumer_first[1]["inputs"]
+    with pytest.raises(fg.FerrogradError, match="range used outside its loop"):
+        fg.Tensor.realize_many([m, s])
