@@ -166,9 +166,52 @@ const GpuPasses& gpu_passes() {
 }
 
 // ── optimize: symbolic + size-1 reduce ranges ───────────────────────────────
+namespace {
+
+// A reduction inlined in another's value can range over the very Range node
+// the enclosing reduction binds: rangeify gives a reduced axis one range per
+// kernel, and a log_softmax row sum summed again over the same axis reuses it.
+// The inner loop shadows the outer one, as two nested C loops of one index
+// name do in the CPU backend's kernel: inside the inner reduction the range
+// is the inner loop's index, outside it the outer's. Give every such inner
+// reduction fresh ranges of the same extents so that each loop has its own.
+UOp rename_shadowed_ranges(UOp k) {
+  int64_t next = 0;
+  for (auto& n : k.toposort())
+    if (n.op() == Op::Range) next = std::max(next, n.arg().a + 1);
+  for (;;) {
+    UOp inner;
+    for (auto& n : k.toposort()) {
+      if (n.op() != Op::Reduce || n.srcs().size() < 2) continue;
+      UOpSet outer(n.srcs().begin() + 1, n.srcs().end());
+      for (auto& m : n.src(0).toposort()) {
+        if (m.op() != Op::Reduce) continue;
+        for (size_t i = 1; i < m.srcs().size() && !inner; i++)
+          if (outer.count(m.src(i))) inner = m;
+        if (inner) break;
+      }
+      if (inner) break;
+    }
+    if (!inner) return k;
+    UOpMap<UOp> fresh;
+    std::vector<UOp> srcs{UOp()};
+    for (size_t i = 1; i < inner.srcs().size(); i++) {
+      const UOp& r = inner.src(i);
+      UOp nr = UOp::make_new(Op::Range, r.dtype(), r.srcs(), Arg::range(next++, r.arg().range_kind()));
+      fresh[r] = nr;
+      srcs.push_back(nr);
+    }
+    srcs[0] = substitute_with_map(inner.src(0), fresh);
+    k = substitute_with_map(k, {{inner, UOp::make_new(Op::Reduce, inner.dtype(), srcs, inner.arg())}});
+  }
+}
+
+}  // namespace
+
 UOp gpu_optimize(const UOp& rangeified) {
   const bool symbolic = gpu_passes().symbolic;
   UOp k = symbolic ? graph_rewrite(rangeified, symbolic_simple) : rangeified;
+  k = rename_shadowed_ranges(k);
   // A reduce range of extent 1 iterates once at index 0: substitute 0 and
   // drop it from the Reduce (the accumulation itself is kept).
   auto drop_unit = [](const UOp& n) -> UOp {
@@ -625,6 +668,7 @@ std::string emit_serial_reduce(Emitter& em, const UOp& R, int lane_outer) {
   em.line(std::string(ctype(R.dtype())) + " " + acc + " = " + init_lit(rop, R.dtype()) + ";");
   size_t opened = 0;
   int unroll = 1;
+  std::string unroll_var;
   for (size_t i = 0; i < ranges.size(); i++) {
     const UOp& r = ranges[i];
     int64_t ext = range_extent(r);
@@ -632,6 +676,7 @@ std::string emit_serial_reduce(Emitter& em, const UOp& R, int lane_outer) {
     bool last = i + 1 == ranges.size();
     if (last && ext > 4 && ext % 4 == 0) {
       unroll = 4;
+      unroll_var = v;
       em.open_scope("for (int " + v + " = 0; " + v + " < " + std::to_string(ext / 4) + "; " + v + "++) {", "}");
       em.define_range(r, "(" + v + "*4)");
       em.set_lane_range(r, 4);
@@ -642,8 +687,29 @@ std::string emit_serial_reduce(Emitter& em, const UOp& R, int lane_outer) {
     opened++;
   }
   const UOp& value = R.src(0);
+  bool nested = false;
+  for (auto& n : value.toposort()) nested = nested || n.op() == Op::Reduce;
   std::string group;
-  if (unroll == 4) {
+  if (unroll == 4 && nested) {
+    // A reduction in the value sets its own lane range while it is emitted,
+    // so the four lanes are emitted one after another instead, each in a
+    // scope of its own with the unrolled range fixed to that lane's index;
+    // the fold order stays (((v0 op v1) op v2) op v3).
+    em.clear_lane_range();
+    const UOp& r = ranges.back();
+    std::vector<std::string> lanes;
+    for (int u = 0; u < 4; u++) {
+      std::string t = em.fresh("lane");
+      em.line(std::string(ctype(value.dtype())) + " " + t + ";");
+      em.open_scope("{", "}");
+      em.define_range(r, "(" + unroll_var + "*4+" + std::to_string(u) + ")");
+      em.line(t + " = " + em.val(value, 0) + ";");
+      em.close_scope();
+      lanes.push_back(t);
+    }
+    group = lanes[0];
+    for (int u = 1; u < 4; u++) group = combine(rop, group, lanes[u]);
+  } else if (unroll == 4) {
     std::vector<std::string> lanes;
     for (int u = 0; u < 4; u++) lanes.push_back(em.val(value, u));
     group = lanes[0];
@@ -2076,8 +2142,10 @@ RenderedKernel render_block(const KernelInfo& ki, KernelClass base, const std::s
   const std::string NT = std::to_string(kBlockThreads);
   Emitter em;
   const UOp* R = ki.reduces.size() == 1 ? &ki.reduces[0] : nullptr;
+  // Innermost reduce range; a reduction whose ranges were all of extent 1
+  // has none left and folds a single term.
   int64_t Lin = 1;
-  if (R) Lin = range_extent(R->srcs().back());
+  if (R && R->srcs().size() >= 2) Lin = range_extent(R->srcs().back());
   const bool serial_form = !R || base == KernelClass::Serial || base == KernelClass::Elementwise || Lin <= 32;
   auto store = [&](const std::string& guard) {
     std::string v = em.val(ki.value, 0);

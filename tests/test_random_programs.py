@@ -18,6 +18,14 @@ def test_random_program_on_the_oracle(fg, cpu, seed):
     assert randprog.check(nodes, fg) <= 1.0
 
 
+@pytest.mark.parametrize("seed", SEEDS)
+def test_random_program_renders_for_hip(fg, cpu, seed):
+    # Every kernel of the program through the HIP lowering and renderer, on
+    # the CPU: a program the renderer cannot emit fails here without a GPU.
+    nodes = randprog.random_program(fg, cpu, seed)
+    fg.debug_plan([n.t for n in nodes], fuse=True, render_hip=True)
+
+
 @pytest.mark.gpu
 @pytest.mark.parametrize("seed", SEEDS)
 def test_random_program_on_hip(fg, hip, seed):
@@ -50,3 +58,44 @@ def test_a_reduction_root_read_by_another_root_on_hip(fg, hip, consumer_first):
     assert rel_err_bound(s.numpy().reshape(1, 16), s64, np.abs(x64).sum(axis=0, keepdims=True), 1e-4) <= 1.0
     assert rel_err_bound(m.numpy().reshape(1, 8), s64 @ w64, np.abs(x64).sum(axis=0, keepdims=True) @ np.abs(w64),
                          1e-4) <= 1.0
+
+
+@pytest.mark.gpu
+def test_a_sum_over_a_unit_axis_on_hip(fg, hip):
+    # All of the reduction's ranges have extent 1: the lowering drops them and
+    # the small-kernel body folds one term per output.
+    import numpy as np
+
+    xa = np.random.default_rng(5).uniform(-1, 1, (32, 1)).astype(np.float32)
+    y = fg.Tensor.new(xa, [32, 1], hip).sum([1])
+    z = y.narrow(0, 26, 4)
+    fg.Tensor.realize_many([y, z])
+    assert np.array_equal(y.numpy().reshape(32, 1), xa)
+    assert np.array_equal(z.numpy().reshape(4, 1), xa[26:30])
+
+
+@pytest.mark.gpu
+def test_a_row_reduction_summed_again_over_its_axis_on_hip(fg, hip):
+    # sum(log_softmax(x, 1)) feeding a matmul: the kernel of the sum inlines
+    # the row sum of exp into a reduction over the same axis. Rangeify gives
+    # both the one range of that axis, the inner loop shadowing the outer; the
+    # lowering renames it, and the outer reduction's unrolled lanes are
+    # emitted one at a time around the inner one.
+    import numpy as np
+
+    from conftest import rel_err_bound
+
+    r = np.random.default_rng(6)
+    xa = r.uniform(-1, 1, (16, 8)).astype(np.float32)
+    wa = r.uniform(-1, 1, (1, 8)).astype(np.float32)
+    x = fg.Tensor.new(xa, [16, 8], hip)
+    w = fg.Tensor.new(wa, [1, 8], hip)
+    ls = x.log_softmax(1)
+    m = ls.sum([0, 1]).matmul(w)
+    fg.Tensor.realize_many([ls, m])
+    x64 = xa.astype(np.float64)
+    z = x64 - x64.max(axis=1, keepdims=True)
+    want = z - np.log(np.exp(z).sum(axis=1, keepdims=True))
+    assert rel_err_bound(ls.numpy().reshape(16, 8), want, np.full((16, 8), 4.0), 1e-4) <= 1.0
+    mag = 4.0 * 128 * np.abs(wa.astype(np.float64))
+    assert rel_err_bound(m.numpy().reshape(1, 8), want.sum() * wa.astype(np.float64), mag, 1e-4) <= 1.0
