@@ -23,6 +23,9 @@ from __future__ import annotations
 import numpy as np
 
 SHAPES = [(4, 6), (6, 4), (3, 4, 5), (8, 16), (16, 8), (2, 3, 4, 2), (32,), (5, 7)]
+# Above the small-kernel limits (4096 outputs), so the row-reduce,
+# column-reduce, elementwise and GEMM kernel classes render too.
+LARGE_SHAPES = [(64, 96), (96, 64), (128, 48), (16, 24, 20), (256, 32), (32, 256), (6, 8, 10, 12), (5000,)]
 
 
 class Node:
@@ -40,11 +43,13 @@ def _scalar(fg, dev, c):
     return fg.Tensor.scalar(float(np.float32(c)), dev)
 
 
-def random_program(fg, dev, seed, depth=7):
+def random_program(fg, dev, seed, depth=7, large=False):
     """Build a random program; returns the nodes to realise (the last one and
-    up to two earlier ones)."""
+    up to two earlier ones). `large` draws from LARGE_SHAPES."""
     rng = np.random.default_rng(seed)
-    pool = [leaf(fg, dev, rng, SHAPES[rng.integers(len(SHAPES))]) for _ in range(2)]
+    shapes = LARGE_SHAPES if large else SHAPES
+    widths = [3, 64, 96, 130] if large else [3, 5, 8]
+    pool = [leaf(fg, dev, rng, shapes[rng.integers(len(shapes))]) for _ in range(2)]
     for _ in range(depth):
         x = pool[rng.integers(len(pool))]
         shape = x.v.shape
@@ -123,7 +128,7 @@ def random_program(fg, dev, seed, depth=7):
             sl[d] = slice(start, start + length)
             out = Node(x.t.narrow(d, start, length), x.v[tuple(sl)], x.m[tuple(sl)])
         elif op == "matmul" and len(shape) == 2:
-            n = int(rng.choice([3, 5, 8]))
+            n = int(rng.choice(widths))
             y = leaf(fg, dev, rng, (shape[1], n))
             out = Node(x.t.matmul(y.t), x.v @ y.v, x.m @ y.m)
         elif op == "log_softmax" and len(shape) == 2:
