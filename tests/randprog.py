@@ -14,7 +14,8 @@ up here as a disagreement.
 Alongside each value the interpreter carries a magnitude: an upper bound of
 the absolute terms that feed each element (sums of |terms| for add, sum and
 matmul, products of magnitudes for mul, the row maximum for max and
-log_softmax, exp's derivative for exp). An element passes when
+log_softmax, exp's derivative for exp; sqrt, 1/z and log of z = x*x + 1 add
+z's bound times the derivative at z). An element passes when
 |got - want| <= 1e-4 * magnitude + 1e-6: f32 rounding over these short
 programs stays orders of magnitude inside that, and an indexing or
 partitioning mistake moves elements by their own size."""
@@ -57,7 +58,7 @@ def random_program(fg, dev, seed, depth=7, large=False):
                          "log_softmax", "contiguous"])
         out = None
         if op == "unary":
-            u = rng.choice(["neg", "relu", "exp", "scale", "sqrt1p"])
+            u = rng.choice(["neg", "relu", "exp", "scale", "sqrt1p", "recip1p", "log1p"])
             if u == "neg":
                 out = Node(x.t.neg(), -x.v, x.m)
             elif u == "relu":
@@ -72,9 +73,17 @@ def random_program(fg, dev, seed, depth=7, large=False):
                 c = float(rng.choice([0.5, -2.0, 0.125, 3.0]))
                 out = Node(x.t.mul(_scalar(fg, dev, c)), x.v * c, x.m * abs(c))
             else:
+                # f(x*x + 1) for f = sqrt, 1/z, log: z >= 1 keeps each defined;
+                # the magnitude adds z's own bound times |f'(z)|.
                 z = x.v * x.v + 1.0
-                out = Node(x.t.mul(x.t).add(_scalar(fg, dev, 1.0)).sqrt(), np.sqrt(z),
-                           np.sqrt(z) + (2 * x.m * np.abs(x.v) + 1.0) / (2 * np.sqrt(z)))
+                zm = 2 * x.m * np.abs(x.v) + 1.0
+                zt = x.t.mul(x.t).add(_scalar(fg, dev, 1.0))
+                if u == "sqrt1p":
+                    out = Node(zt.sqrt(), np.sqrt(z), np.sqrt(z) + zm / (2 * np.sqrt(z)))
+                elif u == "recip1p":
+                    out = Node(zt.reciprocal(), 1.0 / z, 1.0 / z + zm / (z * z))
+                else:
+                    out = Node(zt.log(), np.log(z), np.log(z) + zm / z + 1.0)
         elif op == "binary":
             same = [p for p in pool if p.v.shape == shape and p is not x]
             y = same[rng.integers(len(same))] if same and rng.random() < 0.6 else leaf(fg, dev, rng, shape)

@@ -111,11 +111,12 @@ def test_large_random_program_on_the_oracle(fg, cpu, seed):
     assert randprog.check(nodes, fg) <= 1.0
 
 
-# Seed 1085 (five one-workgroup kernels over 6-element outputs, launched as
-# one batch) stopped the test process for over three minutes on its first
-# GPU run, before it printed a result; its kernels and their batch read as
-# terminating and in bounds, and no cause has been shown, so it stays off
-# the GPU until one is.
+# The program seed 1085 drew before reciprocal and log joined the unary ops
+# (five one-workgroup kernels over 6-element outputs, launched as one batch)
+# stopped the test process for over three minutes on its first GPU run,
+# before it printed a result. Its kernels and their batch read as
+# terminating and in bounds, and no cause has been shown, so the seed stays
+# off the GPU until one is.
 UNEXPLAINED_STALL = {1085}
 
 
