@@ -34,20 +34,27 @@ class Node:
         self.t, self.v, self.m = t, v, m  # device tensor, float64 value, float64 magnitude
 
 
+_LEAVES = []  # the leaves of the program random_program is building
+
+
 def leaf(fg, dev, rng, shape):
     a = rng.uniform(-1, 1, shape).astype(np.float32)
     v = a.astype(np.float64)
-    return Node(fg.Tensor.new(a, list(shape), dev), v, np.abs(v))
+    n = Node(fg.Tensor.new(a, list(shape), dev), v, np.abs(v))
+    _LEAVES.append(n)
+    return n
 
 
 def _scalar(fg, dev, c):
     return fg.Tensor.scalar(float(np.float32(c)), dev)
 
 
-def random_program(fg, dev, seed, depth=7, large=False):
+def random_program(fg, dev, seed, depth=7, large=False, leaves=None):
     """Build a random program; returns the nodes to realise (the last one and
-    up to two earlier ones). `large` draws from LARGE_SHAPES."""
+    up to two earlier ones). `large` draws from LARGE_SHAPES; `leaves`, a
+    list, receives the program's input nodes."""
     rng = np.random.default_rng(seed)
+    _LEAVES.clear()
     shapes = LARGE_SHAPES if large else SHAPES
     widths = [3, 64, 96, 130] if large else [3, 5, 8]
     pool = [leaf(fg, dev, rng, shapes[rng.integers(len(shapes))]) for _ in range(2)]
@@ -156,6 +163,9 @@ def random_program(fg, dev, seed, depth=7, large=False):
     # (schedule.rs:118-133), so a root listed before one it reads would
     # inline that root's reduction as a nested reduce.
     idx = sorted(set(rng.choice(len(pool) - 1, size=min(2, len(pool) - 1), replace=False).tolist()) | {len(pool) - 1})
+    if leaves is not None:
+        leaves.extend(_LEAVES)
+    _LEAVES.clear()
     return [pool[i] for i in idx]
 
 

@@ -129,3 +129,33 @@ def test_large_random_program_on_hip(fg, hip, seed):
         pytest.skip("stalled on its first GPU run with no cause found yet")
     nodes = randprog.random_program(fg, hip, seed, large=True)
     assert randprog.check(nodes, fg) <= 1.0
+
+
+def _program_gradients(fg, dev, seed, large):
+    """d(sum of the last node)/d(each leaf), as float64 arrays."""
+    import numpy as np
+
+    leaves = []
+    nodes = randprog.random_program(fg, dev, seed, large=large, leaves=leaves)
+    last = nodes[-1].t
+    loss = last.sum(list(range(len(last.shape))))
+    grads = loss.gradient([n.t for n in leaves])
+    fg.Tensor.realize_many(grads)
+    return [g.numpy().astype(np.float64).reshape(n.v.shape) for g, n in zip(grads, leaves)]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("seed,large", [(s, False) for s in range(60)] + [(s, True) for s in range(2000, 2040)])
+def test_random_program_gradients_on_hip_match_the_oracle(fg, cpu, hip, seed, large):
+    # The backward graphs (expand-sums, relu and max masks, matmul
+    # transposes, log_softmax's) of the random programs: HIP against the
+    # oracle device, leaf by leaf, within 1e-4 of the largest gradient
+    # element (plus 1e-6). Both share the front end; this checks the HIP
+    # kernels, fusions and batches that run the backward.
+    import numpy as np
+
+    want = _program_gradients(fg, cpu, seed, large)
+    got = _program_gradients(fg, hip, seed, large)
+    scale = max([float(np.abs(w).max()) for w in want] + [1.0])
+    for g, w in zip(got, want):
+        assert np.all(np.abs(g - w) <= 1e-4 * scale + 1e-6), (seed, float(np.max(np.abs(g - w))), scale)
