@@ -461,6 +461,10 @@ int fg_debug_plan(fg_tensor** roots, int n, int fuse, int render, char* buf, siz
     }
     std::ostringstream os;
     os << "{\"items\": [";
+    // With `render`: which launches are block kernels, and their argument
+    // counts, for the batch runs a replayed sequence would launch.
+    std::vector<bool> is_block;
+    std::vector<size_t> nargs;
     if (!rs.empty()) {
       fg::ScheduleOptions opt;
       opt.fuse = fuse != 0;
@@ -499,11 +503,21 @@ int fg_debug_plan(fg_tensor** roots, int n, int fuse, int render, char* buf, siz
              << fg::kernel_class_name(fg::base_class(k)) << "\", \"grid\": [" << rk.grid[0] << ", " << rk.grid[1] << ", "
              << rk.grid[2] << "], \"block\": [" << rk.block[0] << ", " << rk.block[1] << ", " << rk.block[2]
              << "], \"source\": \"" << json_escape(rk.source) << "\"";
+          is_block.push_back(!rk.stage_fn.empty() && rk.launches.empty());
+          nargs.push_back(it.output_buffer ? it.inputs.size() + 1 : it.inputs.size());
         }
         os << "}";
       }
     }
-    os << "]}";
+    os << "]";
+    if (render) {
+      os << ", \"batches\": [";
+      auto runs = fg::block_batch_runs(is_block, nargs);
+      for (size_t i = 0; i < runs.size(); i++)
+        os << (i ? ", " : "") << "[" << runs[i].first << ", " << runs[i].second << "]";
+      os << "]";
+    }
+    os << "}";
     last = os.str();
     if (needed) *needed = last.size() + 1;
   });

@@ -19,6 +19,8 @@
 //                 devectorize.rs:206-214, 274-347) — bit-identical to the CPU.
 #include "gpu_lower.hpp"
 
+#include "../../include/ferrograd_hip.h"
+
 #include <algorithm>
 #include <charconv>
 #include <cmath>
@@ -660,12 +662,36 @@ int64_t total_outputs(const KernelInfo& ki) {
 // ranges in source order; the innermost splits into REDUCE x UNROLL(4) when its
 // extent is a multiple of 4 above 4 (unroll.rs:41-113), and each outer step
 // folds acc = acc (op) (((v0 op v1) op v2) op v3) (devectorize.rs:206-214, 306-319).
+//
+// The loops carry unroll bounds. Left to itself, LLVM fully unrolls a nest of
+// constant-trip loops; for a Max fold (a chain of compare-selects) over a few
+// hundred float4 loads, e.g. max over axes [1,2,3] of f32[6,8,10,12] (8 x 10 x 3
+// trips), hiprtc at -O3 then does not finish at all. So only a nest of at most
+// kSerialFullUnroll iterations, with no reduction inside its value, may unroll
+// fully; otherwise every loop but the innermost runs rolled and the innermost
+// unrolls by at most 4. Unrolling never reorders the fold: the operations stay
+// in source order, and no reassociation is allowed (no fast-math).
+constexpr int64_t kSerialFullUnroll = 16;
+
 std::string emit_serial_reduce(Emitter& em, const UOp& R, int lane_outer) {
   (void)lane_outer;
   Op rop = R.arg().rop;
   std::vector<UOp> ranges(R.srcs().begin() + 1, R.srcs().end());
   std::string acc = em.fresh("acc");
   em.line(std::string(ctype(R.dtype())) + " " + acc + " = " + init_lit(rop, R.dtype()) + ";");
+  const UOp& value = R.src(0);
+  bool nested = false;
+  for (auto& n : value.toposort()) nested = nested || n.op() == Op::Reduce;
+  // Trip count of each loop (the innermost one steps by 4 lanes when it splits).
+  std::vector<int64_t> trips;
+  for (size_t i = 0; i < ranges.size(); i++) {
+    int64_t ext = range_extent(ranges[i]);
+    bool last = i + 1 == ranges.size();
+    trips.push_back(last && ext > 4 && ext % 4 == 0 ? ext / 4 : ext);
+  }
+  int64_t nest = 1;
+  for (auto t : trips) nest *= t;
+  const bool bounded = nested || nest > kSerialFullUnroll;
   size_t opened = 0;
   int unroll = 1;
   std::string unroll_var;
@@ -674,21 +700,20 @@ std::string emit_serial_reduce(Emitter& em, const UOp& R, int lane_outer) {
     int64_t ext = range_extent(r);
     std::string v = "ridx" + std::to_string(r.arg().a) + "_" + std::to_string(em.depth());
     bool last = i + 1 == ranges.size();
+    std::string pragma;
+    if (bounded) pragma = (last && !nested && trips[i] <= 4) ? "" : (last && !nested) ? "#pragma unroll 4\n" : "#pragma unroll 1\n";
     if (last && ext > 4 && ext % 4 == 0) {
       unroll = 4;
       unroll_var = v;
-      em.open_scope("for (int " + v + " = 0; " + v + " < " + std::to_string(ext / 4) + "; " + v + "++) {", "}");
+      em.open_scope(pragma + "for (int " + v + " = 0; " + v + " < " + std::to_string(ext / 4) + "; " + v + "++) {", "}");
       em.define_range(r, "(" + v + "*4)");
       em.set_lane_range(r, 4);
     } else {
-      em.open_scope("for (int " + v + " = 0; " + v + " < " + std::to_string(ext) + "; " + v + "++) {", "}");
+      em.open_scope(pragma + "for (int " + v + " = 0; " + v + " < " + std::to_string(ext) + "; " + v + "++) {", "}");
       em.define_range(r, v);
     }
     opened++;
   }
-  const UOp& value = R.src(0);
-  bool nested = false;
-  for (auto& n : value.toposort()) nested = nested || n.op() == Op::Reduce;
   std::string group;
   if (unroll == 4 && nested) {
     // A reduction in the value sets its own lane range while it is emitted,
@@ -2929,6 +2954,27 @@ RenderedKernel render_block_batch(const std::vector<const RenderedKernel*>& stag
   rk.kind = "block_batch";
   rk.block[0] = kBlockThreads;
   return rk;
+}
+
+std::vector<std::pair<size_t, size_t>> block_batch_runs(const std::vector<bool>& is_block,
+                                                        const std::vector<size_t>& nargs) {
+  FG_CHECK(is_block.size() == nargs.size(), "block_batch_runs: one argument count per launch");
+  std::vector<std::pair<size_t, size_t>> runs;
+  for (size_t i = 0; i < is_block.size();) {
+    if (!is_block[i]) {
+      i++;
+      continue;
+    }
+    size_t n = 1, total = nargs[i];
+    while (i + n < is_block.size() && n < kMaxBatchStages && is_block[i + n] &&
+           total + nargs[i + n] <= FG_MAX_LAUNCH_ARGS) {
+      total += nargs[i + n];
+      n++;
+    }
+    if (n >= 2) runs.emplace_back(i, n);
+    i += n;
+  }
+  return runs;
 }
 
 }  // namespace fg

@@ -81,4 +81,14 @@ KernelClass base_class(const UOp& kernel);
 // that computed it.
 RenderedKernel render_block_batch(const std::vector<const RenderedKernel*>& stages, bool read_back = false);
 
+// The runs of consecutive block kernels a sequence launches as batches, as
+// (first, count) pairs: every run of two or more, split after kMaxBatchStages
+// kernels and before the kernel that would take the run's arguments past
+// FG_MAX_LAUNCH_ARGS (a batch launch passes every stage's arguments).
+// `is_block[i]` tells whether launch i is a block kernel; `nargs[i]` is its
+// argument count.
+constexpr size_t kMaxBatchStages = 16;
+std::vector<std::pair<size_t, size_t>> block_batch_runs(const std::vector<bool>& is_block,
+                                                        const std::vector<size_t>& nargs);
+
 }  // namespace fg

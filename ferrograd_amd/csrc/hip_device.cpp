@@ -294,13 +294,15 @@ class HipDevice : public Device {
         first = progs.size() - 1;
         count = 1;
       }
-      if (count) {
-        std::vector<const RenderedKernel*> stages;
-        size_t total = 3;
-        for (size_t j = first; j < first + count; j++) {
-          stages.push_back(&prog_at(j)->meta);
-          total += args_at(j).size();
-        }
+      std::vector<const RenderedKernel*> stages;
+      size_t total = 3;  // the read-back stage's destination, source and word count
+      for (size_t j = first; j < first + count; j++) {
+        stages.push_back(&prog_at(j)->meta);
+        total += args_at(j).size();
+      }
+      // With no room left for the read-back's arguments, the read-back stays
+      // a kernel of its own after the batch.
+      if (count && total <= FG_MAX_LAUNCH_ARGS) {
         r->rb_batch = compile(render_block_batch(stages, true), total);
         r->rb_first = first;
       }
@@ -445,32 +447,26 @@ class HipDevice : public Device {
   }
 
   // Runs of two or more consecutive block kernels (one workgroup each, no
-  // scratch) in a sequence: each becomes one launch of a batch program that
-  // runs the kernels' bodies in order behind workgroup barriers. At most
-  // kMaxBatch kernels per batch. The batch's code object is cached by its
-  // source like any other.
+  // scratch) in a sequence (block_batch_runs): each becomes one launch of a
+  // batch program that runs the kernels' bodies in order behind workgroup
+  // barriers. The batch's code object is cached by its source like any other.
   void group_blocks(const std::vector<Program*>& progs, std::vector<std::vector<KernelArg>>& args,
                     std::vector<std::pair<size_t, size_t>>& groups, std::vector<std::shared_ptr<Program>>& batches) {
-    constexpr size_t kMaxBatch = 16;
-    auto is_block = [&](size_t i) { return is_block_program(*progs[i]); };
-    for (size_t i = 0; i < progs.size();) {
-      if (!is_block(i)) {
-        i++;
-        continue;
+    std::vector<bool> is_block;
+    std::vector<size_t> nargs;
+    for (size_t i = 0; i < progs.size(); i++) {
+      is_block.push_back(is_block_program(*progs[i]));
+      nargs.push_back(args[i].size());
+    }
+    for (auto [first, n] : block_batch_runs(is_block, nargs)) {
+      std::vector<const RenderedKernel*> stages;
+      size_t total = 0;
+      for (size_t j = first; j < first + n; j++) {
+        stages.push_back(&progs[j]->meta);
+        total += args[j].size();
       }
-      size_t n = 1;
-      while (i + n < progs.size() && n < kMaxBatch && is_block(i + n)) n++;
-      if (n >= 2) {
-        std::vector<const RenderedKernel*> stages;
-        size_t total = 0;
-        for (size_t j = i; j < i + n; j++) {
-          stages.push_back(&progs[j]->meta);
-          total += args[j].size();
-        }
-        batches.push_back(compile(render_block_batch(stages), total));
-        groups.emplace_back(i, n);
-      }
-      i += n;
+      batches.push_back(compile(render_block_batch(stages), total));
+      groups.emplace_back(first, n);
     }
   }
 

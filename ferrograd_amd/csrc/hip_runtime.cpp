@@ -519,7 +519,7 @@ int fg_hip_program_num_args(const fg_prog* p) { return p ? p->num_args : -1; }
 namespace {
 // Points params[i] at the value of args[i] (kernelParams for a HIP launch).
 int marshal_args(const fg_arg* args, int nargs, void** params) {
-  if (nargs > 64) return set_err(FG_ERR_ARGS, "fg_hip_launch: at most 64 arguments");
+  if (nargs > FG_MAX_LAUNCH_ARGS) return set_err(FG_ERR_ARGS, "fg_hip_launch: at most 64 arguments");
   for (int i = 0; i < nargs; i++) {
     switch (args[i].kind) {
       case FG_ARG_PTR: params[i] = const_cast<void**>(&args[i].v.p); break;
@@ -562,7 +562,7 @@ int check_launch(const fg_ctx* c, const fg_prog* p, int nargs, const unsigned gr
 int fg_hip_launch_direct(fg_ctx* c, fg_prog* p, const fg_arg* args, int nargs, const unsigned grid[3],
                          const unsigned block[3], unsigned lds) {
   if (int rc = check_launch(c, p, nargs, grid, block)) return rc;
-  void* params[64];
+  void* params[FG_MAX_LAUNCH_ARGS];
   if (int rc = marshal_args(args, nargs, params)) return rc;
   HIP_TRY(hipModuleLaunchKernel(p->func, grid[0], grid[1], grid[2], block[0], block[1], block[2], lds, c->stream,
                                 params, nullptr));
@@ -574,7 +574,7 @@ int fg_hip_context_device(const fg_ctx* c) { return c ? c->device : -1; }
 int fg_hip_launch(fg_ctx* c, fg_prog* p, const fg_arg* args, int nargs, const unsigned grid[3],
                   const unsigned block[3], unsigned lds) {
   if (int rc = check_launch(c, p, nargs, grid, block)) return rc;
-  void* params[64];
+  void* params[FG_MAX_LAUNCH_ARGS];
   if (int rc = marshal_args(args, nargs, params)) return rc;
   if (c->profiling) {
     // Start/stop events attached to the dispatch itself, so the duration
@@ -624,7 +624,7 @@ int fg_hip_graph_create(fg_ctx* c, int n, fg_prog* const* progs, const unsigned*
   HIP_TRY(hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal));
   int rc = FG_OK;
   for (auto& l : g->launches) {
-    void* params[64];
+    void* params[FG_MAX_LAUNCH_ARGS];
     rc = marshal_args(l.args.data(), static_cast<int>(l.args.size()), params);
     if (rc) break;
     hipError_t e = hipModuleLaunchKernel(l.prog->func, l.grid[0], l.grid[1], l.grid[2], l.block[0], l.block[1],
@@ -675,7 +675,7 @@ int fg_hip_graph_launch(fg_ctx* c, fg_graph* g, const fg_arg* args, int* updated
     const int n = static_cast<int>(l.args.size());
     if (!same_args(l.args.data(), args + off, n)) {
       std::copy(args + off, args + off + n, l.args.begin());
-      void* params[64];
+      void* params[FG_MAX_LAUNCH_ARGS];
       if (int rc = marshal_args(l.args.data(), n, params)) return rc;
       hipKernelNodeParams p = l.params;
       p.kernelParams = params;

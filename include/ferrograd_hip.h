@@ -113,7 +113,11 @@ int fg_hip_program_num_args(const fg_prog* prog);
  * stays loaded until every program sharing it is freed. */
 int fg_hip_program_function(fg_prog* prog, const char* func, int num_args, fg_prog** out);
 
-/* Launch on the context's stream. `nargs` must equal the program's num_args. */
+/* Most arguments one launch takes (fg_hip_launch and graph nodes refuse more). */
+#define FG_MAX_LAUNCH_ARGS 64
+
+/* Launch on the context's stream. `nargs` must equal the program's num_args,
+ * at most FG_MAX_LAUNCH_ARGS. */
 int fg_hip_launch(fg_ctx* ctx, fg_prog* prog, const fg_arg* args, int nargs, const unsigned grid[3],
                   const unsigned block[3], unsigned lds_bytes);
 

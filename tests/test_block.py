@@ -201,3 +201,54 @@ def test_reference_partition_small_kernels_compile_as_blocks(fg, cpu):
     assert blocks and any("void " in it["source"] and "bool* data0" in it["source"] for it in blocks)
     for it in items:
         compile_all(it["source"])
+
+
+def sixteen_roots(fg, dev, seed=11):
+    """16 roots a*b + c*d + e over f32[8], each its own block kernel with 6
+    arguments (output + five inputs): 96 arguments for a run of 16."""
+    r = np.random.default_rng(seed)
+    arrays = [[r.uniform(-1, 1, 8).astype(np.float32) for _ in range(5)] for _ in range(16)]
+    roots = []
+    for a, b, c, d, e in arrays:
+        t = [fg.Tensor.new(v, [8], dev) for v in (a, b, c, d, e)]
+        roots.append(t[0].mul(t[1]).add(t[2].mul(t[3])).add(t[4]))
+    want = [(a * b + c * d) + e for a, b, c, d, e in arrays]  # float32, each op rounded once
+    return roots, want
+
+
+def test_batch_runs_stay_within_the_launch_argument_limit(fg, cpu):
+    # A batch launch passes every stage's arguments, and a launch takes at
+    # most 64 (FG_MAX_LAUNCH_ARGS): the 16 consecutive block kernels split
+    # into runs of at most 10 six-argument kernels.
+    roots, _ = sixteen_roots(fg, cpu)
+    p = fg.debug_plan(roots, fuse=True, render_hip=True)
+    items = p["items"]
+    assert len(items) == 16 and all(it["class"] == "block" for it in items)
+    nargs = [len(it["inputs"]) + 1 for it in items]
+    assert nargs == [6] * 16
+    runs = p["batches"]
+    assert runs == [[0, 10], [10, 6]], runs
+    for first, n in runs:
+        assert sum(nargs[first:first + n]) <= 64
+
+
+def test_batch_runs_split_after_sixteen_kernels(fg, cpu):
+    # Two-argument kernels (relu of one input): the 16-stage cap splits a run
+    # of 20 before the argument limit does.
+    r = np.random.default_rng(12)
+    roots = [fg.Tensor.new(r.uniform(-1, 1, 8).astype(np.float32), [8], cpu).relu() for _ in range(20)]
+    p = fg.debug_plan(roots, fuse=True, render_hip=True)
+    assert p["batches"] == [[0, 16], [16, 4]], p["batches"]
+
+
+@pytest.mark.gpu
+def test_sixteen_block_roots_replayed_twice(fg, hip):
+    # The same 16-root plan realised three times: the first realise records
+    # the plan, the second replays it with its kernels batched, the third
+    # replays the recorded graph. Every result bit for bit against float32.
+    print("sixteen block roots, replayed", flush=True)
+    for rep in range(3):
+        roots, want = sixteen_roots(fg, hip, seed=20 + rep)
+        fg.Tensor.realize_many(roots)
+        for t, w in zip(roots, want):
+            assert np.array_equal(t.numpy().reshape(8), w), rep

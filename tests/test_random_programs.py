@@ -111,13 +111,68 @@ def test_large_random_program_on_the_oracle(fg, cpu, seed):
     assert randprog.check(nodes, fg) <= 1.0
 
 
-# The program seed 1085 drew before reciprocal and log joined the unary ops
-# (five one-workgroup kernels over 6-element outputs, launched as one batch)
-# stopped the test process for over three minutes on its first GPU run,
-# before it printed a result. Its kernels and their batch read as
-# terminating and in bounds, and no cause has been shown, so the seed stays
-# off the GPU until one is.
-UNEXPLAINED_STALL = {1085}
+def serial_max_nest_program(fg, dev):
+    """The program that stalled a GPU run: max over axes [1,2,3] of
+    f32[6,8,10,12] (a one-workgroup kernel that folds 960 terms per output
+    serially: a for 8 x for 10 x for 3 nest of float4 compare-selects), relu,
+    two permutes, a product with a broadcast sum, and a max over every axis,
+    realised as three roots (five block kernels). Left to unroll the whole
+    nest, hiprtc at -O3 never finished compiling its first kernel."""
+    import numpy as np
+
+    rng = np.random.default_rng(1085)
+    x = randprog.leaf(fg, dev, rng, (6, 8, 10, 12))
+    z = randprog.leaf(fg, dev, rng, (1, 1, 1, 6))
+    N = randprog.Node
+    mx = N(x.t.max([1, 2, 3]), x.v.max(axis=(1, 2, 3), keepdims=True), x.m.max(axis=(1, 2, 3), keepdims=True))
+    rl = N(mx.t.relu(), np.where(0 < mx.v, mx.v, 0.0), mx.m)
+    p1 = N(rl.t.permute([1, 2, 0, 3]), rl.v.transpose(1, 2, 0, 3), rl.m.transpose(1, 2, 0, 3))
+    p2 = N(mx.t.permute([2, 1, 3, 0]), mx.v.transpose(2, 1, 3, 0), mx.m.transpose(2, 1, 3, 0))
+    zs = z.t.sum([1, 2, 3])
+    zv, zm = z.v.sum(axis=(1, 2, 3), keepdims=True), z.m.sum(axis=(1, 2, 3), keepdims=True)
+    pr = N(p2.t.mul(zs.expand([1, 1, 1, 6])), p2.v * zv, p2.m * zm)
+    am = N(rl.t.max([0, 1, 2, 3]), rl.v.max(keepdims=True), rl.m.max(keepdims=True))
+    return [p1, pr, am]
+
+
+def test_serial_max_nest_compiles_in_seconds(fg, cpu):
+    # Every kernel of the program, compiled for gfx950 in child processes
+    # against a fresh cache: each serial fold's loops carry unroll bounds, so
+    # the whole plan compiles within the minute (about a second per kernel).
+    from hipcompile import compile_sources
+
+    nodes = serial_max_nest_program(fg, cpu)
+    items = fg.debug_plan([n.t for n in nodes], fuse=True, render_hip=True)["items"]
+    assert [it["class"] for it in items] == ["block"] * 5
+    assert "for (int ridx" in items[0]["source"] and "#pragma unroll 1" in items[0]["source"]
+    compile_sources({it["source"]: it["name"] for it in items}, limit_s=60)
+    assert randprog.check(nodes, fg) <= 1.0
+
+
+@pytest.mark.gpu
+def test_serial_max_nest_on_hip(fg, hip):
+    print("serial max nest program on hip", flush=True)
+    nodes = serial_max_nest_program(fg, hip)
+    assert randprog.check(nodes, fg) <= 1.0
+
+
+def test_every_random_program_compiles_for_gfx950(fg, cpu):
+    # Every kernel of every random program the HIP tests run (small, large,
+    # and the gradient programs' forward graphs), rendered and compiled
+    # compile-only on the CPU, 8 at a time, within a time limit: a kernel
+    # hiprtc cannot compile, or cannot compile in finite time, fails here
+    # without a GPU.
+    from hipcompile import compile_sources
+
+    sources = {}
+    programs = [(s, False) for s in SEEDS] + [(s, True) for s in LARGE_SEEDS + list(range(1000, 1140))]
+    programs += [(s, False) for s in range(60)] + [(s, True) for s in range(2000, 2040)]
+    for seed, large in programs:
+        nodes = randprog.random_program(fg, cpu, seed, large=large)
+        for it in fg.debug_plan([n.t for n in nodes], fuse=True, render_hip=True)["items"]:
+            sources[it["source"]] = it["name"]
+    timings = compile_sources(sources, limit_s=300)
+    assert len(timings) == len(sources) and timings[0][1] < 30, timings[:3]
 
 
 @pytest.mark.gpu
@@ -125,8 +180,6 @@ UNEXPLAINED_STALL = {1085}
 def test_large_random_program_on_hip(fg, hip, seed):
     # Shapes above the small-kernel limits: row and column reductions,
     # elementwise kernels and MFMA GEMMs, as well as block kernels.
-    if seed in UNEXPLAINED_STALL:
-        pytest.skip("stalled on its first GPU run with no cause found yet")
     nodes = randprog.random_program(fg, hip, seed, large=True)
     assert randprog.check(nodes, fg) <= 1.0
 
@@ -149,13 +202,18 @@ def _program_gradients(fg, dev, seed, large):
 def test_random_program_gradients_on_hip_match_the_oracle(fg, cpu, hip, seed, large):
     # The backward graphs (expand-sums, relu and max masks, matmul
     # transposes, log_softmax's) of the random programs: HIP against the
-    # oracle device, leaf by leaf, within 1e-4 of the largest gradient
-    # element (plus 1e-6). Both share the front end; this checks the HIP
-    # kernels, fusions and batches that run the backward.
+    # oracle device, leaf by leaf, each element within 1e-4 of its own leaf's
+    # largest gradient element, plus 1e-6 of the largest over all leaves (so
+    # a leaf whose gradient is all but zero is still held to that). Both
+    # share the front end; this checks the HIP kernels, fusions and batches
+    # that run the backward.
     import numpy as np
 
+    print(f"gradients of random program {seed} (large={large})", flush=True)
     want = _program_gradients(fg, cpu, seed, large)
     got = _program_gradients(fg, hip, seed, large)
-    scale = max([float(np.abs(w).max()) for w in want] + [1.0])
-    for g, w in zip(got, want):
-        assert np.all(np.abs(g - w) <= 1e-4 * scale + 1e-6), (seed, float(np.max(np.abs(g - w))), scale)
+    top = max([float(np.abs(w).max()) for w in want] + [1e-30])
+    for i, (g, w) in enumerate(zip(got, want)):
+        leaf = float(np.abs(w).max())
+        bound = 1e-4 * leaf + 1e-6 * top
+        assert np.all(np.abs(g - w) <= bound), (seed, i, float(np.max(np.abs(g - w))), leaf, top)
