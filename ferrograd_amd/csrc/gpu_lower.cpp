@@ -103,6 +103,7 @@ const char* kernel_class_name(KernelClass k) {
     case KernelClass::Serial: return "serial";
     case KernelClass::NarrowGemm: return "gemm_narrow_f32";
     case KernelClass::Block: return "block";
+    case KernelClass::Sequential: return "sequential";
   }
   return "?";
 }
@@ -379,8 +380,10 @@ class Emitter {
     return d;
   }
 
-  // Index of the innermost open scope that defines a range `n` depends on.
+  // Index of the innermost open scope that defines a range `n` depends on
+  // (with no hoisting: the innermost open scope).
   size_t scope_of(const UOp& n) {
+    if (no_hoist_) return scopes_.size() - 1;
     size_t best = 0;
     for (size_t i = scopes_.size(); i-- > 1;) {
       for (auto* r : scopes_[i]->ranges) {
@@ -426,6 +429,10 @@ class Emitter {
     return unit && lane_base_aligned_;
   }
   void set_lane_base_aligned(bool b) { lane_base_aligned_ = b; }
+  // Every value is emitted where it is first used instead of in the
+  // outermost scope it could live in: a load then runs after every store the
+  // program order puts before it (in-place kernels run sequentially).
+  void set_no_hoist(bool b) { no_hoist_ = b; }
   void set_nontemporal_loads(bool b) { nt_loads_ = b; }
   // Non-temporal loads only for addresses that depend on every one of these
   // ranges (the kernel's output ranges): such an element is read by one
@@ -554,6 +561,7 @@ class Emitter {
   int lanes_ = 1;
   bool lane_base_aligned_ = true;
   bool nt_loads_ = false;
+  bool no_hoist_ = false;
   std::vector<const UOpInner*> nt_ranges_;
   int counter_ = 0;
 };
@@ -768,6 +776,106 @@ RenderedKernel render_serial(const KernelInfo& ki, const std::string& name) {
   rk.source = std::string(kPrelude) + signature(ki, name, 256) + " {\n" + em.code() + "}\n";
   rk.block[0] = 256;
   rk.grid[0] = static_cast<unsigned>((T + 255) / 256);
+  return rk;
+}
+
+// ── Sequential: in-place updates that read their destination elsewhere ─────
+// The reference compiles such a kernel to nested C loops and calls it once on
+// one thread (clang.rs:28-280, cpu.rs:373-377), so each load sees the stores
+// the loop order puts before it, e.g. w.assign(w + wᵀ) reads elements the
+// same call has already overwritten. No parallel mapping keeps that, so one
+// thread runs the kernel in that order: output loops outermost first, each
+// output's value computed right before its store, every load emitted where
+// it is used (no hoisting out of a loop). The innermost output loop is split
+// into groups of 4 lanes where the reference's upcast pass splits it
+// (upcast.rs:79-104: the last output loop, extent above 4 and a multiple of
+// 4, no ALU between a reduction and the store). Within a group the
+// reference evaluates the lanes' reductions, and the values no lane index
+// reaches, before the first lane's store, then each lane's value and store
+// in lane order; so does this kernel. Reductions fold in the reference's
+// order (emit_serial_reduce).
+RenderedKernel render_sequential(const KernelInfo& ki, const std::string& name) {
+  Emitter em;
+  em.set_no_hoist(true);
+  em.reduce_cb_ = [&](const UOp& R, int lane) {
+    std::string acc = emit_serial_reduce(em, R, lane);
+    em.remember_here(R, lane, acc);
+    return acc;
+  };
+  em.line("if (blockIdx.x != 0 || threadIdx.x != 0) return;");
+  const size_t nr = ki.out_ranges.size();
+  const bool post_reduce_alu = ki.value.op() != Op::Reduce && !ki.reduces.empty();
+  const bool upcast = nr > 0 && ki.out_ext[nr - 1] > 4 && ki.out_ext[nr - 1] % 4 == 0 && !post_reduce_alu;
+  for (size_t i = 0; i + (upcast ? 1 : 0) < nr; i++) {
+    const UOp& r = ki.out_ranges[i];
+    const std::string v = "idx" + std::to_string(r.arg().a);
+    em.open_scope("#pragma unroll 1\nfor (int " + v + " = 0; " + v + " < " + std::to_string(ki.out_ext[i]) + "; " + v +
+                      "++) {",
+                  "}");
+    em.define_range(r, v);
+  }
+  auto store = [&] {
+    std::string v = em.val(ki.value, 0);
+    em.line(pname(ki.out_param) + "[" + em.idx(ki.out_index, 0) + "] = " + v + ";");
+  };
+  if (upcast) {
+    const UOp& r = ki.out_ranges[nr - 1];
+    const std::string g = "grp" + std::to_string(r.arg().a);
+    em.open_scope("#pragma unroll 1\nfor (int " + g + " = 0; " + g + " < " + std::to_string(ki.out_ext[nr - 1] / 4) +
+                      "; " + g + "++) {",
+                  "}");
+    auto lane_index = [&](int u) { return "(" + g + "*4+" + std::to_string(u) + ")"; };
+    // The value's largest subexpressions that no lane index reaches, and the
+    // reductions (outside other reductions) that one does.
+    std::vector<UOp> invariant, lane_reduces;
+    UOpSet seen;
+    // Loads and reductions are leaves of this walk; it descends through ALU.
+    std::function<void(const UOp&)> walk = [&](const UOp& n) {
+      if (!seen.insert(n).second) return;
+      if (n.op() == Op::Const || n.op() == Op::ParamScalar || n.op() == Op::Range ||
+          ((n.op() == Op::Add || n.op() == Op::Mul) && n.dtype().kind == DTypeKind::I32))
+        return;  // index arithmetic, rendered inline
+      if (!em.depends_on(n, r.get())) {
+        invariant.push_back(n);
+        return;
+      }
+      if (n.op() == Op::Reduce) lane_reduces.push_back(n);
+      if (n.op() == Op::Reduce || n.op() == Op::Load) return;
+      for (auto& x : n.srcs()) walk(x);
+    };
+    walk(ki.value);
+    for (auto& n : invariant) em.val(n, 0);
+    std::vector<std::vector<std::string>> held(4);
+    for (int u = 0; u < 4; u++) {
+      for (auto& R : lane_reduces) {
+        std::string h = em.fresh("lred");
+        em.line(std::string(ctype(R.dtype())) + " " + h + ";");
+        em.open_scope("{", "}");
+        em.define_range(r, lane_index(u));
+        std::string acc = em.val(R, 0);
+        em.line(h + " = " + acc + ";");
+        em.close_scope();
+        held[u].push_back(h);
+      }
+    }
+    for (int u = 0; u < 4; u++) {
+      em.open_scope("{", "}");
+      em.define_range(r, lane_index(u));
+      for (size_t k = 0; k < lane_reduces.size(); k++) em.remember_here(lane_reduces[k], 0, held[u][k]);
+      store();
+      em.close_scope();
+    }
+    em.close_scope();
+  } else {
+    store();
+  }
+  for (size_t i = 0; i + (upcast ? 1 : 0) < nr; i++) em.close_scope();
+  RenderedKernel rk;
+  rk.name = name;
+  rk.kind = kernel_class_name(KernelClass::Sequential);
+  rk.source = std::string(kPrelude) + signature(ki, name, 64) + " {\n" + em.code() + "}\n";
+  rk.block[0] = 64;
+  rk.grid[0] = 1;
   return rk;
 }
 
@@ -2129,7 +2237,7 @@ int64_t reduce_terms(const UOp& R) {
 }
 
 bool block_eligible(const KernelInfo& ki, KernelClass base) {
-  if (base == KernelClass::Gemm || base == KernelClass::NarrowGemm) return false;
+  if (base == KernelClass::Gemm || base == KernelClass::NarrowGemm || base == KernelClass::Sequential) return false;
   const int64_t T = total_outputs(ki);
   if (T > kBlockMaxOutputs) return false;
   std::set<const UOpInner*> nested;
@@ -2797,6 +2905,7 @@ bool reads_dest_elsewhere(const KernelInfo& ki) {
 // The class a kernel would have on its own size (no block promotion).
 KernelClass base_class(const UOp& kernel) {
   KernelInfo ki = analyze_kernel(kernel);
+  if (reads_dest_elsewhere(ki)) return KernelClass::Sequential;
   if (ki.reduces.empty()) return KernelClass::Elementwise;
   if (ki.reduces.size() > 1) return KernelClass::Serial;
   GemmMatch g;
@@ -2846,13 +2955,14 @@ RenderedKernel render_hip(const UOp& kernel, const std::string& name, int force_
                                                          " outputs; kernel indexes are int32 (at most 2^31-1)");
   FG_CHECK(!nests_reduce_over_same_range(kernel),
            "kernel nests a reduction inside another over the same range; it must be materialised first");
-  FG_CHECK(!reads_dest_elsewhere(ki),
-           "in-place update reads its destination at another index; the HIP device runs kernels in parallel and "
-           "cannot reproduce the sequential CPU order");
-  KernelClass k = force_class >= 0 ? static_cast<KernelClass>(force_class) : classify_kernel(kernel);
+  // An in-place update that reads its destination at another index has one
+  // valid order, the reference's sequential one, whatever class is asked for.
+  KernelClass k = reads_dest_elsewhere(ki)  ? KernelClass::Sequential
+                  : force_class >= 0        ? static_cast<KernelClass>(force_class)
+                                            : classify_kernel(kernel);
   if (!ki.reduces.empty() && k == KernelClass::Elementwise) k = KernelClass::Serial;
   // The symbol carries the lowering class so profiles name what ran.
-  static const char* suffix[] = {"_gemm", "_ew", "_rowred", "_colred", "_serial", "_ngemm", "_blk"};
+  static const char* suffix[] = {"_gemm", "_ew", "_rowred", "_colred", "_serial", "_ngemm", "_blk", "_seq"};
   const std::string sym = name + suffix[static_cast<int>(k)];
   std::vector<std::pair<int, DType>> params;
   for (auto& [slot, p] : ki.params) params.emplace_back(slot, p.dtype());
@@ -2877,6 +2987,7 @@ RenderedKernel render_hip(const UOp& kernel, const std::string& name, int force_
     case KernelClass::RowReduce: rk = render_row_reduce(ki, sym); break;
     case KernelClass::ColumnReduce: rk = render_column_reduce(ki, sym); break;
     case KernelClass::Serial: rk = render_serial(ki, sym); break;
+    case KernelClass::Sequential: rk = render_sequential(ki, sym); break;
     case KernelClass::Block: {
       const KernelClass base = base_class(kernel);
       FG_CHECK(block_eligible(ki, base), "kernel is too large for one workgroup");

@@ -35,7 +35,9 @@ KernelInfo analyze_kernel(const UOp& sink);
 int64_t range_extent(const UOp& r);
 
 // Lowering classes, in the order they are tried.
-enum class KernelClass { Gemm, Elementwise, RowReduce, ColumnReduce, Serial, NarrowGemm, Block };
+// Sequential: an in-place update that reads its destination at another
+// index, run by one thread in the reference's loop order.
+enum class KernelClass { Gemm, Elementwise, RowReduce, ColumnReduce, Serial, NarrowGemm, Block, Sequential };
 const char* kernel_class_name(KernelClass k);
 
 // The HIP path's optional passes, selected by the OPT environment variable

@@ -127,11 +127,15 @@ def test_narrowed_operands_stay_on_mfma_with_vector_loads(fg, cpu):
     compile_only(fg, src, gemm[0]["name"] + "_part")
 
 
-def test_in_place_update_reading_other_indices_is_rejected(fg, cpu):
+def test_in_place_update_reading_other_indices_runs_sequentially(fg, cpu):
+    # One thread in the reference's loop order (tests/test_in_place.py has
+    # the values): no parallel class may take it, whatever OPT enables.
     w = fg.Tensor.new(np.arange(4, dtype=np.float32), [2, 2], cpu)
     w.assign(w.add(w.permute([1, 0])))
-    with pytest.raises(fg.FerrogradError, match="reads its destination at another index"):
-        hip_plan(fg, [w])
+    (it,) = hip_plan(fg, [w])
+    assert it["class"] == "sequential" and it["base_class"] == "sequential"
+    assert it["grid"] == [1, 1, 1] and "threadIdx.x != 0) return;" in it["source"]
+    compile_only(fg, it["source"], it["name"])
 
 
 def test_reshape_of_permuted_view_is_an_error_not_a_crash(fg, cpu):
