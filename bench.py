@@ -252,7 +252,33 @@ def mlp_gemm_flops(batch, dims):
     return f
 
 
-def bench_mlp(fg, ctx, steps, warmup, batch, dims, native_steps=None):
+def bench_batched_loop(fg, model, opt, batch, dims, steps, nbatches=234):
+    """examples/mnist.rs:84-98 as written: a resident training set of
+    `nbatches` whole batches (234 of 256 rows: MNIST's 60,000 images), a new
+    narrow()ed batch every step, run by fg_mlp_train_batches. Synthetic
+    U(0,1) images and one-hot labels; the upload is outside the timing."""
+    from ferrograd_amd.mlp import synthetic_batch, train_batches_native
+
+    xs, ts = synthetic_batch(batch * nbatches, dims[0], dims[-1], 17, 18)
+    x = fg.Tensor.new(xs, list(xs.shape), "hip")
+    t = fg.Tensor.new(ts, list(ts.shape), "hip")
+    train_batches_native(model, opt, x, t, batch, 8)
+    fg.synchronize()
+    s0 = fg.stats()
+    t0 = time.perf_counter()
+    losses = train_batches_native(model, opt, x, t, batch, steps, first_batch=8)
+    fg.synchronize()
+    ms = (time.perf_counter() - t0) * 1000.0 / steps
+    s1 = fg.stats()
+    return {"ms_per_step": ms, "steps_per_s": 1e3 / ms, "steps": steps,
+            "steps_from_capture": s1["steps_replayed"] - s0["steps_replayed"],
+            "dataset_rows": batch * nbatches, "losses_finite": bool(np.all(np.isfinite(losses))),
+            "caller": "fg_mlp_train_batches: examples/mnist.rs:84-98 with batch i = rows narrow(0, 256*i, 256) of a "
+                      "resident [59904, 784] set, one call for all timed steps; captured steps take the batch start "
+                      "as a kernel argument of the replayed graph"}
+
+
+def bench_mlp(fg, ctx, steps, warmup, batch, dims, native_steps=None, batched=False):
     from ferrograd_amd.mlp import mlp_setup, train_steps_native
 
     # The first step runs while the biases still hold allocate()'s zeros (a
@@ -283,6 +309,7 @@ def bench_mlp(fg, ctx, steps, warmup, batch, dims, native_steps=None):
     # first steps record the plans and its last step runs in full).
     replayed = s1["steps_replayed"] - s0["steps_replayed"]
     host = timed.host_ms
+    narrowed = bench_batched_loop(fg, model, opt, batch, dims, native_steps) if batched else None
     kern = by_kernel(prof, steps)
     check = check_mlp_step_on_device(fg, model, opt, x, t, batch, dims)
     check["losses_finite"] = bool(np.all(np.isfinite(losses + native_losses)))
@@ -293,9 +320,11 @@ def bench_mlp(fg, ctx, steps, warmup, batch, dims, native_steps=None):
     flops = mlp_gemm_flops(batch, dims)
     tf = lambda t: flops / (t / 1e3) / 1e12 / FP32_MFMA_PEAK_TFLOPS if t else None  # noqa: E731
     return {"ms_per_step": ms_native, "steps_per_s": 1e3 / ms_native,
-            "caller": "native loop (fg_mlp_train_steps, examples/mnist.rs:84-101 restated, one call for all timed "
-                      "steps; steps after the first repeated ones launch from the step capture as one HIP graph); "
-                      "*_python: the same steps driven op by op from Python",
+            "caller": "native loop on one fixed resident batch (fg_mlp_train_steps: the loop body of "
+                      "examples/mnist.rs:90-98, one call for all timed steps; steps after the first repeated ones "
+                      "launch from the step capture as one HIP graph); *_python: the same steps driven op by op "
+                      "from Python; narrowed_batches: the mnist.rs loop with a new narrow()ed batch every step",
+            "narrowed_batches": narrowed,
             "native_steps": native_steps, "native_steps_from_capture": replayed,
             "ms_per_step_python": ms, "steps_per_s_python": 1e3 / ms,
             "device_ms_per_step": dev_ms, "host_ms_per_step": host_native, "host_ms_per_step_python": host,
@@ -508,8 +537,10 @@ def main():
         # The native call records its capture in its first steps and runs its
         # last in full; 200 steps (about 12 ms) make that a realistic loop's share.
         sec["c4"] = bench_mlp(fg, ctx, args.steps, args.warmup, 256, (784, 128, 10),
-                              native_steps=max(args.steps, 200))
-        log(f"c4: {sec['c4']['steps_per_s']:.1f} steps/s (native loop), {sec['c4']['steps_per_s_python']:.1f} from Python")
+                              native_steps=max(args.steps, 200), batched=True)
+        log(f"c4: {sec['c4']['steps_per_s']:.1f} steps/s (native loop, fixed batch), "
+            f"{sec['c4']['narrowed_batches']['steps_per_s']:.1f} (native loop, narrowed batches), "
+            f"{sec['c4']['steps_per_s_python']:.1f} from Python")
     if "c5" in only:
         sec["c5"] = bench_mlp(fg, ctx, max(3, args.steps // 4), 2, 8192, (784, 4096, 4096, 10))
         log(f"c5: {sec['c5']['steps_per_s']:.2f} steps/s (native loop), {sec['c5']['steps_per_s_python']:.2f} from Python, "

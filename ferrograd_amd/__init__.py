@@ -89,6 +89,8 @@ def _declare(l: ctypes.CDLL) -> None:
         "fg_sgd_zero_grad": (c_int, [P]),
         "fg_sgd_step": (c_int, [P]),
         "fg_mlp_train_steps": (c_int, [P, c_int, P, P, P, c_int, ctypes.POINTER(ctypes.c_float)]),
+        "fg_mlp_train_batches": (c_int, [P, c_int, P, P, P, ctypes.c_int64, ctypes.c_int64, c_int,
+                                         ctypes.POINTER(ctypes.c_float)]),
         "fg_sgd_free": (c_int, [P]),
         "fg_synchronize": (c_int, [c_int]),
         "fg_default_device": (c_int, [ctypes.POINTER(c_int)]),
@@ -451,6 +453,19 @@ def train_steps_native(layers: Sequence[Linear], opt: Sgd, x: Tensor, targets: T
     arr = (ctypes.c_void_p * max(1, len(layers)))(*[l._h.value for l in layers])
     out = (ctypes.c_float * max(1, steps))()
     _check(lib().fg_mlp_train_steps(arr, len(layers), opt._h, x._h, targets._h, int(steps), out))
+    return [float(out[i]) for i in range(steps)]
+
+
+def train_batches_native(layers: Sequence[Linear], opt: Sgd, images: Tensor, targets: Tensor, batch_size: int,
+                         steps: int, first_batch: int = 0) -> list:
+    """fg_mlp_train_batches: the same loop over resident `images` and
+    `targets`, step i on rows narrow(0, s, batch_size) with s = ((first_batch
+    + i) mod (rows // batch_size)) * batch_size (examples/mnist.rs:84-87);
+    the losses."""
+    arr = (ctypes.c_void_p * max(1, len(layers)))(*[l._h.value for l in layers])
+    out = (ctypes.c_float * max(1, steps))()
+    _check(lib().fg_mlp_train_batches(arr, len(layers), opt._h, images._h, targets._h, int(batch_size),
+                                      int(first_batch), int(steps), out))
     return [float(out[i]) for i in range(steps)]
 
 

@@ -323,6 +323,22 @@ int fg_mlp_train_steps(fg_linear* const* layers, int nlayers, fg_sgd* opt, fg_te
   });
 }
 
+int fg_mlp_train_batches(fg_linear* const* layers, int nlayers, fg_sgd* opt, fg_tensor* images, fg_tensor* targets,
+                         int64_t batch_size, int64_t first_batch, int steps, float* losses) {
+  return guard([&] {
+    FG_CHECK(layers && nlayers > 0 && opt && images && targets && (losses || steps == 0),
+             "fg_mlp_train_batches: null argument or no layers");
+    FG_CHECK(batch_size > 0, "fg_mlp_train_batches: batch size must be positive");
+    std::vector<const fg::Linear*> ls;
+    for (int i = 0; i < nlayers; i++) {
+      FG_CHECK(layers[i], "fg_mlp_train_batches: null layer");
+      ls.push_back(&layers[i]->l);
+    }
+    std::vector<float> v = fg::train_steps(ls, opt->s, images->t, targets->t, steps, batch_size, first_batch);
+    std::copy(v.begin(), v.end(), losses);
+  });
+}
+
 int fg_linear_num_params(fg_linear* l, int* n) {
   return guard([&] { *n = static_cast<int>(l->l.parameters().size()); });
 }

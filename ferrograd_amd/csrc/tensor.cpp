@@ -825,7 +825,9 @@ void replay_plan(Device& backend, const GraphKey& k, const std::shared_ptr<Cache
 // earlier kernel of the same step.
 struct CapturedStep {
   struct Arg {
-    enum Kind : uint8_t { Persistent, Output, Value } kind = Value;
+    // StepStart: the start of the step's batch (a narrow() of the inputs
+    // that moves every step), passed in by each replay.
+    enum Kind : uint8_t { Persistent, Output, Value, StepStart } kind = Value;
     Buffer buf;
     uint32_t out = 0;
     KernelArg value;
@@ -846,9 +848,13 @@ struct CapturedStep {
 
 // The capture of step `cur`, given the step before it, or null when the two
 // did not replay the same plans over the same persistent buffers, or when
-// `result` is not one of the step's outputs.
+// `result` is not one of the step's outputs. A Shrink start (a narrow())
+// that has the same value in both steps stays a constant; one that equals
+// each step's batch start (`start_prev`, `start_cur`, which differ) becomes
+// that start on every replay; any other change gives up.
 std::unique_ptr<CapturedStep> capture_step(const std::vector<ReplayRecord>& prev,
-                                           const std::vector<ReplayRecord>& cur, const Buffer& result) {
+                                           const std::vector<ReplayRecord>& cur, const Buffer& result,
+                                           int64_t start_prev = 0, int64_t start_cur = 0) {
   if (cur.empty() || prev.size() != cur.size()) return nullptr;
   auto cap = std::make_unique<CapturedStep>();
   std::unordered_map<const BufferInner*, uint32_t> out_cur, out_prev;  // output buffer -> kernel of the step
@@ -856,7 +862,7 @@ std::unique_ptr<CapturedStep> capture_step(const std::vector<ReplayRecord>& prev
   for (size_t r = 0; r < cur.size(); r++) {
     const ReplayRecord& c = cur[r];
     const ReplayRecord& p = prev[r];
-    if (c.plan != p.plan || c.start_values != p.start_values) return nullptr;
+    if (c.plan != p.plan || c.start_values.size() != p.start_values.size()) return nullptr;
     size_t si = 0;
     for (const PlanKernel& pk : c.plan->kernels) {
       CapturedStep::Kernel k;
@@ -869,7 +875,15 @@ std::unique_ptr<CapturedStep> capture_step(const std::vector<ReplayRecord>& prev
         if (pa.kind == PlanArg::Value) {
           a.value = pa.value;
         } else if (pa.kind == PlanArg::Start) {
-          a.value = KernelArg::i32(c.start_values.at(si++));
+          const int32_t vc = c.start_values.at(si), vp = p.start_values.at(si);
+          si++;
+          if (vc == vp) {
+            a.value = KernelArg::i32(vc);
+          } else if (start_cur != start_prev && vc == start_cur && vp == start_prev) {
+            a.kind = CapturedStep::Arg::StepStart;
+          } else {
+            return nullptr;
+          }
         } else if (pa.kind == PlanArg::Output) {
           a.kind = CapturedStep::Arg::Output;
           a.out = base + pa.index;
@@ -914,7 +928,7 @@ std::unique_ptr<CapturedStep> capture_step(const std::vector<ReplayRecord>& prev
 // Launches every kernel of a captured step as one sequence (a single HIP
 // graph from its second run on), with the step's result (the loss) read back
 // into `slot` (Device::read_async) behind it.
-void replay_step(Device& backend, CapturedStep& cap, int slot) {
+void replay_step(Device& backend, CapturedStep& cap, int slot, int64_t start = 0) {
   const size_t n = cap.kernels.size();
   std::vector<Buffer> outs(n);
   std::vector<Program*> progs(n);
@@ -933,6 +947,7 @@ void replay_step(Device& backend, CapturedStep& cap, int slot) {
     }
     for (const CapturedStep::Arg& a : k.args) {
       if (a.kind == CapturedStep::Arg::Value) args[j].push_back(a.value);
+      else if (a.kind == CapturedStep::Arg::StepStart) args[j].push_back(KernelArg::i32(static_cast<int32_t>(start)));
       else if (a.kind == CapturedStep::Arg::Persistent) args[j].push_back(KernelArg::buf(a.buf));
       else args[j].push_back(KernelArg::buf(outs[a.out]));
     }
@@ -1339,9 +1354,22 @@ void Sgd::step() const {  // optim.rs:60-71
 //   step always runs in full, so the parameters, their gradients and every
 //   live tensor end as after `steps` ordinary steps.
 std::vector<float> train_steps(const std::vector<const Linear*>& layers, const Sgd& opt, const Tensor& x,
-                               const Tensor& targets, int steps) {
+                               const Tensor& targets, int steps, int64_t batch, int64_t first_batch) {
   FG_CHECK(!layers.empty(), "train_steps requires at least one layer");
   FG_CHECK(steps >= 0, "train_steps: negative step count");
+  int64_t num_batches = 0;
+  if (batch > 0) {
+    const Shape& xs = x.shape();
+    const Shape& ts = targets.shape();
+    FG_CHECK(!xs.empty() && !ts.empty() && xs[0] == ts[0],
+             "train_steps: images and targets must have the same number of rows");
+    FG_CHECK(static_cast<int64_t>(xs[0]) >= batch, "train_steps: batch size larger than the dataset");
+    FG_CHECK(first_batch >= 0, "train_steps: negative first batch");
+    num_batches = static_cast<int64_t>(xs[0]) / batch;
+  }
+  // Step i's batch start (mnist.rs:85-87): batches in order, wrapping over
+  // the whole ones as the epochs do.
+  auto start_of = [&](int i) { return batch > 0 ? ((first_batch + i) % num_batches) * batch : int64_t(0); };
   std::vector<float> losses(static_cast<size_t>(steps));
   Device& dev = get_device(x.device());
   // Step i's loss lands in read-back slot i % in_flight and is waited for
@@ -1364,7 +1392,7 @@ std::vector<float> train_steps(const std::vector<const Linear*>& layers, const S
   bool prev_valid = false;
   for (int i = 0; i < steps; i++) {
     if (cap && i + 1 < steps) {
-      replay_step(dev, *cap, slot(i));
+      replay_step(dev, *cap, slot(i), start_of(i));
       realize_stats().steps_replayed++;
       if (i >= in_flight - 1) collect(i - (in_flight - 1));
       continue;
@@ -1372,19 +1400,21 @@ std::vector<float> train_steps(const std::vector<const Linear*>& layers, const S
     StepRecorder rec;
     {
       RecorderScope scope(capture && !cap ? &rec : nullptr);
-      Tensor h = x;
+      Tensor h = batch > 0 ? x.narrow(0, start_of(i), batch) : x;
+      const Tensor t = batch > 0 ? targets.narrow(0, start_of(i), batch) : targets;
       for (size_t l = 0; l < layers.size(); l++) {
         h = layers[l]->forward(h);
         if (l + 1 < layers.size()) h = h.relu();
       }
-      Tensor loss = h.cross_entropy(targets);
+      Tensor loss = h.cross_entropy(t);
       opt.zero_grad();
       loss.backward();
       opt.step();
       Buffer lb = loss.realized_buffer();
       dev.read_async(lb, slot(i));  // the loss's read-back, queued behind the step
       if (capture && !cap) {
-        if (rec.valid && prev_valid && (cap = capture_step(prev, rec.records, lb))) realize_stats().steps_captured++;
+        if (rec.valid && prev_valid && (cap = capture_step(prev, rec.records, lb, start_of(i - 1), start_of(i))))
+          realize_stats().steps_captured++;
         prev = cap ? std::vector<ReplayRecord>() : std::move(rec.records);
         prev_valid = !cap && rec.valid;
       }

@@ -142,9 +142,11 @@ void collect_held_nodes(PtrIndexMap* held, std::vector<const UOpInner*>* list);
 // as a compiled caller of the reference runs it: logits = layers through ReLU
 // between them (mnist.rs:30-54 generalised to any depth), loss =
 // cross_entropy, zero_grad, backward, step, then the loss read back. Returns
-// each step's loss.
+// each step's loss. With `batch` > 0, `x` and `targets` are whole datasets and
+// step i trains on rows [s, s + batch) through narrow(), s = ((first_batch +
+// i) mod (rows / batch)) * batch, as mnist.rs:84-87 batches an epoch.
 std::vector<float> train_steps(const std::vector<const Linear*>& layers, const Sgd& opt, const Tensor& x,
-                               const Tensor& targets, int steps);
+                               const Tensor& targets, int steps, int64_t batch = 0, int64_t first_batch = 0);
 
 // Offline MNIST IDX files (dataset.rs:116-161): images as f32 [count, 784]
 // scaled by 1/255 on `dev`, labels as bytes.

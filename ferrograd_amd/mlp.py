@@ -67,6 +67,17 @@ def train_steps_native(model: Mlp, opt: Sgd, x: Tensor, targets: Tensor, steps: 
     return native(model.layers, opt, x, targets, steps)
 
 
+def train_batches_native(model: Mlp, opt: Sgd, images: Tensor, targets: Tensor, batch_size: int, steps: int,
+                         first_batch: int = 0) -> list:
+    """`steps` train steps over narrow()ed batches of the resident `images`
+    and `targets` (examples/mnist.rs:84-98), batch index first_batch + i
+    wrapping over the whole batches, looped in native code
+    (fg_mlp_train_batches); returns the losses."""
+    from . import train_batches_native as native
+
+    return native(model.layers, opt, images, targets, batch_size, steps, first_batch)
+
+
 def synthetic_batch(batch: int, in_features: int, classes: int, seed_x: int, seed_y: int):
     """x ~ U(0,1) [batch, in]; labels floor(u*classes) one-hot."""
     x = np.random.default_rng(seed_x).uniform(0, 1, (batch, in_features)).astype(np.float32)
@@ -102,11 +113,13 @@ def predictions(logits: np.ndarray) -> np.ndarray:
 
 
 def train_mnist(dataset, device=None, epochs: int = 5, batch_size: int = 256, lr: float = 0.01,
-                max_batches: int | None = None, log=print) -> dict:
+                max_batches: int | None = None, log=print, native: bool = False) -> dict:
     """examples/mnist.rs:59-126 on `device`: Linear(784,128) -> ReLU ->
     Linear(128,10), cross-entropy, SGD; batches are narrow()ed views of the
     resident training set. Returns per-batch losses and per-epoch average loss
-    and test accuracy (percent)."""
+    and test accuracy (percent). With `native`, each epoch's batch loop runs
+    in native code (fg_mlp_train_batches: the same steps, captured and
+    replayed with each batch's start as an argument)."""
     train_targets = Tensor.new(one_hot(dataset.train_labels, dataset.num_classes),
                                [dataset.train_len(), dataset.num_classes], device)
     model = Mlp((784, 128, 10), device)
@@ -120,7 +133,14 @@ def train_mnist(dataset, device=None, epochs: int = 5, batch_size: int = 256, lr
     history = {"batch_loss": [], "epoch_loss": [], "accuracy": []}
     for epoch in range(epochs):
         epoch_loss = np.float32(0.0)
-        for b in range(runs):
+        if native:
+            for b, v in enumerate(train_batches_native(model, opt, dataset.train_images, train_targets, batch_size,
+                                                       runs)):
+                epoch_loss = np.float32(epoch_loss + np.float32(v))
+                history["batch_loss"].append(v)
+                if log:
+                    log(f"  epoch {epoch} batch {b:>4}/{num_batches}  loss={v:.4f}")
+        for b in range(0 if native else runs):
             start = b * batch_size
             x = dataset.train_images.narrow(0, start, batch_size)
             t = train_targets.narrow(0, start, batch_size)

@@ -113,6 +113,13 @@ int fg_linear_free(fg_linear* l);
  * driven call by call. */
 int fg_mlp_train_steps(fg_linear* const* layers, int nlayers, fg_sgd* opt, fg_tensor* x, fg_tensor* targets, int steps,
                        float* losses);
+/* The same loop over a resident dataset, batched as examples/mnist.rs:84-87:
+ * step i trains on rows [s, s + batch_size) of `images` and `targets`
+ * (narrow(0, s, batch_size)), s = ((first_batch + i) mod (rows / batch_size))
+ * * batch_size, so consecutive calls continue through the epochs. Captured
+ * steps take each batch's start as a kernel argument of the replay. */
+int fg_mlp_train_batches(fg_linear* const* layers, int nlayers, fg_sgd* opt, fg_tensor* images, fg_tensor* targets,
+                         int64_t batch_size, int64_t first_batch, int steps, float* losses);
 
 /* optim::Sgd (optim.rs:16-71). */
 int fg_sgd_new(fg_tensor** params, int n, float lr, fg_sgd** out);

@@ -231,6 +231,9 @@ extern "C" {
     pub fn fg_linear_free(l: *mut fg_linear) -> i32;
     pub fn fg_mlp_train_steps(layers: *const *mut fg_linear, nlayers: i32, opt: *mut fg_sgd, x: *mut fg_tensor,
                               targets: *mut fg_tensor, steps: i32, losses: *mut f32) -> i32;
+    pub fn fg_mlp_train_batches(layers: *const *mut fg_linear, nlayers: i32, opt: *mut fg_sgd,
+                                images: *mut fg_tensor, targets: *mut fg_tensor, batch_size: i64,
+                                first_batch: i64, steps: i32, losses: *mut f32) -> i32;
     pub fn fg_sgd_new(params: *mut *mut fg_tensor, n: i32, lr: f32, out: *mut *mut fg_sgd) -> i32;
     pub fn fg_sgd_zero_grad(s: *mut fg_sgd) -> i32;
     pub fn fg_sgd_step(s: *mut fg_sgd) -> i32;

@@ -126,3 +126,84 @@ def test_native_loop_matches_python_loop_hip(fg, cpu, batch, dims):
     assert np.allclose(l_rec, l_nat, rtol=1e-6)
     l_cpu, _ = run(fg, cpu, dims, batch, 9, native=True)
     assert np.allclose(l_nat, l_cpu, rtol=1e-4, atol=1e-6)
+
+
+def run_batches(fg, dev, dims, batch, nbatches, steps, native, chunks=None, first=0):
+    """examples/mnist.rs:84-98 over a resident dataset of `nbatches` batches:
+    step i narrows batch (first + i) mod nbatches. Losses, then parameters and
+    the last step's gradients."""
+    from ferrograd_amd.mlp import Mlp, synthetic_batch, train_batches_native, train_step
+
+    fg.reset_init_seed(42)
+    model = Mlp(dims, dev)
+    opt = fg.Sgd(model.parameters(), 0.01)
+    # one row more than the whole batches: the remainder is never trained on
+    xs, ts = synthetic_batch(batch * nbatches + 1, dims[0], dims[-1], 7, 8)
+    x = fg.Tensor.new(xs, list(xs.shape), dev)
+    t = fg.Tensor.new(ts, list(ts.shape), dev)
+    if native:
+        losses, done = [], first
+        for n in chunks or [steps]:
+            losses += train_batches_native(model, opt, x, t, batch, n, first_batch=done)
+            done += n
+    else:
+        losses = []
+        for i in range(steps):
+            s = ((first + i) % nbatches) * batch
+            losses.append(train_step(model, opt, x.narrow(0, s, batch), t.narrow(0, s, batch)).to_vec()[0])
+    params = model.parameters()
+    return losses, [p.numpy() for p in params] + [p.grad().numpy() for p in params]
+
+
+@pytest.mark.parametrize("dims", [(16, 8, 4), (12, 16, 8, 5)])
+def test_native_batched_loop_matches_python_loop_cpu(fg, cpu, dims):
+    # 14 steps over 6 batches (every start taken, then wrapping): from the
+    # third step on, the steps replay the capture with their own batch start.
+    # Bit for bit against the narrow()ed loop driven from Python, also when
+    # entered in chunks that continue from the previous call's batch.
+    before = fg.stats()
+    l_py, p_py = run_batches(fg, cpu, dims, 8, 6, 14, native=False)
+    l_nat, p_nat = run_batches(fg, cpu, dims, 8, 6, 14, native=True)
+    assert fg.stats()["steps_replayed"] - before["steps_replayed"] >= 10
+    assert l_nat == l_py and len(set(l_py)) == 14
+    assert all(np.array_equal(a, b) for a, b in zip(p_nat, p_py))
+    l_ch, p_ch = run_batches(fg, cpu, dims, 8, 6, 14, native=True, chunks=[5, 1, 8])
+    assert l_ch == l_py and all(np.array_equal(a, b) for a, b in zip(p_ch, p_py))
+    l_f, _ = run_batches(fg, cpu, dims, 8, 6, 5, native=False, first=4)
+    l_fn, _ = run_batches(fg, cpu, dims, 8, 6, 5, native=True, first=4)
+    assert l_f == l_fn
+
+
+def test_native_batched_loop_errors(fg, cpu):
+    from ferrograd_amd.mlp import Mlp
+
+    model = Mlp((4, 3), cpu)
+    opt = fg.Sgd(model.parameters(), 0.01)
+    x = fg.Tensor.new(np.ones((10, 4), np.float32), [10, 4], cpu)
+    t = fg.Tensor.new(np.ones((9, 3), np.float32), [9, 3], cpu)
+    with pytest.raises(fg.FerrogradError, match="same number of rows"):
+        fg.train_batches_native(model.layers, opt, x, t, 2, 1)
+    t = fg.Tensor.new(np.ones((10, 3), np.float32), [10, 3], cpu)
+    with pytest.raises(fg.FerrogradError, match="batch size larger than the dataset"):
+        fg.train_batches_native(model.layers, opt, x, t, 11, 1)
+    with pytest.raises(fg.FerrogradError, match="batch size must be positive"):
+        fg.train_batches_native(model.layers, opt, x, t, 0, 1)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("batch,dims", [(256, (784, 128, 10)), (64, (96, 64, 32, 10))])
+def test_native_batched_loop_matches_python_loop_hip(fg, cpu, batch, dims):
+    # The mnist.rs loop with a new batch every step: captured steps take the
+    # batch start as a changed kernel argument of the replayed graph.
+    print(f"batched native loop B={batch} dims={dims}", flush=True)
+    l_py, p_py = run_batches(fg, "hip", dims, batch, 7, 16, native=False)
+    before = fg.stats()
+    l_nat, p_nat = run_batches(fg, "hip", dims, batch, 7, 16, native=True)
+    # steps 4 to 14: steps 0-3 record (zero biases, then the steady plan twice), 15 runs in full
+    assert fg.stats()["steps_replayed"] - before["steps_replayed"] >= 11
+    assert l_nat == l_py
+    assert all(np.array_equal(a, b) for a, b in zip(p_nat, p_py))
+    l_ch, p_ch = run_batches(fg, "hip", dims, batch, 7, 16, native=True, chunks=[3, 13])
+    assert l_ch == l_py and all(np.array_equal(a, b) for a, b in zip(p_ch, p_py))
+    l_cpu, _ = run_batches(fg, cpu, dims, batch, 7, 16, native=True)
+    assert np.allclose(l_nat, l_cpu, rtol=1e-4, atol=1e-6)
