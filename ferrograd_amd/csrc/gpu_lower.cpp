@@ -1571,6 +1571,31 @@ GemmTile choose_gemm_tile(int64_t M, int64_t N, int64_t K) {
   return best;
 }
 
+constexpr int64_t kSmallGemmMaxWork = int64_t(1) << 26;  // M*N*K
+constexpr int kSmallGemmMaxGroups = 4;                   // 16-k groups per wave
+
+bool small_gemm_fits(int64_t M, int64_t N, int64_t K) {
+  GemmTile forced;
+  if (gemm_tile_override(&forced)) return false;
+  return M * N * K <= kSmallGemmMaxWork;
+}
+
+// Waves per workgroup: enough that no wave folds more than G groups of 16 k
+// (kSmallGemmMaxGroups; FG_SMALL_GEMM_GROUPS overrides it for tuning, read
+// once), at most 16 (1024 threads).
+int small_gemm_waves(int64_t K) {
+  static const int64_t G = [] {
+    const char* e = std::getenv("FG_SMALL_GEMM_GROUPS");
+    if (!e || !*e) return static_cast<int64_t>(kSmallGemmMaxGroups);
+    char* end = nullptr;
+    const long v = std::strtol(e, &end, 10);
+    FG_CHECK(*end == '\0' && v >= 1 && v <= 64, std::string("FG_SMALL_GEMM_GROUPS must be 1 to 64; got '") + e + "'");
+    return static_cast<int64_t>(v);
+  }();
+  const int64_t kg = (K + 15) / 16;
+  return static_cast<int>(std::min<int64_t>(16, std::max<int64_t>(1, (kg + G - 1) / G)));
+}
+
 bool match_gemm(const KernelInfo& ki, GemmMatch* g) {
   if (ki.reduces.size() != 1 || ki.out_ranges.size() != 2) return false;
   const UOp& R = ki.reduces[0];
@@ -1597,6 +1622,7 @@ bool match_gemm(const KernelInfo& ki, GemmMatch* g) {
   g->N = range_extent(g->rn);
   g->K = range_extent(rk);
   if (std::min(g->M, g->N) < 8 || g->M * g->N * g->K < (1LL << 18)) return false;
+  if (small_gemm_fits(g->M, g->N, g->K)) return true;
   if (g->M <= 32 || g->N <= 32) {
     // A narrow product pays for a 32-wide MFMA tile only when the grid fills
     // the chip; otherwise the row and column reductions serve it better.
@@ -1604,6 +1630,121 @@ bool match_gemm(const KernelInfo& ki, GemmMatch* g) {
     if (((g->M + t.BM - 1) / t.BM) * ((g->N + t.BN - 1) / t.BN) * t.S < 128) return false;
   }
   return true;
+}
+
+// ── Small GEMM: one pass, the K range split over the waves of a workgroup ──
+// A product too small to fill the chip with whole tiles (an MLP's 784->128
+// layer at batch 256: 256x128, K 784) otherwise runs split-K: a partial pass
+// plus a finishing pass, two launches of a few microseconds each, most of it
+// launch and memory latency. Here each workgroup owns one 16x16 output tile
+// (v_mfma_f32_16x16x4f32) and its W waves each fold a contiguous share of the
+// K range, in groups of 16 k (four MFMAs: in step u, lane l supplies k =
+// 16g + 4*(l/16) + u of row l%16, the same k for both operands, so a
+// k-contiguous operand's four steps are one lane's four consecutive floats).
+// A wave first loads all of its operands, evaluating the operand expressions
+// (relu masks, transposed views) on them, then runs its MFMAs. The W partial
+// tiles meet in LDS and are summed in wave order by one thread per output,
+// which then runs the epilogue (bias, relu mask, SGD update). One launch, no
+// scratch, a fixed fold order.
+RenderedKernel render_small_gemm(const KernelInfo& ki, const GemmMatch& g, const std::string& name) {
+  const int64_t M = g.M, N = g.N, K = g.K;
+  const int64_t KG = (K + 15) / 16, ntm = (M + 15) / 16, ntn = (N + 15) / 16;
+  const int W = small_gemm_waves(K);
+  const int64_t GMAX = (KG + W - 1) / W;  // groups the busiest wave folds
+  const int NT = 64 * W;
+  std::ostringstream s;
+  s << kPrelude;
+  s << signature(ki, name, NT) << " {\n";
+  s << "  __shared__ float fg_part[" << W << "][256];\n";
+  s << "  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, q = lane >> 4, r16 = lane & 15;\n";
+  s << "  const int tm = (int)(blockIdx.x / " << ntn << "), tn = (int)(blockIdx.x % " << ntn << ");\n";
+  s << "  const int m0 = tm * 16, n0 = tn * 16;\n";
+  // This wave's groups of 16 k: [gbeg, gend).
+  s << "  const int gbeg = (int)(((long)wave * " << KG << ") / " << W << "), gend = (int)(((long)(wave + 1) * " << KG
+    << ") / " << W << ");\n";
+  s << "  const int am = m0 + r16 < " << M << " ? m0 + r16 : " << (M - 1) << ";\n";
+  s << "  const int bn = n0 + r16 < " << N << " ? n0 + r16 : " << (N - 1) << ";\n";
+  s << "  const bool arow = m0 + r16 < " << M << ", brow = n0 + r16 < " << N << ";\n";
+  s << "  float av[" << GMAX << "][4], bv[" << GMAX << "][4];\n";
+  // Loads of every group first (all in flight together), then the MFMAs.
+  Emitter em;
+  em.define_range(g.a.rout, "am");
+  em.define_range(g.b.rout, "bn");
+  em.open_scope("#pragma unroll\nfor (int gi = 0; gi < " + std::to_string(GMAX) + "; gi++) {", "}");
+  em.line("const int kb = (gbeg + gi) * 16 + 4 * q;");
+  em.line("const bool gin = gbeg + gi < gend;");
+  if (K % 4 == 0) {
+    // A lane's four k are all in range or all out: one clamped base, and the
+    // four steps as lanes of that base (16-byte loads where k is unit-stride).
+    em.line("const bool kin = gin && kb < " + std::to_string(K) + ";");
+    em.line("const int kc = kin ? kb : 0;");
+    em.define_range(g.rk, "kc");
+    em.set_lane_range(g.rk, 4);
+    for (int u = 0; u < 4; u++) {
+      const std::string a = em.val(g.a.expr, u), b = em.val(g.b.expr, u);
+      em.line("av[gi][" + std::to_string(u) + "] = (kin && arow) ? " + a + " : 0.0f;");
+      em.line("bv[gi][" + std::to_string(u) + "] = (kin && brow) ? " + b + " : 0.0f;");
+    }
+    em.clear_lane_range();
+  } else {
+    for (int u = 0; u < 4; u++) {
+      em.open_scope("{", "}");
+      em.line("const bool kin = gin && kb + " + std::to_string(u) + " < " + std::to_string(K) + ";");
+      em.line("const int kc = kin ? kb + " + std::to_string(u) + " : 0;");
+      em.define_range(g.rk, "kc");
+      const std::string a = em.val(g.a.expr, 0), b = em.val(g.b.expr, 0);
+      em.line("av[gi][" + std::to_string(u) + "] = (kin && arow) ? " + a + " : 0.0f;");
+      em.line("bv[gi][" + std::to_string(u) + "] = (kin && brow) ? " + b + " : 0.0f;");
+      em.close_scope();
+    }
+  }
+  em.close_scope();
+  s << em.code();
+  s << R"(  fg_f4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+  #pragma unroll
+  for (int gi = 0; gi < GMAX_; gi++)
+    #pragma unroll
+    for (int u = 0; u < 4; u++) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av[gi][u], bv[gi][u], acc, 0, 0, 0);
+  // D[4*(lane/16) + e][lane%16] = acc[e]
+  #pragma unroll
+  for (int e = 0; e < 4; e++) fg_part[wave][(4 * q + e) * 16 + r16] = acc[e];
+  __syncthreads();
+  for (int o = tid; o < 256; o += 64 * W_) {
+  float sum = fg_part[0][o];
+  #pragma unroll
+  for (int w = 1; w < W_; w++) sum = sum + fg_part[w][o];
+  const int grow = m0 + (o >> 4), gcol = n0 + (o & 15);
+  if (grow < M_ && gcol < N_) {
+)";
+  {
+    Emitter ep;
+    ep.define_range(g.rm, "grow");
+    ep.define_range(g.rn, "gcol");
+    ep.reduce_cb_ = [&](const UOp& RR, int) -> std::string {
+      FG_CHECK(RR == g.R, "gemm epilogue sees one reduction");
+      return "sum";
+    };
+    std::string v = ep.val(ki.value, 0);
+    ep.line(pname(ki.out_param) + "[" + ep.idx(ki.out_index, 0) + "] = " + v + ";");
+    s << ep.code();
+  }
+  s << "  }\n  }\n}\n";
+  std::string src = s.str();
+  auto def = [&](const std::string& k, int64_t v) {
+    const std::string d = "#define " + k + " " + std::to_string(v) + "\n";
+    src.insert(src.find("extern \"C\""), d);
+  };
+  def("GMAX_", GMAX);
+  def("W_", W);
+  def("M_", M);
+  def("N_", N);
+  RenderedKernel rk;
+  rk.name = name;
+  rk.kind = kernel_class_name(KernelClass::Gemm);
+  rk.source = src;
+  rk.block[0] = static_cast<unsigned>(NT);
+  rk.grid[0] = static_cast<unsigned>(ntm * ntn);
+  return rk;
 }
 
 // Helpers of the generated GEMM: vector types for 1/2/4 operands per LDS read
@@ -1751,6 +1892,7 @@ std::string gemm_stream_k(std::string src) {
 }
 
 RenderedKernel render_gemm(const KernelInfo& ki, const GemmMatch& g, const std::string& name) {
+  if (small_gemm_fits(g.M, g.N, g.K)) return render_small_gemm(ki, g, name);
   const int64_t M = g.M, N = g.N, K = g.K;
   const GemmTile tile = choose_gemm_tile(M, N, K);
   const int BM = tile.BM, BN = tile.BN, BK = tile.BK, WGM = tile.WGM, WGN = tile.WGN, NT = tile.nt();
@@ -2911,8 +3053,14 @@ KernelClass base_class(const UOp& kernel) {
   GemmMatch g;
   const GpuPasses& on = gpu_passes();
   if ((on.mfma || on.narrow) && match_gemm(ki, &g)) {
+    // A narrow product whose wide operand streams along k runs in one pass
+    // as VALU rows; otherwise a small product takes the one-pass small GEMM
+    // before the narrow columns' two passes.
     NarrowPlan np;
-    if (on.narrow && narrow_plan(g, &np)) return KernelClass::NarrowGemm;
+    const bool narrow = on.narrow && narrow_plan(g, &np);
+    if (narrow && np.rows) return KernelClass::NarrowGemm;
+    if (on.mfma && small_gemm_fits(g.M, g.N, g.K)) return KernelClass::Gemm;
+    if (narrow) return KernelClass::NarrowGemm;
     if (on.mfma) return KernelClass::Gemm;
   }
   const UOp& R = ki.reduces[0];

@@ -54,9 +54,9 @@ def test_c3_is_one_mfma_gemm_reading_w_directly(fg, cpu):
     # matmul's permute(...).contiguous() of Wᵀ is a copy of W in W's own order
     # (tensor.rs:771-777): the GEMM reads W itself; the reference partition
     # keeps the copy kernel.
-    x = fg.Tensor.new(np.ones((256, 256), np.float32), [256, 256], cpu)
-    w = fg.Tensor.new(np.ones((256, 256), np.float32), [256, 256], cpu)
-    b = fg.Tensor.new(np.ones(256, np.float32), [256], cpu)
+    x = fg.Tensor.new(np.ones((512, 512), np.float32), [512, 512], cpu)
+    w = fg.Tensor.new(np.ones((512, 512), np.float32), [512, 512], cpu)
+    b = fg.Tensor.new(np.ones(512, np.float32), [512], cpu)
     y = x.matmul(w.permute([1, 0])).add(b)
     items = hip_plan(fg, [y])
     assert [it["class"] for it in items] == ["gemm_mfma_f32"]
@@ -66,22 +66,27 @@ def test_c3_is_one_mfma_gemm_reading_w_directly(fg, cpu):
     compile_only(fg, src, items[0]["name"])
 
 
-@pytest.mark.parametrize("mnk,split", [((256, 128, 784), True), ((100, 20, 8192), True), ((4096, 4096, 64), False),
-                                       ((256, 10, 128), False)])
-def test_short_grid_and_narrow_gemms_split_k(fg, cpu, mnk, split):
+@pytest.mark.parametrize("mnk,kind", [((256, 128, 784), "small"), ((100, 20, 8192), "small"),
+                                      ((128, 10, 256), "small"), ((128, 784, 256), "small"),
+                                      ((4096, 4096, 64), "whole"), ((1024, 20, 8192), "split"),
+                                      ((2048, 64, 2048), "split")])
+def test_gemm_forms_by_size(fg, cpu, mnk, kind):
+    # Up to M*N*K = 2^26 (an MLP's layers at batch 256): one pass of 16x16
+    # tiles with K split over the workgroup's waves, no scratch. Larger
+    # products: 32x32 MFMA tiles, split-K (or stream-K) with a finishing pass
+    # when whole tiles would not fill the chip.
     m, n, k = mnk
     x = fg.Tensor.new(np.ones((m, k), np.float32), [m, k], cpu)
     w = fg.Tensor.new(np.ones((n, k), np.float32), [n, k], cpu)
     items = hip_plan(fg, [x.matmul(w.permute([1, 0]))])
     gemm = [it for it in items if it["class"] == "gemm_mfma_f32"]
-    if (m, n, k) == (256, 10, 128):
-        # Too small a grid for a 32-wide tile: stays a row reduction (2560
-        # outputs of 128 terms are too much work for one workgroup).
-        assert not gemm and items[-1]["class"] == "row_reduce"
-        return
     assert len(gemm) == 1
     src = gemm[0]["source"]
-    assert ("_part(" in src and "_fin(" in src and "fg_scratch" in src) == split
+    split = "_part(" in src and "_fin(" in src and "fg_scratch" in src
+    small = "__builtin_amdgcn_mfma_f32_16x16x4f32" in src and "fg_part[" in src
+    assert (kind == "small") == small and (kind == "split") == split, (small, split)
+    if kind == "small":
+        assert gemm[0]["grid"] == [((m + 15) // 16) * ((n + 15) // 16), 1, 1]
     compile_only(fg, src, gemm[0]["name"] + ("_part" if split else ""))
 
 
@@ -123,8 +128,8 @@ def test_narrowed_operands_stay_on_mfma_with_vector_loads(fg, cpu):
     gemm = [it for it in items if it["class"] == "gemm_mfma_f32"]
     assert len(gemm) == 1
     src = gemm[0]["source"]
-    assert "*(const fg_f4*)(data" in src and "_part(" in src
-    compile_only(fg, src, gemm[0]["name"] + "_part")
+    assert "*(const fg_f4*)(data" in src and "_part(" not in src and "*784)" in src
+    compile_only(fg, src, gemm[0]["name"])
 
 
 def test_in_place_update_reading_other_indices_runs_sequentially(fg, cpu):

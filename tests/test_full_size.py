@@ -50,8 +50,8 @@ def test_c3_full_size_sampled_rows(fg, hip):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("batch", [1024, 8192])
-def test_wide_mlp_train_step_product_by_product(fg, hip, batch):
+@pytest.mark.parametrize("batch,lr", [(1024, 0.01), (8192, 0.01), (8192, 1.0)])
+def test_wide_mlp_train_step_product_by_product(fg, hip, batch, lr):
     """One C5 train step (784 -> 4096 -> 4096 -> 10) at the benched B=8192 and
     at 1024, where the GEMM tile and split-K choices differ (choose_gemm_tile
     picks them from M, N and K). The step's own pre-activations are read from
@@ -60,11 +60,17 @@ def test_wide_mlp_train_step_product_by_product(fg, hip, batch):
     logits, and each parameter's effective gradient (p0 - p1)/lr against
     float64 backward products on the device's forward values, for sampled
     rows of W1 and W2 and all of W3 and every bias
-    (tests/f64ref.py: check_mlp_step)."""
+    (tests/f64ref.py: check_mlp_step).
+
+    The effective gradient carries the update's own rounding, ulp(p1)/lr:
+    at lr 0.01 that term dominates the bound for W1 and W2 (|p| about 0.05).
+    At lr 1 it is 100 times smaller, so the fused weight-gradient + SGD
+    kernels are held to the 1e-4 * sum|terms| of their products."""
     import f64ref
     from ferrograd_amd.mlp import Mlp, synthetic_batch
 
-    dims, lr = (784, 4096, 4096, 10), 0.01
+    print(f"C5 step B={batch} lr={lr}", flush=True)
+    dims = (784, 4096, 4096, 10)
     xs, ts = synthetic_batch(batch, dims[0], dims[-1], 9, 10)
     fg.reset_init_seed(42)
     model = Mlp(dims, hip)

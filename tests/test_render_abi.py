@@ -25,7 +25,7 @@ from conftest import rel_err_bound, seeded
 
 
 HOST = {"x": (64, 96), "w": (48, 96), "b": (48,), "a": (1000,), "bb": (1000,), "c": (1000,), "tall": (8192, 64),
-        "g": (2048, 128), "h": (2048, 96)}
+        "g": (8192, 128), "h": (8192, 96), "gs": (2048, 128), "hs": (2048, 80)}
 
 
 def host_arrays():
@@ -44,7 +44,10 @@ def programs(fg, dev):
     s0, s1 = fg.Tensor.scalar(0.5, dev), fg.Tensor.scalar(1.0, dev)
     wg = fg.Tensor.new(np.zeros((128, 96), np.float32), [128, 96], dev).with_requires_grad(True)
     loss = T["h"].matmul(wg.permute([1, 0])).mul(T["g"]).sum([0, 1])
-    (dw,) = loss.gradient([wg])  # dW = gᵀ·h, K = 2048: split over K
+    (dw,) = loss.gradient([wg])  # dW = gᵀ·h, K = 8192: split over K
+    ws = fg.Tensor.new(np.zeros((128, 80), np.float32), [128, 80], dev).with_requires_grad(True)
+    loss_s = T["hs"].matmul(ws.permute([1, 0])).mul(T["gs"]).sum([0, 1])
+    (dws,) = loss_s.gradient([ws])  # K = 2048: the one-pass small GEMM
     half, one = np.array([0.5], np.float32), np.array([1.0], np.float32)
     return {
         "c1": (T["x"].mul(s0).add(s1).relu().sum([1]), [H["x"], half, one]),
@@ -52,6 +55,7 @@ def programs(fg, dev):
         "c3": (T["x"].matmul(T["w"].permute([1, 0])).add(T["b"]), [H["x"], H["w"], H["b"]]),
         "colsum_split": (T["tall"].sum([0]), [H["tall"]]),
         "dw_split_k": (dw, None),  # inputs g and h, matched by size
+        "dw_small": (dws, None),  # inputs gs and hs, matched by size
     }
 
 
@@ -79,6 +83,11 @@ def test_kernel_text_round_trip_reproduces_the_rendering(fg, cpu):
     # A column sum too long for one workgroup: split into partials and a finishing pass.
     cols = fg.Tensor.new(np.ones((4096, 512), np.float32), [4096, 512], cpu)
     items += fg.debug_plan([cols.sum([0])], fuse=True, render_hip=True)["items"]
+    # A product above the one-pass small-GEMM size with too few tiles for the
+    # chip: split-K partials and a finishing pass.
+    a = fg.Tensor.new(np.ones((2048, 2048), np.float32), [2048, 2048], cpu)
+    w = fg.Tensor.new(np.ones((64, 2048), np.float32), [64, 2048], cpu)
+    items += fg.debug_plan([a.matmul(w.permute([1, 0]))], fuse=True, render_hip=True)["items"]
     kinds = set()
     for it in items:
         r = Rendered(it["kernel"])
@@ -200,7 +209,7 @@ def run_rendered(ctx, text, inputs, out_numel):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("name", ["c1", "c2", "c3", "colsum_split", "dw_split_k"])
+@pytest.mark.parametrize("name", ["c1", "c2", "c3", "colsum_split", "dw_split_k", "dw_small"])
 def test_rendered_kernels_run_and_match_the_oracle(fg, cpu, hip, name):
     from ferrograd_amd.hip import Context
 
@@ -209,13 +218,15 @@ def test_rendered_kernels_run_and_match_the_oracle(fg, cpu, hip, name):
     (it,) = plan(fg, root)
     want = root.numpy().reshape(-1)  # realised on the oracle
     if inputs is None:
-        inputs = {H[k].size: H[k] for k in ("g", "h")}
+        inputs = {H[k].size: H[k] for k in (("gs", "hs") if name == "dw_small" else ("g", "h"))}
     got, r = run_rendered(Context.of_device(), it["kernel"], inputs, want.size)
     if name == "c2":
         assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
         return
     if name in ("colsum_split", "dw_split_k"):
         assert r.scratch_bytes > 0 and len(r.launches) == 2
+    if name == "dw_small":
+        assert r.scratch_bytes == 0 and len(r.launches) == 1 and "mfma_f32_16x16x4f32" in r.source
     # Reductions and products: 1e-4 of sum |terms| against the oracle.
     f64 = {k: v.astype(np.float64) for k, v in H.items()}
     scale = {
@@ -223,6 +234,7 @@ def test_rendered_kernels_run_and_match_the_oracle(fg, cpu, hip, name):
         "c3": lambda: np.abs(f64["x"]) @ np.abs(f64["w"]).T + np.abs(f64["b"]),
         "colsum_split": lambda: np.abs(f64["tall"]).sum(0),
         "dw_split_k": lambda: np.abs(f64["g"]).T @ np.abs(f64["h"]),
+        "dw_small": lambda: np.abs(f64["gs"]).T @ np.abs(f64["hs"]),
     }[name]().reshape(-1)
     assert rel_err_bound(got, want, scale, 1e-4) <= 1.0
 

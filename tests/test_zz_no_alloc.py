@@ -66,8 +66,8 @@ def test_noalloc_matches_kernel_run_on_two_calls(fg, hip):
     ctx = Context.of_device()
     results = []
     # First call: 32 MiB of split-K partials; second: a smaller problem
-    # (4 MiB), run over the first call's leftovers.
-    for (B, M, N, seed) in ((8192, 512, 256, 1), (2048, 256, 128, 2)):
+    # (8 MiB), run over the first call's leftovers.
+    for (B, M, N, seed) in ((8192, 512, 256, 1), (4096, 256, 128, 2)):
         r, text, g, h = dw_kernel(fg, B, M, N, seed)
         assert 0 < r.scratch_bytes <= FG_NOALLOC_SCRATCH_BYTES and len(r.launches) == 2
         outs = run_both(ctx, fg, r, text, g, h, M, N)
