@@ -35,11 +35,22 @@ class FerrogradError(RuntimeError):
     """An error reported by the native library (the reference panics here)."""
 
 
+# The hot Tensor methods live in the CPython extension `_fgc` (csrc/pymodule.c),
+# which links the native library. Until it is built (python -m
+# ferrograd_amd.build) the package imports, and lib() refuses to run.
+try:
+    from . import _fgc
+except ImportError as _fgc_missing:  # noqa: F841
+    _fgc = None
+else:
+    _fgc.set_error_class(FerrogradError)
+
+
 def lib() -> ctypes.CDLL:
     """Load (once) and return the native library."""
     global _lib
     if _lib is None:
-        if not os.path.exists(LIB_PATH):
+        if not os.path.exists(LIB_PATH) or _fgc is None:
             raise FerrogradError(f"native library not built: {LIB_PATH} (run python -m ferrograd_amd.build)")
         l = ctypes.CDLL(LIB_PATH, mode=ctypes.RTLD_GLOBAL)
         _declare(l)
@@ -153,28 +164,23 @@ def _dtype_code(dtype) -> int:
     raise FerrogradError(f"unsupported dtype {dtype!r}")
 
 
-class Tensor:
-    """A lazily evaluated tensor (tensor.rs:95-97). Handles alias shared state."""
+class Tensor(_fgc.TensorBase if _fgc is not None else object):
+    """A lazily evaluated tensor (tensor.rs:95-97). Handles alias shared state.
 
-    __slots__ = ("_h", "__weakref__")
+    The handle (`_h`, an int) and the graph-building ops (unary, binary,
+    reductions, movement, narrow, log_softmax, realize, assign, alias) come
+    from the extension type; `Tensor(handle)` adopts a handle the C-ABI
+    returned."""
 
-    def __init__(self, handle: int):
-        self._h = ctypes.c_void_p(handle)
-
-    def __del__(self):
-        if _lib is not None and self._h:
-            _lib.fg_tensor_free(self._h)
+    __slots__ = ()
 
     @staticmethod
     def _out(fn, *args) -> "Tensor":
-        # Hot path of every op: one ctypes call, and the returned handle
-        # object becomes the tensor's handle as is.
+        # One ctypes call that returns a new handle through its last argument.
         out = ctypes.c_void_p()
         if fn(*args, ctypes.byref(out)):
             raise FerrogradError(_lib.fg_last_error().decode())
-        t = Tensor.__new__(Tensor)
-        t._h = out
-        return t
+        return _fgc.from_handle(Tensor, out.value)
 
     # ── construction (tensor.rs:260-312) ─────────────────────────────────
     @staticmethod
@@ -254,10 +260,6 @@ class Tensor:
         _check(lib().fg_tensor_set_requires_grad(self._h, int(requires_grad)))
         return self
 
-    def alias(self) -> "Tensor":
-        """A second handle to the same tensor identity (a Rust `clone`)."""
-        return Tensor._out(lib().fg_tensor_unary, self._h, 10)
-
     def data_ptr(self) -> tuple:
         """(device pointer, byte size) of a realised tensor's storage."""
         p, n = ctypes.c_void_p(), ctypes.c_size_t()
@@ -269,62 +271,10 @@ class Tensor:
         _check(lib().fg_tensor_same(self._h, other._h, ctypes.byref(s)))
         return bool(s.value)
 
-    # ── elementwise (tensor.rs:442-531) ──────────────────────────────────
-    # A Tensor exists only once the library is loaded, so its methods use
-    # `_lib` directly.
-    def _u(self, op: int) -> "Tensor":
-        return Tensor._out(_lib.fg_tensor_unary, self._h, op)
-
-    def _b(self, other: "Tensor", op: int) -> "Tensor":
-        return Tensor._out(_lib.fg_tensor_binary, self._h, other._h, op)
-
-    def neg(self): return self._u(0)
-    def reciprocal(self): return self._u(1)
-    def exp2(self): return self._u(2)
-    def log2(self): return self._u(3)
-    def sqrt(self): return self._u(4)
-    def relu(self): return self._u(5)
-    def exp(self): return self._u(6)
-    def log(self): return self._u(7)
-    def contiguous(self): return self._u(8)
-    def detach(self): return self._u(9)
-    def add(self, o): return self._b(o, 0)
-    def mul(self, o): return self._b(o, 1)
-    def sub(self, o): return self._b(o, 2)
-    def matmul(self, o): return self._b(o, 3)
-    def cross_entropy(self, targets): return self._b(targets, 4)
-
-    # ── movement / reductions (tensor.rs:539-752) ────────────────────────
-    def reshape(self, shape):
-        s, n = _i64(shape)
-        return Tensor._out(_lib.fg_tensor_movement, self._h, 0, s, n)
-
-    def permute(self, order):
-        s, n = _i64(order)
-        return Tensor._out(_lib.fg_tensor_movement, self._h, 1, s, n)
-
-    def expand(self, shape):
-        s, n = _i64(shape)
-        return Tensor._out(_lib.fg_tensor_movement, self._h, 2, s, n)
-
-    def narrow(self, dim: int, start: int, length: int):
-        return Tensor._out(lib().fg_tensor_narrow, self._h, dim, start, length)
-
-    def sum(self, axes):
-        s, n = _i64(axes)
-        return Tensor._out(_lib.fg_tensor_reduce, self._h, 0, s, n)
-
-    def max(self, axes):
-        s, n = _i64(axes)
-        return Tensor._out(lib().fg_tensor_reduce, self._h, 1, s, n)
-
-    def log_softmax(self, axis: int):
-        return Tensor._out(lib().fg_tensor_log_softmax, self._h, axis)
-
-    # ── in-place (tensor.rs:399-440) ─────────────────────────────────────
-    def assign(self, other: "Tensor") -> "Tensor":
-        _check(lib().fg_tensor_assign(self._h, other._h))
-        return self
+    # ── ops (tensor.rs:442-778): neg, reciprocal, exp2, log2, sqrt, relu, exp,
+    # log, contiguous, detach, add, mul, sub, matmul, cross_entropy, reshape,
+    # permute, expand, narrow, sum, max, log_softmax, assign and realize are
+    # the extension type's methods (csrc/pymodule.c).
 
     def replace(self, other: "Tensor") -> "Tensor":
         _check(lib().fg_tensor_replace(self._h, other._h))
@@ -333,13 +283,8 @@ class Tensor:
     # ── realisation (tensor.rs:781-930) ──────────────────────────────────
     @staticmethod
     def realize_many(tensors: Sequence["Tensor"]) -> None:
-        arr = (ctypes.c_void_p * max(1, len(tensors)))(*[t._h.value for t in tensors])
+        arr = (ctypes.c_void_p * max(1, len(tensors)))(*[t._h for t in tensors])
         _check(lib().fg_tensor_realize_many(arr, len(tensors)))
-
-    def realize(self) -> "Tensor":
-        if _lib.fg_tensor_realize_many(ctypes.byref(self._h), 1):  # a one-element fg_tensor* array
-            raise FerrogradError(_lib.fg_last_error().decode())
-        return self
 
     def numpy(self) -> np.ndarray:
         code = self.dtype
@@ -379,17 +324,17 @@ class Tensor:
     def grad(self) -> "Tensor | None":
         out = ctypes.c_void_p()
         _check(lib().fg_tensor_grad(self._h, ctypes.byref(out)))
-        return Tensor(out.value) if out.value else None
+        return _fgc.from_handle(Tensor, out.value) if out.value else None
 
     def backward(self) -> None:
         _check(lib().fg_tensor_backward(self._h))
 
     def gradient(self, targets: Sequence["Tensor"]) -> list:
         n = len(targets)
-        ins = (ctypes.c_void_p * max(1, n))(*[t._h.value for t in targets])
+        ins = (ctypes.c_void_p * max(1, n))(*[t._h for t in targets])
         outs = (ctypes.c_void_p * max(1, n))()
         _check(lib().fg_tensor_gradient(self._h, ins, n, outs))
-        return [Tensor(outs[i]) for i in range(n)]
+        return [_fgc.from_handle(Tensor, outs[i]) for i in range(n)]
 
     def __repr__(self) -> str:
         try:
@@ -429,7 +374,7 @@ class Sgd:
     """optim::Sgd (optim.rs:16-71)."""
 
     def __init__(self, params: Sequence[Tensor], lr: float):
-        arr = (ctypes.c_void_p * max(1, len(params)))(*[p._h.value for p in params])
+        arr = (ctypes.c_void_p * max(1, len(params)))(*[p._h for p in params])
         h = ctypes.c_void_p()
         _check(lib().fg_sgd_new(arr, len(params), ctypes.c_float(lr), ctypes.byref(h)))
         self._h = h
@@ -536,7 +481,7 @@ def plan_stats() -> dict:
 def debug_plan(roots: Sequence[Tensor], fuse: bool = False, render_hip: bool = False) -> dict:
     """Schedule `roots` without running them; optionally render HIP kernels."""
     import json
-    arr = (ctypes.c_void_p * max(1, len(roots)))(*[t._h.value for t in roots])
+    arr = (ctypes.c_void_p * max(1, len(roots)))(*[t._h for t in roots])
     need = ctypes.c_size_t()
     _check(lib().fg_debug_plan(arr, len(roots), int(fuse), int(render_hip), None, 0, ctypes.byref(need)))
     buf = ctypes.create_string_buffer(need.value + 1)

@@ -37,8 +37,23 @@ def _run(cmd: list[str]) -> None:
         raise RuntimeError("command failed: " + " ".join(cmd))
 
 
+def build_python_module() -> str:
+    """The CPython extension `_fgc` (csrc/pymodule.c): the hot Tensor methods
+    as one C call each, linked against the library next to it."""
+    import sysconfig
+
+    out = os.path.join(HERE, "_fgc" + sysconfig.get_config_var("EXT_SUFFIX"))
+    tmp = out + ".tmp"
+    _run(["gcc", "-O2", "-g0", "-fPIC", "-shared", "-Wall", "-I" + sysconfig.get_paths()["include"],
+          "-I" + os.path.join(ROOT, "include"), os.path.join(CSRC, "pymodule.c"), "-o", tmp,
+          "-L" + HERE, "-lferrograd_amd", "-Wl,-rpath,$ORIGIN"])
+    os.replace(tmp, out)
+    return out
+
+
 def build(jobs: int = 8) -> str:
-    """Compile every source (always) and link the shared library."""
+    """Compile every source (always), link the shared library and build the
+    Python extension over it."""
     os.makedirs(OBJ, exist_ok=True)
 
     def compile_one(src: str) -> str:
@@ -51,6 +66,7 @@ def build(jobs: int = 8) -> str:
     tmp = LIB + ".tmp"
     _run([HIPCC, *objs, "-o", tmp, *LDFLAGS])
     os.replace(tmp, LIB)
+    build_python_module()
     return LIB
 
 

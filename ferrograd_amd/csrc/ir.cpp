@@ -466,10 +466,17 @@ bool UOp::has_shape() const {
   return shape_opt(&s);
 }
 
-Shape UOp::shape() const {
-  Shape s;
-  FG_CHECK(shape_opt(&s), "tensor must have shape");
-  return s;
+Shape UOp::shape() const { return shape_ref(); }
+
+const Shape& UOp::shape_ref() const {
+  if (p_->shape_state == -1) {
+    Shape s;
+    bool ok = compute_shape(&s);
+    p_->shape_state = ok ? 1 : 0;
+    if (ok) p_->shape_cache = std::move(s);
+  }
+  FG_CHECK(p_->shape_state == 1, "tensor must have shape");
+  return p_->shape_cache;
 }
 
 bool UOp::has_buffer_identity() const {

@@ -183,6 +183,7 @@ class UOp {
   DeviceId device() const;
   bool has_shape() const;
   Shape shape() const;  // fails if none
+  const Shape& shape_ref() const;  // the cached shape, by reference; fails if none
   bool shape_opt(Shape* out) const;
   bool has_buffer_identity() const;
   bool is_const() const { return op() == Op::Const; }

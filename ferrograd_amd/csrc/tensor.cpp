@@ -165,6 +165,7 @@ Tensor Tensor::scalar_f32(float v, DeviceId dev) { return new_f32({v}, Shape{1},
 DeviceId Tensor::device() const { return uop().device(); }
 DType Tensor::dtype() const { return uop().dtype(); }
 Shape Tensor::shape() const { return uop().shape(); }
+const Shape& Tensor::shape_ref() const { return p_->uop.shape_ref(); }
 size_t Tensor::numel() const { return fg::numel(shape()); }
 size_t Tensor::ndim() const { return shape().size(); }
 
@@ -216,19 +217,28 @@ Tensor Tensor::unary(Op op) const {
 
 Tensor Tensor::binary(const Tensor& o, Op op, DType out) const {  // tensor.rs:449-459
   FG_CHECK(device() == o.device(), "binary ops require tensors on the same device");
-  FG_CHECK(shape() == o.shape(), std::string("shape mismatch for ") + op_name(op));
+  FG_CHECK(shape_ref() == o.shape_ref(), std::string("shape mismatch for ") + op_name(op));
   return from_uop(UOp::make_new(op, out, {uop(), o.uop()}, Arg::none()), requires_grad() || o.requires_grad());
 }
 
+// One side of a broadcast: the reshape to `target`'s rank and the expand to
+// `target`, as tensor.rs:1068-1092 builds them (each step skipped when it
+// would not change the shape), without a Tensor for each intermediate view.
+static UOp broadcast_side(const UOp& u, const Shape& target) {
+  const Shape& s = u.shape_ref();
+  Shape padded = pad_left(s, target.size());
+  UOp r = padded == s ? u : UOp::reshape(u, padded);
+  return padded == target ? r : UOp::expand(r, target);
+}
+
 Tensor Tensor::broadcasted(const Tensor& o, Op op, DType out) const {  // tensor.rs:461-467, 1068-1092
-  if (shape() == o.shape()) return binary(o, op, out);
+  if (shape_ref() == o.shape_ref()) return binary(o, op, out);
   FG_CHECK(device() == o.device(), "broadcast requires tensors on the same device");
   Shape target;
-  FG_CHECK(broadcast_with(shape(), o.shape(), &target),
+  FG_CHECK(broadcast_with(shape_ref(), o.shape_ref(), &target),
            "broadcast: incompatible dims for " + shape_str(shape()) + " vs " + shape_str(o.shape()));
-  Tensor l = reshape(pad_left(shape(), target.size())).expand(target);
-  Tensor r = o.reshape(pad_left(o.shape(), target.size())).expand(target);
-  return l.binary(r, op, out);
+  UOp l = broadcast_side(uop(), target), r = broadcast_side(o.uop(), target);
+  return from_uop(UOp::make_new(op, out, {l, r}, Arg::none()), requires_grad() || o.requires_grad());
 }
 
 Tensor Tensor::add(const Tensor& o) const { return broadcasted(o, Op::Add, dtype()); }
@@ -240,10 +250,33 @@ Tensor Tensor::exp2() const { return unary(Op::Exp2); }
 Tensor Tensor::log2() const { return unary(Op::Log2); }
 Tensor Tensor::sqrt() const { return unary(Op::Sqrt); }
 
+// relu's zeros (tensor.rs:517-531). The reference allocates a fresh zero
+// tensor at every call; that buffer is never handed out or written, so one
+// zero buffer per (device, dtype, shape) gives the same graphs and values
+// without a buffer per call, and a loop that rebuilds the same relu gets the
+// same graph nodes every time. At most 64 shapes are kept; past that the
+// cache starts over (buffers in use stay alive through their graphs).
+static UOp relu_zeros(const Shape& shape, DeviceId dev, DType dt) {
+  struct Entry {
+    DeviceId dev;
+    DType dt;
+    Shape shape;
+    UOp zeros;
+  };
+  static auto* cache = new std::vector<Entry>();
+  for (auto& e : *cache)
+    if (e.dev == dev && e.dt == dt && e.shape == shape) return e.zeros;
+  if (cache->size() >= 64) cache->clear();
+  Device& backend = get_device(dev);
+  Buffer b = backend.allocate(dt, fg::numel(shape));
+  cache->push_back({dev, dt, shape, UOp::reshape(UOp::buffer(b, dt, dev), shape)});
+  return cache->back().zeros;
+}
+
 Tensor Tensor::relu() const {  // tensor.rs:517-531
-  Tensor zero = zeros(shape(), device(), dtype());
-  Tensor cond = zero.binary(*this, Op::CmpLt, DType::Bool());
-  return from_uop(UOp::make_new(Op::Where, dtype(), {cond.uop(), uop(), zero.uop()}, Arg::none()), requires_grad());
+  const UOp zero = relu_zeros(shape_ref(), device(), dtype());
+  const UOp cond = UOp::make_new(Op::CmpLt, DType::Bool(), {zero, uop()}, Arg::none());
+  return from_uop(UOp::make_new(Op::Where, dtype(), {cond, uop(), zero}, Arg::none()), requires_grad());
 }
 
 // A constant the library itself builds into graphs (LOG2_E in exp, LN_2 in

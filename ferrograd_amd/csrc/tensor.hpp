@@ -34,6 +34,7 @@ class Tensor {
   DeviceId device() const;
   DType dtype() const;
   Shape shape() const;
+  const Shape& shape_ref() const;  // no copy; valid while the tensor's graph node lives
   size_t numel() const;
   size_t ndim() const;
   bool is_realized() const;

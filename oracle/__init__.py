@@ -62,7 +62,7 @@ def plan_c(roots) -> list:
     l.fg_oracle_plan_c.restype = ctypes.c_int
     l.fg_oracle_plan_c.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.c_int, ctypes.c_char_p, ctypes.c_size_t,
                                    ctypes.POINTER(ctypes.c_size_t)]
-    arr = (ctypes.c_void_p * max(1, len(roots)))(*[t._h.value for t in roots])
+    arr = (ctypes.c_void_p * max(1, len(roots)))(*[t._h for t in roots])
     need = ctypes.c_size_t()
     rc = l.fg_oracle_plan_c(arr, len(roots), None, 0, ctypes.byref(need))
     buf = ctypes.create_string_buffer(need.value + 1)
