@@ -143,6 +143,10 @@ class Device {
   // Whether schedule-time value-preserving fusion (shared elementwise
   // subexpressions inlined into one kernel, zero buffers folded) is enabled.
   virtual bool fuse_elementwise() const { return false; }
+  // Whether relu may take its zeros from one never-written buffer per
+  // (dtype, shape) instead of allocating fresh zeros per call as the
+  // reference does (tensor.rs:517-531); same values, no allocation.
+  virtual bool shares_relu_zeros() const { return false; }
 
   // device.rs:323-327
   std::shared_ptr<Program> cached_program(const UOp& sink);

@@ -491,6 +491,8 @@ class HipDevice : public Device {
     if (ctx_) check(fg_hip_sync(ctx_), "fg_hip_sync");
   }
 
+  bool shares_relu_zeros() const override { return true; }
+
   // FG_FUSE=0, or an OPT list without "fuse", keeps the reference's kernel
   // partition (read once per process).
   bool fuse_elementwise() const override {

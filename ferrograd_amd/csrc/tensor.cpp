@@ -251,12 +251,16 @@ Tensor Tensor::log2() const { return unary(Op::Log2); }
 Tensor Tensor::sqrt() const { return unary(Op::Sqrt); }
 
 // relu's zeros (tensor.rs:517-531). The reference allocates a fresh zero
-// tensor at every call; that buffer is never handed out or written, so one
-// zero buffer per (device, dtype, shape) gives the same graphs and values
-// without a buffer per call, and a loop that rebuilds the same relu gets the
-// same graph nodes every time. At most 64 shapes are kept; past that the
-// cache starts over (buffers in use stay alive through their graphs).
+// tensor at every call; that buffer is never handed out or written, so on a
+// device that allows it (the HIP device) one zero buffer per (dtype, shape)
+// gives the same graphs and values without a buffer per call, and a loop
+// that rebuilds the same relu gets the same graph nodes every time. At most
+// 64 shapes are kept; past that the cache starts over (buffers in use stay
+// alive through their graphs). Other devices allocate per call.
 static UOp relu_zeros(const Shape& shape, DeviceId dev, DType dt) {
+  Device& backend = get_device(dev);
+  if (!backend.shares_relu_zeros())
+    return UOp::reshape(UOp::buffer(backend.allocate(dt, fg::numel(shape)), dt, dev), shape);
   struct Entry {
     DeviceId dev;
     DType dt;
@@ -267,7 +271,6 @@ static UOp relu_zeros(const Shape& shape, DeviceId dev, DType dt) {
   for (auto& e : *cache)
     if (e.dev == dev && e.dt == dt && e.shape == shape) return e.zeros;
   if (cache->size() >= 64) cache->clear();
-  Device& backend = get_device(dev);
   Buffer b = backend.allocate(dt, fg::numel(shape));
   cache->push_back({dev, dt, shape, UOp::reshape(UOp::buffer(b, dt, dev), shape)});
   return cache->back().zeros;

@@ -206,3 +206,74 @@ def test_in_place_update_replayed_on_hip(fg, cpu, hip):
     for k in range(3):
         e = transpose_add_loops(e)
         assert np.array_equal(outs["cpu"][k], e) and np.array_equal(outs["hip"][k], e), k
+
+
+def random_in_place(fg, dev, seed):
+    """w.assign(e(w)) for a random elementwise expression e over views of w
+    itself (its transpose, a broadcast row or column of it, a narrowed
+    window) and other leaves, realised twice in a row. Elementwise ops round
+    the same way on both devices, so whatever partition and order the
+    schedule gives, the sequential kernels must reproduce the oracle's bits.
+    Returns the two results."""
+    r = np.random.default_rng(seed)
+    n = int(r.choice([3, 4, 5, 8, 12]))
+    m = n if r.random() < 0.6 else int(r.choice([4, 6, 8]))
+    a = r.uniform(-1, 1, (n, m)).astype(F)
+    w = fg.Tensor.new(a, [n, m], dev)
+    others = [fg.Tensor.new(r.uniform(-1, 1, (n, m)).astype(F), [n, m], dev) for _ in range(2)]
+    outs = []
+    for _ in range(2):
+        def view():
+            k = int(r.integers(5 if n == m else 4))
+            if k == 0:
+                return w
+            if k == 1:
+                i = int(r.integers(n))
+                return w.narrow(0, i, 1).expand([n, m])
+            if k == 2:
+                j = int(r.integers(m))
+                return w.narrow(1, j, 1).expand([n, m])
+            if k == 3:
+                return others[int(r.integers(2))]
+            return w.permute([1, 0])
+        e = view()
+        for _ in range(int(r.integers(1, 4))):
+            op = int(r.integers(5))
+            if op == 0:
+                e = e.add(view())
+            elif op == 1:
+                e = e.mul(view())
+            elif op == 2:
+                e = e.relu()
+            elif op == 3:
+                e = e.mul(fg.Tensor.scalar(float(r.choice([0.5, -1.5, 0.25])), dev))
+            else:
+                e = e.sub(view())
+        w.assign(e)
+        w.realize()
+        outs.append(w.numpy().reshape(n, m).copy())
+    return outs
+
+
+@pytest.mark.parametrize("seed", range(40))
+def test_random_in_place_programs_keep_their_bits_under_the_fusions(fg, cpu, seed):
+    import oracle
+
+    plain = random_in_place(fg, cpu, seed)
+    oracle.set_fuse(True)
+    try:
+        fused = random_in_place(fg, cpu, seed)
+    finally:
+        oracle.set_fuse(False)
+    for p, q in zip(plain, fused):
+        assert np.array_equal(p, q)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("seed", range(40))
+def test_random_in_place_programs_on_hip(fg, cpu, hip, seed):
+    print(f"random in-place program {seed}", flush=True)
+    want = random_in_place(fg, cpu, seed)
+    got = random_in_place(fg, hip, seed)
+    for g, w in zip(got, want):
+        assert np.array_equal(g, w), float(np.max(np.abs(g.astype(np.float64) - w)))
