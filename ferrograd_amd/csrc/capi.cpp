@@ -481,6 +481,8 @@ int fg_debug_plan(fg_tensor** roots, int n, int fuse, int render, char* buf, siz
     // counts, for the batch runs a replayed sequence would launch.
     std::vector<bool> is_block;
     std::vector<size_t> nargs;
+    std::vector<fg::RenderedKernel> rks;
+    std::vector<std::vector<fg::BatchArg>> binfo;
     if (!rs.empty()) {
       fg::ScheduleOptions opt;
       opt.fuse = fuse != 0;
@@ -521,6 +523,13 @@ int fg_debug_plan(fg_tensor** roots, int n, int fuse, int render, char* buf, siz
              << "], \"source\": \"" << json_escape(rk.source) << "\"";
           is_block.push_back(!rk.stage_fn.empty() && rk.launches.empty());
           nargs.push_back(it.output_buffer ? it.inputs.size() + 1 : it.inputs.size());
+          std::vector<fg::BatchArg> bi;
+          if (it.output_buffer) bi.push_back({it.output_buffer.get(), it.output_buffer->numel});
+          for (auto& a : it.inputs)
+            bi.push_back(a.kind == fg::KernelArg::Kind::Buffer ? fg::BatchArg{a.buffer.get(), a.buffer->numel}
+                                                              : fg::BatchArg{});
+          binfo.push_back(std::move(bi));
+          rks.push_back(std::move(rk));
         }
         os << "}";
       }
@@ -531,6 +540,21 @@ int fg_debug_plan(fg_tensor** roots, int n, int fuse, int render, char* buf, siz
       auto runs = fg::block_batch_runs(is_block, nargs);
       for (size_t i = 0; i < runs.size(); i++)
         os << (i ? ", " : "") << "[" << runs[i].first << ", " << runs[i].second << "]";
+      // Each run's batch kernel as a replayed sequence would compile it (in
+      // plan order), with the stage outputs it keeps in LDS.
+      os << "], \"batch_kernels\": [";
+      for (size_t i = 0; i < runs.size(); i++) {
+        std::vector<const fg::RenderedKernel*> stages;
+        std::vector<std::vector<fg::BatchArg>> args;
+        for (size_t j = runs[i].first; j < runs[i].first + runs[i].second; j++) {
+          stages.push_back(&rks[j]);
+          args.push_back(binfo[j]);
+        }
+        const fg::BatchForwarding fwd = fg::batch_forwarding(stages, args);
+        const fg::RenderedKernel bk = fg::render_block_batch(stages, false, &fwd);
+        os << (i ? ", " : "") << "{\"name\": \"" << bk.name << "\", \"forwarded\": " << fwd.dtypes.size()
+           << ", \"source\": \"" << json_escape(bk.source) << "\"}";
+      }
       os << "]";
     }
     os << "}";

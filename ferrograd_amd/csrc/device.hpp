@@ -72,6 +72,8 @@ struct RenderedKernel {
   std::string kind;  // lowering class, for debug output and tests
   std::vector<std::pair<int, DType>> params;  // (slot, dtype) in launch order
   int out_slot = -1;                           // the parameter slot the kernel stores to
+  bool reads_output = false;                   // whether it also loads from that parameter (in place)
+  size_t out_count = 0;                        // elements of that parameter it stores
   // Multi-kernel programs: when non-empty these launches run in order instead
   // of the single (name, grid, block) launch. With scratch_bytes > 0 the
   // program owns a device scratch buffer passed as the last argument of every

@@ -3145,6 +3145,8 @@ RenderedKernel render_hip(const UOp& kernel, const std::string& name, int force_
   }
   rk.params = params;
   rk.out_slot = static_cast<int>(ki.out_param.arg().a);
+  for (auto& ld : loads_in(ki.value)) rk.reads_output = rk.reads_output || ld.src(0).src(0) == ki.out_param;
+  rk.out_count = static_cast<size_t>(total_outputs(ki));
   return rk;
 }
 
@@ -3172,12 +3174,21 @@ RenderedKernel render_hip_stable(const UOp& kernel) {
   return rk;
 }
 
-RenderedKernel render_block_batch(const std::vector<const RenderedKernel*>& stages, bool read_back) {
+RenderedKernel render_block_batch(const std::vector<const RenderedKernel*>& stages, bool read_back,
+                                  const BatchForwarding* fwd) {
   FG_CHECK(stages.size() >= (read_back ? 1u : 2u), "a batch runs at least two block kernels");
   static const std::string kPlaceholder = "FGBATCHNAME";
   std::ostringstream src, params, body;
   src << kPrelude;
   std::set<std::string> defined;
+  size_t nargs = 0;
+  for (auto* st : stages) nargs += st->stage_types.size();
+  FG_CHECK(!fwd || fwd->arg_buffer.size() == nargs, "batch forwarding: one entry per argument");
+  if (fwd) {
+    for (size_t k = 0; k < fwd->dtypes.size(); k++)
+      body << "  __shared__ __attribute__((aligned(16))) " << ctype(fwd->dtypes[k]) << " fg_fwd" << k << "["
+           << fwd->numels[k] << "];\n";
+  }
   size_t n = 0;
   for (size_t i = 0; i < stages.size(); i++) {
     const RenderedKernel& st = *stages[i];
@@ -3187,9 +3198,17 @@ RenderedKernel render_block_batch(const std::vector<const RenderedKernel*>& stag
     body << "  " << st.stage_fn << "(";
     for (size_t j = 0; j < st.stage_types.size(); j++, n++) {
       params << (n ? ", " : "") << st.stage_types[j] << " a" << n;
-      body << (j ? ", " : "") << "a" << n;
+      const int k = fwd ? fwd->arg_buffer[n] : -1;
+      body << (j ? ", " : "") << (k >= 0 ? "fg_fwd" + std::to_string(k) : "a" + std::to_string(n));
     }
     body << ");\n";
+  }
+  if (fwd && !fwd->dtypes.empty()) {
+    // The forwarded outputs reach their buffers once every stage has run.
+    body << "  __syncthreads();\n";
+    for (size_t k = 0; k < fwd->dtypes.size(); k++)
+      body << "  for (int i = threadIdx.x; i < " << fwd->numels[k] << "; i += " << kBlockThreads << ") a"
+           << fwd->out_arg[k] << "[i] = fg_fwd" << k << "[i];\n";
   }
   if (read_back) {
     params << ", unsigned int* rb_dst, const unsigned int* rb_src, int rb_words";
@@ -3213,6 +3232,48 @@ RenderedKernel render_block_batch(const std::vector<const RenderedKernel*>& stag
   rk.kind = "block_batch";
   rk.block[0] = kBlockThreads;
   return rk;
+}
+
+BatchForwarding batch_forwarding(const std::vector<const RenderedKernel*>& stages,
+                                 const std::vector<std::vector<BatchArg>>& args) {
+  FG_CHECK(stages.size() == args.size(), "batch_forwarding: one argument list per stage");
+  BatchForwarding f;
+  auto out_param = [&](size_t j, size_t q) {
+    const RenderedKernel& m = *stages[j];
+    return q < m.params.size() && m.params[q].first == m.out_slot && args[j][q].id;
+  };
+  std::map<const void*, int> writers;
+  for (size_t j = 0; j < stages.size(); j++)
+    for (size_t q = 0; q < args[j].size(); q++)
+      if (out_param(j, q)) writers[args[j][q].id]++;
+  std::map<const void*, int> lds;  // buffer -> its LDS array, once its writer has run
+  size_t bytes = 0;
+  for (size_t j = 0; j < stages.size(); j++) {
+    const RenderedKernel& m = *stages[j];
+    const size_t base = f.arg_buffer.size();
+    f.arg_buffer.resize(base + args[j].size(), -1);
+    for (size_t q = 0; q < args[j].size(); q++) {
+      auto it = args[j][q].id ? lds.find(args[j][q].id) : lds.end();
+      if (it != lds.end()) f.arg_buffer[base + q] = it->second;
+    }
+    for (size_t q = 0; q < args[j].size(); q++) {
+      if (!out_param(j, q)) continue;
+      const DType dt = m.params[q].second;
+      const size_t numel = args[j][q].numel, sz = numel * dt.size_bytes();
+      const bool kind_ok = dt == DType::F32() || dt == DType::I32() || dt == DType::Bool();
+      if (writers[args[j][q].id] != 1 || m.reads_output || m.out_count != numel || !kind_ok ||
+          bytes + sz > kBatchForwardBytes)
+        continue;
+      bytes += (sz + 15) / 16 * 16;
+      const int k = static_cast<int>(f.dtypes.size());
+      f.dtypes.push_back(dt);
+      f.numels.push_back(numel);
+      f.out_arg.push_back(static_cast<int>(base + q));
+      f.arg_buffer[base + q] = k;
+      lds[args[j][q].id] = k;
+    }
+  }
+  return f;
 }
 
 std::vector<std::pair<size_t, size_t>> block_batch_runs(const std::vector<bool>& is_block,

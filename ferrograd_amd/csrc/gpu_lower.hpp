@@ -81,7 +81,36 @@ KernelClass base_class(const UOp& kernel);
 // rb_src, rb_words) and a last stage, after a barrier, copies rb_words 32-bit
 // words from rb_src to rb_dst: the sequence's result read back by the launch
 // that computed it.
-RenderedKernel render_block_batch(const std::vector<const RenderedKernel*>& stages, bool read_back = false);
+//
+// With `fwd`, stage outputs that later stages of the batch read stay in LDS:
+// the producing stage writes an LDS array instead of its buffer, the later
+// stages read that array, and once every stage has run the arrays are copied
+// to their buffers. A stage-to-stage hand-off then waits for LDS, not for
+// global stores to reach L2 and loads to come back.
+struct BatchForwarding {
+  std::vector<int> arg_buffer;  // per argument of the batch: the LDS array it reads or writes, or -1
+  std::vector<DType> dtypes;    // per LDS array
+  std::vector<size_t> numels;
+  std::vector<int> out_arg;     // the producing stage's output argument (the copy's destination)
+};
+// The LDS a batch may spend on forwarded outputs (the stage bodies keep their
+// own few kilobytes).
+constexpr size_t kBatchForwardBytes = 64 * 1024;
+// One argument of a stage, for choosing what to forward: the buffer's
+// identity (null for a scalar) and its element count.
+struct BatchArg {
+  const void* id = nullptr;
+  size_t numel = 0;
+};
+// Which stage outputs stay in LDS. An output is kept when one stage alone
+// writes its buffer, writes every element of it and does not read it, its
+// dtype is f32, i32 or bool, and it fits in what is left of
+// kBatchForwardBytes; stages after the writer read the LDS array, stages
+// before it the buffer (its contents before the batch, as in the sequence).
+BatchForwarding batch_forwarding(const std::vector<const RenderedKernel*>& stages,
+                                 const std::vector<std::vector<BatchArg>>& args);
+RenderedKernel render_block_batch(const std::vector<const RenderedKernel*>& stages, bool read_back = false,
+                                  const BatchForwarding* fwd = nullptr);
 
 // The runs of consecutive block kernels a sequence launches as batches, as
 // (first, count) pairs: every run of two or more, split after kMaxBatchStages

@@ -3,6 +3,7 @@
 // gpu_lower.cpp as its optimize/render stages.
 #include <cstdlib>
 #include <cstring>
+#include <map>
 #include <set>
 
 #include "../../include/ferrograd_hip.h"
@@ -303,7 +304,14 @@ class HipDevice : public Device {
       // With no room left for the read-back's arguments, the read-back stays
       // a kernel of its own after the batch.
       if (count && total <= FG_MAX_LAUNCH_ARGS) {
-        r->rb_batch = compile(render_block_batch(stages, true), total);
+        std::vector<Program*> ordered;
+        std::vector<std::vector<KernelArg>> ordered_args;
+        for (size_t j = 0; j < progs.size(); j++) {
+          ordered.push_back(prog_at(j));
+          ordered_args.push_back(args_at(j));
+        }
+        const BatchForwarding fwd = forwarding_of(ordered, ordered_args, first, count);
+        r->rb_batch = compile(render_block_batch(stages, true, forwarding_on() ? &fwd : nullptr), total);
         r->rb_first = first;
       }
     }
@@ -392,6 +400,15 @@ class HipDevice : public Device {
     }
   }
 
+  // FG_BATCH_LDS=0 keeps every batch stage's output in its buffer (read once).
+  static bool forwarding_on() {
+    static const bool on = [] {
+      const char* e = std::getenv("FG_BATCH_LDS");
+      return !(e && std::strcmp(e, "0") == 0);
+    }();
+    return on;
+  }
+
   // A block kernel: one workgroup, a single launch, no scratch; its body can
   // run as a stage of a batch.
   static bool is_block_program(Program& prog) {
@@ -446,10 +463,28 @@ class HipDevice : public Device {
     return order;
   }
 
+  // The LDS forwarding of the batch of progs[first, first + n): buffers are
+  // told apart by identity (within one sequence every output is a buffer of
+  // its own and every input a live one).
+  static BatchForwarding forwarding_of(const std::vector<Program*>& progs, std::vector<std::vector<KernelArg>>& args,
+                                       size_t first, size_t n) {
+    std::vector<const RenderedKernel*> stages;
+    std::vector<std::vector<BatchArg>> info;
+    for (size_t j = first; j < first + n; j++) {
+      stages.push_back(&progs[j]->meta);
+      info.emplace_back();
+      for (auto& a : args[j])
+        info.back().push_back(a.kind == KernelArg::Kind::Buffer ? BatchArg{a.buffer.get(), a.buffer->numel}
+                                                                 : BatchArg{});
+    }
+    return batch_forwarding(stages, info);
+  }
+
   // Runs of two or more consecutive block kernels (one workgroup each, no
   // scratch) in a sequence (block_batch_runs): each becomes one launch of a
   // batch program that runs the kernels' bodies in order behind workgroup
-  // barriers. The batch's code object is cached by its source like any other.
+  // barriers, its stages' outputs handed on through LDS (batch_forwarding).
+  // The batch's code object is cached by its source like any other.
   void group_blocks(const std::vector<Program*>& progs, std::vector<std::vector<KernelArg>>& args,
                     std::vector<std::pair<size_t, size_t>>& groups, std::vector<std::shared_ptr<Program>>& batches) {
     std::vector<bool> is_block;
@@ -465,7 +500,8 @@ class HipDevice : public Device {
         stages.push_back(&progs[j]->meta);
         total += args[j].size();
       }
-      batches.push_back(compile(render_block_batch(stages), total));
+      const BatchForwarding fwd = forwarding_of(progs, args, first, n);
+      batches.push_back(compile(render_block_batch(stages, false, forwarding_on() ? &fwd : nullptr), total));
       groups.emplace_back(first, n);
     }
   }

@@ -252,3 +252,58 @@ def test_sixteen_block_roots_replayed_twice(fg, hip):
         fg.Tensor.realize_many(roots)
         for t, w in zip(roots, want):
             assert np.array_equal(t.numpy().reshape(8), w), rep
+
+
+def test_c4_batches_keep_stage_outputs_in_lds_and_compile(fg, cpu):
+    # The C4 step's runs of block kernels as batches: every stage output of
+    # the softmax run is one stage's full, not in-place, output, so all six
+    # stay in LDS and reach their buffers after the last stage; the batch
+    # kernels compile for gfx950.
+    from hipcompile import compile_sources
+    from ferrograd_amd.mlp import Mlp, synthetic_batch
+
+    fg.reset_init_seed(42)
+    m = Mlp((784, 128, 10), cpu)
+    opt = fg.Sgd(m.parameters(), 0.01)
+    xs, ts = synthetic_batch(256, 784, 10, 7, 8)
+    x = fg.Tensor.new(xs, list(xs.shape), cpu)
+    t = fg.Tensor.new(ts, list(ts.shape), cpu)
+    loss = m.forward(x).cross_entropy(t)
+    opt.zero_grad()
+    loss.backward()
+    opt.step()
+    loss.to_vec()
+    loss = m.forward(x).cross_entropy(t)
+    opt.zero_grad()
+    loss.backward()
+    ps = m.parameters()
+    for p in ps:
+        p.assign(p.detach().sub(p.grad().mul(fg.Tensor.scalar(0.01, cpu))))
+    plan = fg.debug_plan(ps + [loss], fuse=True, render_hip=True)
+    bks = plan["batch_kernels"]
+    assert len(bks) == len(plan["batches"]) >= 2
+    first = bks[0]
+    assert first["forwarded"] == plan["batches"][0][1] == 6
+    src = first["source"]
+    assert src.count("__shared__ __attribute__((aligned(16))) float fg_fwd") == 6
+    assert src.count("] = fg_fwd") == 6  # each array copied to its buffer once, after the last stage
+    compile_sources({b["source"]: b["name"] for b in bks}, limit_s=120)
+
+
+def test_batch_forwarding_skips_in_place_and_partial_outputs(fg, cpu):
+    # An in-place SGD-style update reads its destination: its output stays in
+    # its buffer, and later stages read the buffer.
+    r = np.random.default_rng(4)
+    w = fg.Tensor.new(r.uniform(-1, 1, (8, 8)).astype(np.float32), [8, 8], cpu)
+    g = fg.Tensor.new(r.uniform(-1, 1, (8, 8)).astype(np.float32), [8, 8], cpu)
+    h = g.mul(g)
+    w.assign(w.sub(h.mul(fg.Tensor.scalar(0.5, cpu))))
+    plan = fg.debug_plan([h, w], fuse=True, render_hip=True)
+    assert [it["class"] for it in plan["items"]] == ["block", "block"] and plan["batches"] == [[0, 2]]
+    bk = plan["batch_kernels"][0]
+    src = bk["source"][bk["source"].index('extern "C"'):]
+    # h, a fresh full output, is forwarded and read by the update from LDS;
+    # w's in-place update (its output is argument 2) writes its buffer.
+    assert bk["forwarded"] == 1
+    assert "_blk_body(fg_fwd0, a1);" in src and "_blk_body(a2, fg_fwd0, a4);" in src
+    assert "a0[i] = fg_fwd0[i]" in src and "a2[i] =" not in src
