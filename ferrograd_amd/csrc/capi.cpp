@@ -555,6 +555,20 @@ int fg_debug_plan(fg_tensor** roots, int n, int fuse, int render, char* buf, siz
         os << (i ? ", " : "") << "{\"name\": \"" << bk.name << "\", \"forwarded\": " << fwd.dtypes.size()
            << ", \"source\": \"" << json_escape(bk.source) << "\"}";
       }
+      // Adjacent independent kernels that a replayed sequence would launch
+      // together (in plan order, outside the batches).
+      os << "], \"pairs\": [";
+      std::vector<bool> in_batch(rks.size(), false);
+      for (auto [f, c] : runs)
+        for (size_t j = f; j < f + c; j++) in_batch[j] = true;
+      std::vector<const fg::RenderedKernel*> all;
+      for (auto& r : rks) all.push_back(&r);
+      auto firsts = fg::pair_runs(all, binfo, in_batch);
+      for (size_t i = 0; i < firsts.size(); i++) {
+        const fg::RenderedKernel pk = fg::render_hfused(rks[firsts[i]], rks[firsts[i] + 1]);
+        os << (i ? ", " : "") << "{\"first\": " << firsts[i] << ", \"name\": \"" << pk.name
+           << "\", \"grid\": " << pk.grid[0] << ", \"source\": \"" << json_escape(pk.source) << "\"}";
+      }
       os << "]";
     }
     os << "}";

@@ -85,6 +85,11 @@ struct RenderedKernel {
   // of them as one launch (render_block_batch).
   std::string stage_fn, stage_src;
   std::vector<std::string> stage_types;
+  // Kernels whose body is a device function of its block index (the small
+  // GEMM): the function, its source and its parameter types in slot order,
+  // so a device can run two independent ones in one launch (render_hfused).
+  std::string hbody_fn, hbody_src;
+  std::vector<std::string> hbody_types;
 };
 
 struct Program {

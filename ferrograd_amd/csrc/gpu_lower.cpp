@@ -1646,6 +1646,8 @@ bool match_gemm(const KernelInfo& ki, GemmMatch* g) {
 // tiles meet in LDS and are summed in wave order by one thread per output,
 // which then runs the epilogue (bias, relu mask, SGD update). One launch, no
 // scratch, a fixed fold order.
+std::string block_params(const KernelInfo& ki, std::vector<std::string>* types, std::vector<std::string>* names);
+
 RenderedKernel render_small_gemm(const KernelInfo& ki, const GemmMatch& g, const std::string& name) {
   const int64_t M = g.M, N = g.N, K = g.K;
   const int64_t KG = (K + 15) / 16, ntm = (M + 15) / 16, ntn = (N + 15) / 16;
@@ -1653,11 +1655,14 @@ RenderedKernel render_small_gemm(const KernelInfo& ki, const GemmMatch& g, const
   const int64_t GMAX = (KG + W - 1) / W;  // groups the busiest wave folds
   const int NT = 64 * W;
   std::ostringstream s;
-  s << kPrelude;
-  s << signature(ki, name, NT) << " {\n";
+  // The kernel's body as a device function of its block index (fg_bid), so a
+  // launch may also run it beside another kernel (render_hfused).
+  std::vector<std::string> types, names;
+  const std::string params = block_params(ki, &types, &names);
+  s << "__device__ __forceinline__ void " << name << "_hb(" << params << ", unsigned fg_bid) {\n";
   s << "  __shared__ float fg_part[" << W << "][256];\n";
   s << "  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, q = lane >> 4, r16 = lane & 15;\n";
-  s << "  const int tm = (int)(blockIdx.x / " << ntn << "), tn = (int)(blockIdx.x % " << ntn << ");\n";
+  s << "  const int tm = (int)(fg_bid / " << ntn << "), tn = (int)(fg_bid % " << ntn << ");\n";
   s << "  const int m0 = tm * 16, n0 = tn * 16;\n";
   // This wave's groups of 16 k: [gbeg, gend).
   s << "  const int gbeg = (int)(((long)wave * " << KG << ") / " << W << "), gend = (int)(((long)(wave + 1) * " << KG
@@ -1700,22 +1705,21 @@ RenderedKernel render_small_gemm(const KernelInfo& ki, const GemmMatch& g, const
   }
   em.close_scope();
   s << em.code();
-  s << R"(  fg_f4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-  #pragma unroll
-  for (int gi = 0; gi < GMAX_; gi++)
-    #pragma unroll
-    for (int u = 0; u < 4; u++) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av[gi][u], bv[gi][u], acc, 0, 0, 0);
-  // D[4*(lane/16) + e][lane%16] = acc[e]
-  #pragma unroll
-  for (int e = 0; e < 4; e++) fg_part[wave][(4 * q + e) * 16 + r16] = acc[e];
-  __syncthreads();
-  for (int o = tid; o < 256; o += 64 * W_) {
-  float sum = fg_part[0][o];
-  #pragma unroll
-  for (int w = 1; w < W_; w++) sum = sum + fg_part[w][o];
-  const int grow = m0 + (o >> 4), gcol = n0 + (o & 15);
-  if (grow < M_ && gcol < N_) {
-)";
+  s << "  fg_f4 acc = {0.0f, 0.0f, 0.0f, 0.0f};\n"
+       "  #pragma unroll\n"
+       "  for (int gi = 0; gi < " << GMAX << "; gi++)\n"
+       "    #pragma unroll\n"
+       "    for (int u = 0; u < 4; u++) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av[gi][u], bv[gi][u], acc, 0, 0, 0);\n"
+       "  // D[4*(lane/16) + e][lane%16] = acc[e]\n"
+       "  #pragma unroll\n"
+       "  for (int e = 0; e < 4; e++) fg_part[wave][(4 * q + e) * 16 + r16] = acc[e];\n"
+       "  __syncthreads();\n"
+       "  for (int o = tid; o < 256; o += " << NT << ") {\n"
+       "  float sum = fg_part[0][o];\n"
+       "  #pragma unroll\n"
+       "  for (int w = 1; w < " << W << "; w++) sum = sum + fg_part[w][o];\n"
+       "  const int grow = m0 + (o >> 4), gcol = n0 + (o & 15);\n"
+       "  if (grow < " << M << " && gcol < " << N << ") {\n";
   {
     Emitter ep;
     ep.define_range(g.rm, "grow");
@@ -1729,19 +1733,15 @@ RenderedKernel render_small_gemm(const KernelInfo& ki, const GemmMatch& g, const
     s << ep.code();
   }
   s << "  }\n  }\n}\n";
-  std::string src = s.str();
-  auto def = [&](const std::string& k, int64_t v) {
-    const std::string d = "#define " + k + " " + std::to_string(v) + "\n";
-    src.insert(src.find("extern \"C\""), d);
-  };
-  def("GMAX_", GMAX);
-  def("W_", W);
-  def("M_", M);
-  def("N_", N);
   RenderedKernel rk;
   rk.name = name;
   rk.kind = kernel_class_name(KernelClass::Gemm);
-  rk.source = src;
+  rk.hbody_fn = name + "_hb";
+  rk.hbody_src = s.str();
+  rk.hbody_types = types;
+  std::string call = rk.hbody_fn + "(";
+  for (auto& n : names) call += n + ", ";
+  rk.source = std::string(kPrelude) + rk.hbody_src + signature(ki, name, NT) + " {\n  " + call + "blockIdx.x);\n}\n";
   rk.block[0] = static_cast<unsigned>(NT);
   rk.grid[0] = static_cast<unsigned>(ntm * ntn);
   return rk;
@@ -3170,6 +3170,8 @@ RenderedKernel render_hip_stable(const UOp& kernel) {
   replace_all(rk.name);
   replace_all(rk.stage_fn);
   replace_all(rk.stage_src);
+  replace_all(rk.hbody_fn);
+  replace_all(rk.hbody_src);
   for (auto& l : rk.launches) replace_all(l.func);
   return rk;
 }
@@ -3232,6 +3234,88 @@ RenderedKernel render_block_batch(const std::vector<const RenderedKernel*>& stag
   rk.kind = "block_batch";
   rk.block[0] = kBlockThreads;
   return rk;
+}
+
+RenderedKernel render_hfused(const RenderedKernel& a, const RenderedKernel& b) {
+  FG_CHECK(!a.hbody_fn.empty() && !b.hbody_fn.empty(), "render_hfused: kernels without a block-index body");
+  // Bodies are emitted once per name: one name must mean one body.
+  FG_CHECK(a.hbody_fn != b.hbody_fn || a.hbody_src == b.hbody_src,
+           "render_hfused: two different bodies named " + a.hbody_fn);
+  FG_CHECK(a.source.find(a.hbody_fn + "(") != std::string::npos &&
+               b.source.find(b.hbody_fn + "(") != std::string::npos,
+           "render_hfused: a body is not the one its kernel calls");
+  FG_CHECK(a.block[0] == b.block[0] && a.block[1] == 1 && a.block[2] == 1 && b.block[1] == 1 && b.block[2] == 1 &&
+               a.grid[1] == 1 && a.grid[2] == 1 && b.grid[1] == 1 && b.grid[2] == 1,
+           "render_hfused: the kernels' launch shapes differ");
+  static const std::string kPlaceholder = "FGHFUSEDNAME";
+  std::ostringstream src, params, call_a, call_b;
+  src << kPrelude << a.hbody_src;
+  if (b.hbody_fn != a.hbody_fn) src << b.hbody_src;
+  size_t n = 0;
+  call_a << a.hbody_fn << "(";
+  for (auto& t : a.hbody_types) {
+    params << (n ? ", " : "") << t << " a" << n;
+    call_a << "a" << n++ << ", ";
+  }
+  call_b << b.hbody_fn << "(";
+  for (auto& t : b.hbody_types) {
+    params << (n ? ", " : "") << t << " a" << n;
+    call_b << "a" << n++ << ", ";
+  }
+  src << "extern \"C\" __global__ void __launch_bounds__(" << a.block[0] << ") " << kPlaceholder << "(" << params.str()
+      << ") {\n  if (blockIdx.x < " << a.grid[0] << "u) " << call_a.str() << "blockIdx.x);\n  else " << call_b.str()
+      << "blockIdx.x - " << a.grid[0] << "u);\n}\n";
+  RenderedKernel rk;
+  rk.source = src.str();
+  uint64_t h = 1469598103934665603ULL;
+  for (unsigned char c : rk.source) {
+    h ^= c;
+    h *= 1099511628211ULL;
+  }
+  char hex[40];
+  std::snprintf(hex, sizeof(hex), "k%012llx_pair", static_cast<unsigned long long>(h & 0xffffffffffffULL));
+  for (size_t p = rk.source.find(kPlaceholder); p != std::string::npos; p = rk.source.find(kPlaceholder, p))
+    rk.source.replace(p, kPlaceholder.size(), hex);
+  rk.name = hex;
+  rk.kind = "pair";
+  rk.block[0] = a.block[0];
+  rk.grid[0] = a.grid[0] + b.grid[0];
+  return rk;
+}
+
+std::vector<size_t> pair_runs(const std::vector<const RenderedKernel*>& kernels,
+                              const std::vector<std::vector<BatchArg>>& args, const std::vector<bool>& excluded) {
+  FG_CHECK(kernels.size() == args.size() && kernels.size() == excluded.size(), "pair_runs: one entry per kernel");
+  const size_t n = kernels.size();
+  auto pairable = [&](size_t i) {
+    const RenderedKernel& m = *kernels[i];
+    return !excluded[i] && !m.hbody_fn.empty() && m.launches.empty() && m.scratch_bytes == 0;
+  };
+  auto sets = [&](size_t i, std::set<const void*>& reads, std::set<const void*>& writes) {
+    const RenderedKernel& m = *kernels[i];
+    for (size_t j = 0; j < args[i].size(); j++) {
+      if (!args[i][j].id) continue;
+      const bool out = j < m.params.size() && m.params[j].first == m.out_slot;
+      (out ? writes : reads).insert(args[i][j].id);
+      if (out) reads.insert(args[i][j].id);
+    }
+  };
+  std::vector<size_t> firsts;
+  for (size_t i = 0; i + 1 < n; i++) {
+    if (!pairable(i) || !pairable(i + 1)) continue;
+    const RenderedKernel &a = *kernels[i], &b = *kernels[i + 1];
+    if (a.block[0] != b.block[0] || args[i].size() + args[i + 1].size() > FG_MAX_LAUNCH_ARGS) continue;
+    std::set<const void*> ra, wa, rb, wb;
+    sets(i, ra, wa);
+    sets(i + 1, rb, wb);
+    bool indep = true;
+    for (const void* w : wa) indep = indep && !rb.count(w) && !wb.count(w);
+    for (const void* w : wb) indep = indep && !ra.count(w);
+    if (!indep) continue;
+    firsts.push_back(i);
+    i++;
+  }
+  return firsts;
 }
 
 BatchForwarding batch_forwarding(const std::vector<const RenderedKernel*>& stages,

@@ -112,6 +112,21 @@ BatchForwarding batch_forwarding(const std::vector<const RenderedKernel*>& stage
 RenderedKernel render_block_batch(const std::vector<const RenderedKernel*>& stages, bool read_back = false,
                                   const BatchForwarding* fwd = nullptr);
 
+// One launch that runs two independent kernels side by side: workgroups
+// [0, a.grid) run a's body, the rest b's (the small GEMM's block-index
+// bodies, hbody_fn). Both must have the same 1-D workgroup size; the launch
+// takes a's arguments, then b's.
+RenderedKernel render_hfused(const RenderedKernel& a, const RenderedKernel& b);
+// Adjacent kernels of a sequence that can share one launch: both one-launch
+// kernels with a block-index body (hbody_fn) and no scratch, the same
+// workgroup size, neither marked in `excluded` (kernels in a batch), at most
+// FG_MAX_LAUNCH_ARGS arguments together, and independent: neither writes a
+// buffer the other reads or writes (buffers by identity, as in
+// batch_forwarding). Taken greedily in sequence order; returns the first
+// kernel of each pair.
+std::vector<size_t> pair_runs(const std::vector<const RenderedKernel*>& kernels,
+                              const std::vector<std::vector<BatchArg>>& args, const std::vector<bool>& excluded);
+
 // The runs of consecutive block kernels a sequence launches as batches, as
 // (first, count) pairs: every run of two or more, split after kMaxBatchStages
 // kernels and before the kernel that would take the run's arguments past

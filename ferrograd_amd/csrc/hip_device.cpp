@@ -256,6 +256,10 @@ class HipDevice : public Device {
       // program, count) and the batch program of each.
       std::vector<std::pair<size_t, size_t>> groups;
       std::vector<std::shared_ptr<Program>> batches;
+      // Pairs of adjacent independent kernels launched together
+      // (render_hfused): the first program of each pair, and its launch.
+      std::vector<size_t> pair_first;
+      std::vector<std::shared_ptr<Program>> pairs;
       std::vector<size_t> order;  // launch order of the programs (empty: as given)
       // The sequence's last launch with the read-back as its last stage, when
       // that launch is a block kernel or a batch of them: from program
@@ -283,6 +287,7 @@ class HipDevice : public Device {
         ordered_args.push_back(args[k]);
       }
       group_blocks(ordered, ordered_args, r->groups, r->batches);
+      if (pairs_on()) pair_kernels(ordered, ordered_args, r->groups, r->pair_first, r->pairs);
     }
     auto prog_at = [&](size_t i) -> Program* { return r->order.empty() ? progs[i] : progs[r->order[i]]; };
     auto args_at = [&](size_t i) -> std::vector<KernelArg>& { return r->order.empty() ? args[i] : args[r->order[i]]; };
@@ -339,7 +344,7 @@ class HipDevice : public Device {
       nargs.push_back(static_cast<int>(a.size()));
       all.insert(all.end(), a.begin(), a.end());
     };
-    size_t next_group = 0;
+    size_t next_group = 0, next_pair = 0;
     for (size_t i = 0; i < progs.size(); i++) {
       if (fold_rb && i == r->rb_first) {
         std::vector<fg_arg> a;
@@ -364,6 +369,16 @@ class HipDevice : public Device {
         add(bp.prog, bp.meta.grid, bp.meta.block, bp.meta.lds_bytes, a);
         next_group++;
         i += n - 1;
+        continue;
+      }
+      if (next_pair < r->pair_first.size() && r->pair_first[next_pair] == i) {
+        std::vector<fg_arg> a = marshal(static_cast<HipProgram&>(*prog_at(i)), args_at(i));
+        std::vector<fg_arg> b = marshal(static_cast<HipProgram&>(*prog_at(i + 1)), args_at(i + 1));
+        a.insert(a.end(), b.begin(), b.end());
+        auto& pp = static_cast<HipProgram&>(*r->pairs[next_pair]);
+        add(pp.prog, pp.meta.grid, pp.meta.block, pp.meta.lds_bytes, a);
+        next_pair++;
+        i++;
         continue;
       }
       auto& p = static_cast<HipProgram&>(*prog_at(i));
@@ -397,6 +412,42 @@ class HipDevice : public Device {
       check(fg_hip_launch(ctx(), lp[i], all.data() + off, nargs[i], &grids[3 * i], &blocks[3 * i], lds[i]),
             "execution failed");
       off += static_cast<size_t>(nargs[i]);
+    }
+  }
+
+  // FG_PAIRS=0 launches every kernel of a sequence on its own (read once);
+  // pairs also need the batch pass (OPT).
+  static bool pairs_on() {
+    static const bool on = [] {
+      const char* e = std::getenv("FG_PAIRS");
+      return !(e && std::strcmp(e, "0") == 0);
+    }();
+    return on && gpu_passes().batch;
+  }
+
+  // Adjacent kernels of the sequence that share one launch (pair_runs,
+  // render_hfused); kernels in a batch stay out of pairs. Buffers are told
+  // apart by identity, as in forwarding_of.
+  void pair_kernels(const std::vector<Program*>& progs, std::vector<std::vector<KernelArg>>& args,
+                    const std::vector<std::pair<size_t, size_t>>& groups, std::vector<size_t>& pair_first,
+                    std::vector<std::shared_ptr<Program>>& pairs) {
+    const size_t n = progs.size();
+    std::vector<bool> grouped(n, false);
+    for (auto [f, c] : groups)
+      for (size_t j = f; j < f + c; j++) grouped[j] = true;
+    std::vector<const RenderedKernel*> metas;
+    std::vector<std::vector<BatchArg>> info;
+    for (size_t i = 0; i < n; i++) {
+      metas.push_back(&progs[i]->meta);
+      info.emplace_back();
+      for (auto& a : args[i])
+        info.back().push_back(a.kind == KernelArg::Kind::Buffer ? BatchArg{a.buffer.get(), a.buffer->numel}
+                                                                 : BatchArg{});
+      if (static_cast<HipProgram&>(*progs[i]).scratch) grouped[i] = true;
+    }
+    for (size_t i : pair_runs(metas, info, grouped)) {
+      pairs.push_back(compile(render_hfused(progs[i]->meta, progs[i + 1]->meta), args[i].size() + args[i + 1].size()));
+      pair_first.push_back(i);
     }
   }
 
