@@ -1653,6 +1653,11 @@ RenderedKernel render_small_gemm(const KernelInfo& ki, const GemmMatch& g, const
   const int64_t KG = (K + 15) / 16, ntm = (M + 15) / 16, ntn = (N + 15) / 16;
   const int W = small_gemm_waves(K);
   const int64_t GMAX = (KG + W - 1) / W;  // groups the busiest wave folds
+  // Groups loaded together: at most kSmallGemmMaxGroups, so a long K range
+  // (the waves are at most 16) runs as a rolled loop of such chunks instead
+  // of holding all of its operands in registers.
+  const int64_t CH = std::min<int64_t>(GMAX, kSmallGemmMaxGroups);
+  const bool chunked = CH < GMAX;
   const int NT = 64 * W;
   std::ostringstream s;
   // The kernel's body as a device function of its block index (fg_bid), so a
@@ -1670,14 +1675,18 @@ RenderedKernel render_small_gemm(const KernelInfo& ki, const GemmMatch& g, const
   s << "  const int am = m0 + r16 < " << M << " ? m0 + r16 : " << (M - 1) << ";\n";
   s << "  const int bn = n0 + r16 < " << N << " ? n0 + r16 : " << (N - 1) << ";\n";
   s << "  const bool arow = m0 + r16 < " << M << ", brow = n0 + r16 < " << N << ";\n";
-  s << "  float av[" << GMAX << "][4], bv[" << GMAX << "][4];\n";
-  // Loads of every group first (all in flight together), then the MFMAs.
+  s << "  fg_f4 acc = {0.0f, 0.0f, 0.0f, 0.0f};\n";
+  if (chunked) s << "  #pragma unroll 1\n  for (int c0 = 0; c0 < " << GMAX << "; c0 += " << CH << ") {\n";
+  else s << "  {\n  constexpr int c0 = 0;\n";
+  s << "  float av[" << CH << "][4], bv[" << CH << "][4];\n";
+  // Loads of every group of the chunk first (all in flight together), then
+  // the MFMAs.
   Emitter em;
   em.define_range(g.a.rout, "am");
   em.define_range(g.b.rout, "bn");
-  em.open_scope("#pragma unroll\nfor (int gi = 0; gi < " + std::to_string(GMAX) + "; gi++) {", "}");
-  em.line("const int kb = (gbeg + gi) * 16 + 4 * q;");
-  em.line("const bool gin = gbeg + gi < gend;");
+  em.open_scope("#pragma unroll\nfor (int gi = 0; gi < " + std::to_string(CH) + "; gi++) {", "}");
+  em.line("const int kb = (gbeg + c0 + gi) * 16 + 4 * q;");
+  em.line("const bool gin = gbeg + c0 + gi < gend;");
   if (K % 4 == 0) {
     // A lane's four k are all in range or all out: one clamped base, and the
     // four steps as lanes of that base (16-byte loads where k is unit-stride).
@@ -1705,11 +1714,11 @@ RenderedKernel render_small_gemm(const KernelInfo& ki, const GemmMatch& g, const
   }
   em.close_scope();
   s << em.code();
-  s << "  fg_f4 acc = {0.0f, 0.0f, 0.0f, 0.0f};\n"
-       "  #pragma unroll\n"
-       "  for (int gi = 0; gi < " << GMAX << "; gi++)\n"
+  s << "  #pragma unroll\n"
+       "  for (int gi = 0; gi < " << CH << "; gi++)\n"
        "    #pragma unroll\n"
        "    for (int u = 0; u < 4; u++) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av[gi][u], bv[gi][u], acc, 0, 0, 0);\n"
+       "  }\n"
        "  // D[4*(lane/16) + e][lane%16] = acc[e]\n"
        "  #pragma unroll\n"
        "  for (int e = 0; e < 4; e++) fg_part[wave][(4 * q + e) * 16 + r16] = acc[e];\n"

@@ -121,3 +121,57 @@ def test_forced_160_wide_tiles_against_float64(tile):
     env = dict(os.environ, FG_GEMM_TILE=tile)
     r = subprocess.run([sys.executable, "-c", FORCED, root], env=env, capture_output=True, text=True, timeout=240)
     assert r.returncode == 0, r.stdout + r.stderr
+
+
+# One-pass small GEMMs (M*N*K <= 2^26): forward x·Wᵀ, dX = G·W and dW = Gᵀ·X
+# of Linear layers at these (B, in, out), covering K a multiple of 4 (16-byte
+# loads of a lane's four k) and not (one element per step), ragged 16x16
+# tiles, one to sixteen waves per workgroup, and a K range long enough that
+# each wave folds its groups in rolled chunks of four ((16, 20000, 16): dW's
+# K is 16, forward's 20000).
+SMALL = [(256, 784, 128), (256, 128, 10), (65, 129, 47), (100, 8192, 20), (16, 20000, 16), (250, 96, 64)]
+
+
+def small_gemm_sources(fg, p):
+    out = {}
+    for name, t in p.items():
+        items = [it for it in fg.debug_plan([t], fuse=True, render_hip=True)["items"]
+                 if it["class"] == "gemm_mfma_f32"]
+        out[name] = items[0]["source"] if items else None
+    return out
+
+
+@pytest.mark.parametrize("shape", SMALL)
+def test_small_gemm_forms(fg, cpu, shape):
+    from hipcompile import compile_sources
+
+    B, fi, fo = shape
+    ones = np.ones
+    p = products(fg, cpu, ones((B, fi), np.float32), ones((fo, fi), np.float32), ones((B, fo), np.float32))
+    srcs = {k: v for k, v in small_gemm_sources(fg, p).items() if v}
+    assert srcs, "no product took the GEMM path"
+    for name, src in srcs.items():
+        assert "mfma_f32_16x16x4f32" in src and "_part(" not in src, name
+    if shape == (16, 20000, 16):
+        assert "for (int c0 = 0; c0 <" in srcs["fwd"]
+    compile_sources({v: k for k, v in srcs.items()}, limit_s=120)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("shape", SMALL)
+def test_small_gemms_against_float64(fg, hip, shape):
+    B, fi, fo = shape
+    print(f"small gemm products {shape}", flush=True)
+    r = np.random.default_rng(sum(shape))
+    x = r.uniform(-1, 1, (B, fi)).astype(np.float32)
+    w = r.uniform(-1, 1, (fo, fi)).astype(np.float32)
+    g = r.uniform(-1, 1, (B, fo)).astype(np.float32)
+    p = products(fg, hip, x, w, g)
+    fg.Tensor.realize_many(list(p.values()))
+    x64, w64, g64 = (a.astype(np.float64) for a in (x, w, g))
+    want = {"fwd": (x64 @ w64.T, np.abs(x64) @ np.abs(w64).T), "dx": (g64 @ w64, np.abs(g64) @ np.abs(w64)),
+            "dw": (g64.T @ x64, np.abs(g64).T @ np.abs(x64))}
+    for name, t in p.items():
+        v, sc = want[name]
+        got = t.numpy().astype(np.float64).reshape(v.shape)
+        assert rel_err_bound(got, v, sc, 1e-4) <= 1.0, name
