@@ -97,3 +97,34 @@ def test_mnist_loop_matches_cpu_on_hip(fg, cpu, hip, tmp_path):
         runs[dev] = train_mnist(MNISTDataset.load(d, dev), dev, epochs=2, batch_size=64, lr=0.05, log=None)
     np.testing.assert_allclose(runs[hip]["batch_loss"], runs[cpu]["batch_loss"], rtol=1e-4)
     assert runs[hip]["accuracy"] == runs[cpu]["accuracy"]
+
+
+def test_mnist_native_loop_matches_the_python_loop_on_cpu(fg, cpu, tmp_path):
+    # train_mnist(native=True) runs each epoch's batches through
+    # fg_mlp_train_batches (captured steps that take each batch's start as an
+    # argument): the same losses and accuracies bit for bit.
+    from ferrograd_amd.dataset import MNISTDataset
+    from ferrograd_amd.mlp import train_mnist
+
+    d, *_ = make_mnist(tmp_path)
+    runs = {}
+    for native in (False, True):
+        fg.reset_init_seed(42)
+        runs[native] = train_mnist(MNISTDataset.load(d, cpu), cpu, epochs=2, batch_size=64, lr=0.05, log=None,
+                                   native=native)
+    assert runs[True] == runs[False]
+
+
+@pytest.mark.gpu
+def test_mnist_native_loop_matches_the_python_loop_on_hip(fg, hip, tmp_path):
+    from ferrograd_amd.dataset import MNISTDataset
+    from ferrograd_amd.mlp import train_mnist
+
+    print("mnist loop, native and Python-driven, on hip", flush=True)
+    d, *_ = make_mnist(tmp_path)
+    runs = {}
+    for native in (False, True):
+        fg.reset_init_seed(42)
+        runs[native] = train_mnist(MNISTDataset.load(d, hip), hip, epochs=2, batch_size=64, lr=0.05, log=None,
+                                   native=native)
+    assert runs[True] == runs[False]
