@@ -40,6 +40,13 @@ static PyObject* wrap(PyTypeObject* tp, fg_tensor* h) {
 
 static int check_tensor(PyObject* o, TensorObject** out);
 
+/* Every op needs a handle: Tensor() without one is an empty shell. */
+static int has_handle(TensorObject* t) {
+  if (t->h) return 1;
+  PyErr_SetString(g_error_class ? g_error_class : PyExc_RuntimeError, "tensor has no handle");
+  return 0;
+}
+
 static void t_dealloc(TensorObject* self) {
   if (self->weakrefs) PyObject_ClearWeakRefs((PyObject*)self);
   if (self->h) fg_tensor_free(self->h);
@@ -69,6 +76,7 @@ static PyObject* t_get_h(TensorObject* self, void* closure) {
 }
 
 static PyObject* unary(TensorObject* self, int op) {
+  if (!has_handle(self)) return NULL;
   fg_tensor* out = NULL;
   if (fg_tensor_unary(self->h, op, &out)) return raise_last();
   return wrap(Py_TYPE(self), out);
@@ -76,7 +84,7 @@ static PyObject* unary(TensorObject* self, int op) {
 
 static PyObject* binary(TensorObject* self, PyObject* other, int op) {
   TensorObject* o;
-  if (check_tensor(other, &o)) return NULL;
+  if (check_tensor(other, &o) || !has_handle(self) || !has_handle(o)) return NULL;
   fg_tensor* out = NULL;
   if (fg_tensor_binary(self->h, o->h, op, &out)) return raise_last();
   return wrap(Py_TYPE(self), out);
@@ -106,6 +114,7 @@ static int int64s(PyObject* seq, int64_t* buf, int* n) {
 }
 
 static PyObject* reduce(TensorObject* self, PyObject* axes, int op) {
+  if (!has_handle(self)) return NULL;
   int64_t a[16];
   int n = 0;
   if (int64s(axes, a, &n)) return NULL;
@@ -115,6 +124,7 @@ static PyObject* reduce(TensorObject* self, PyObject* axes, int op) {
 }
 
 static PyObject* movement(TensorObject* self, PyObject* arg, int op) {
+  if (!has_handle(self)) return NULL;
   int64_t a[16];
   int n = 0;
   if (int64s(arg, a, &n)) return NULL;
@@ -172,6 +182,7 @@ static PyObject* t_narrow(TensorObject* self, PyObject* const* args, Py_ssize_t 
     PyErr_SetString(PyExc_TypeError, "narrow(dim, start, length)");
     return NULL;
   }
+  if (!has_handle(self)) return NULL;
   long long v[3];
   for (int i = 0; i < 3; i++) {
     v[i] = PyLong_AsLongLong(args[i]);
@@ -183,6 +194,7 @@ static PyObject* t_narrow(TensorObject* self, PyObject* const* args, Py_ssize_t 
 }
 
 static PyObject* t_log_softmax(TensorObject* self, PyObject* axis) {
+  if (!has_handle(self)) return NULL;
   long long a = PyLong_AsLongLong(axis);
   if (a == -1 && PyErr_Occurred()) return NULL;
   fg_tensor* out = NULL;
@@ -192,6 +204,7 @@ static PyObject* t_log_softmax(TensorObject* self, PyObject* axis) {
 
 static PyObject* t_realize(TensorObject* self, PyObject* unused) {
   (void)unused;
+  if (!has_handle(self)) return NULL;
   if (fg_tensor_realize_many(&self->h, 1)) return raise_last();
   Py_INCREF(self);
   return (PyObject*)self;
@@ -199,7 +212,7 @@ static PyObject* t_realize(TensorObject* self, PyObject* unused) {
 
 static PyObject* t_assign(TensorObject* self, PyObject* other) {
   TensorObject* o;
-  if (check_tensor(other, &o)) return NULL;
+  if (check_tensor(other, &o) || !has_handle(self) || !has_handle(o)) return NULL;
   if (fg_tensor_assign(self->h, o->h)) return raise_last();
   Py_INCREF(self);
   return (PyObject*)self;
