@@ -3205,7 +3205,8 @@ RenderedKernel render_block_batch(const std::vector<const RenderedKernel*>& stag
     const RenderedKernel& st = *stages[i];
     FG_CHECK(!st.stage_fn.empty(), "kernel " + st.name + " is not a block kernel");
     if (defined.insert(st.stage_fn).second) src << st.stage_src;
-    if (i) body << "  __syncthreads();\n";
+    const bool barrier = fwd && !fwd->barrier.empty() ? fwd->barrier[i] != 0 : i > 0;
+    if (barrier) body << "  __syncthreads();\n";
     body << "  " << st.stage_fn << "(";
     for (size_t j = 0; j < st.stage_types.size(); j++, n++) {
       params << (n ? ", " : "") << st.stage_types[j] << " a" << n;
@@ -3365,6 +3366,31 @@ BatchForwarding batch_forwarding(const std::vector<const RenderedKernel*>& stage
       f.arg_buffer[base + q] = k;
       lds[args[j][q].id] = k;
     }
+  }
+  // Barriers only where a stage depends on one run since the last barrier.
+  std::set<const void*> reads, writes;
+  std::set<std::string> bodies;
+  for (size_t j = 0; j < stages.size(); j++) {
+    const RenderedKernel& m = *stages[j];
+    std::set<const void*> rj, wj;
+    for (size_t q = 0; q < args[j].size(); q++) {
+      if (!args[j][q].id) continue;
+      const bool out = q < m.params.size() && m.params[q].first == m.out_slot;
+      (out ? wj : rj).insert(args[j][q].id);
+      if (out && m.reads_output) rj.insert(args[j][q].id);
+    }
+    bool dep = bodies.count(m.stage_fn) > 0;
+    for (const void* x : rj) dep = dep || writes.count(x);
+    for (const void* x : wj) dep = dep || writes.count(x) || reads.count(x);
+    f.barrier.push_back(j > 0 && dep ? 1 : 0);
+    if (j > 0 && dep) {
+      reads.clear();
+      writes.clear();
+      bodies.clear();
+    }
+    reads.insert(rj.begin(), rj.end());
+    writes.insert(wj.begin(), wj.end());
+    bodies.insert(m.stage_fn);
   }
   return f;
 }

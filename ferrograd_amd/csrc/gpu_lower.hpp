@@ -92,6 +92,11 @@ struct BatchForwarding {
   std::vector<DType> dtypes;    // per LDS array
   std::vector<size_t> numels;
   std::vector<int> out_arg;     // the producing stage's output argument (the copy's destination)
+  // Per stage: whether a workgroup barrier precedes it. A stage needs one
+  // when it reads a buffer a stage since the last barrier writes, writes one
+  // such a stage reads or writes, or shares a body (and so its LDS) with one;
+  // empty means a barrier before every stage but the first.
+  std::vector<uint8_t> barrier;
 };
 // The LDS a batch may spend on forwarded outputs (the stage bodies keep their
 // own few kilobytes).

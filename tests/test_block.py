@@ -371,3 +371,35 @@ def test_paired_small_gemms_on_hip(fg, cpu, hip):
             scale = np.abs(l.astype(np.float64)) @ np.abs(r.astype(np.float64))
             got = y.numpy().astype(np.float64).reshape(want.shape)
             assert np.all(np.abs(got - want) <= 1e-4 * scale), rep
+
+
+def test_batch_barriers_only_between_dependent_stages(fg, cpu):
+    # C4's softmax batch: the fifth stage reads only an input of the batch,
+    # so no barrier separates it from the fourth; every other stage reads its
+    # predecessor's output. One more barrier precedes the copies to the
+    # buffers.
+    from ferrograd_amd.mlp import Mlp, synthetic_batch
+
+    fg.reset_init_seed(42)
+    m = Mlp((784, 128, 10), cpu)
+    xs, ts = synthetic_batch(256, 784, 10, 7, 8)
+    loss = m.forward(fg.Tensor.new(xs, list(xs.shape), cpu)).cross_entropy(fg.Tensor.new(ts, list(ts.shape), cpu))
+    loss.backward()
+    ps = m.parameters()
+    for p in ps:
+        p.assign(p.detach().sub(p.grad().mul(fg.Tensor.scalar(0.01, cpu))))
+    plan = fg.debug_plan(ps + [loss], fuse=True, render_hip=True)
+    src = plan["batch_kernels"][0]["source"]
+    body = src[src.index('extern "C"'):]
+    assert plan["batches"][0][1] == 6 and body.count("__syncthreads();") == 5
+
+
+def test_batch_stages_sharing_a_body_keep_their_barriers(fg, cpu):
+    # Sixteen roots of one structure: every stage is the same body function,
+    # whose static LDS the next call would reuse, so even independent stages
+    # stay behind barriers.
+    roots, _ = sixteen_roots(fg, cpu)
+    plan = fg.debug_plan(roots, fuse=True, render_hip=True)
+    for (first, n), bk in zip(plan["batches"], plan["batch_kernels"]):
+        body = bk["source"][bk["source"].index('extern "C"'):]
+        assert body.count("__syncthreads();") == (n - 1) + (1 if bk["forwarded"] else 0)
