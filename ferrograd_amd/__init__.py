@@ -12,6 +12,7 @@ the import of any op raises.
 from __future__ import annotations
 
 import ctypes
+import importlib
 import os
 from typing import Iterable, Sequence
 
@@ -39,7 +40,9 @@ class FerrogradError(RuntimeError):
 # which links the native library. Until it is built (python -m
 # ferrograd_amd.build) the package imports, and lib() refuses to run.
 try:
-    from . import _fgc
+    # import_module, not `from . import`: a reload after the build must not
+    # take the None this name held before the extension existed.
+    _fgc = importlib.import_module("._fgc", __name__)
 except ImportError as _fgc_missing:  # noqa: F841
     _fgc = None
 else:
