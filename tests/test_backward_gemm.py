@@ -109,6 +109,29 @@ def test_sgd_update_fused_with_dw(fg, hip, name):
     assert err <= 1.0
 
 
+@pytest.mark.parametrize("name", sorted(SHAPES))
+def test_sgd_update_fused_with_dw_at_full_precision(fg, hip, name):
+    # With W at the scale of an initialised layer the update's own rounding,
+    # ulp(W1)/lr, is tens of times the product's error bound and hides it.
+    # With W a millionth of that, W1 is about -lr·dW and that rounding is
+    # about 2^-24 of the gradient: the fused kernel's effective gradient is
+    # then held to 1e-4·Σ|terms| of the exact product (plus 2^-22 |dW| for
+    # the f32 roundings of dW, lr·dW and the update).
+    B, fi, fo = SHAPES[name]
+    h, _, w, g = inputs(B, fi, fo, 43)
+    w = (w * np.float32(1e-6)).astype(np.float32)
+    w1 = sgd_through_dw(fg, hip, h, w, g)
+    orow = rows_of(fo, 48, 4)
+    g64, h64 = g.astype(np.float64)[:, orow], h.astype(np.float64)
+    want, scale = g64.T @ h64, np.abs(g64).T @ np.abs(h64)
+    lr32 = float(np.float32(LR))
+    geff = (w[orow].astype(np.float64) - w1[orow].astype(np.float64)) / lr32
+    ulp_term = np.spacing(np.abs(w1[orow])).astype(np.float64) / lr32
+    assert np.median(ulp_term / (1e-4 * scale)) < 0.01  # the product's own bound dominates
+    bound = 1e-4 * scale + 2.0 ** -22 * np.abs(want) + ulp_term
+    assert float(np.max(np.abs(geff - want) / bound)) <= 1.0
+
+
 @pytest.mark.parametrize("name", ["c4_l1", "c4_l2"])
 def test_backward_products_against_the_oracle(fg, cpu, name):
     B, fi, fo = SHAPES[name]
