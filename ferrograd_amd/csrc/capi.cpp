@@ -569,6 +569,26 @@ int fg_debug_plan(fg_tensor** roots, int n, int fuse, int render, char* buf, siz
         os << (i ? ", " : "") << "{\"first\": " << firsts[i] << ", \"name\": \"" << pk.name
            << "\", \"grid\": " << pk.grid[0] << ", \"source\": \"" << json_escape(pk.source) << "\"}";
       }
+      // Batches that a replayed sequence would run beside an adjacent
+      // independent small GEMM or pair (in plan order), and that launch.
+      os << "], \"hbatches\": [";
+      auto hruns = fg::hbatch_runs(all, binfo, runs, firsts);
+      for (size_t i = 0; i < hruns.size(); i++) {
+        const auto [f, c] = runs[hruns[i].group];
+        std::vector<const fg::RenderedKernel*> hb, stages;
+        std::vector<std::vector<fg::BatchArg>> args;
+        for (size_t j : hruns[i].hb) hb.push_back(&rks[j]);
+        for (size_t j = f; j < f + c; j++) {
+          stages.push_back(&rks[j]);
+          args.push_back(binfo[j]);
+        }
+        const fg::BatchForwarding fwd = fg::batch_forwarding(stages, args);
+        const fg::RenderedKernel hk = fg::render_hbatch(hb, stages, false, &fwd);
+        os << (i ? ", " : "") << "{\"hb\": [";
+        for (size_t j = 0; j < hruns[i].hb.size(); j++) os << (j ? ", " : "") << hruns[i].hb[j];
+        os << "], \"batch\": " << hruns[i].group << ", \"name\": \"" << hk.name << "\", \"grid\": " << hk.grid[0]
+           << ", \"source\": \"" << json_escape(hk.source) << "\"}";
+      }
       os << "]";
     }
     os << "}";

@@ -3185,13 +3185,13 @@ RenderedKernel render_hip_stable(const UOp& kernel) {
   return rk;
 }
 
-RenderedKernel render_block_batch(const std::vector<const RenderedKernel*>& stages, bool read_back,
-                                  const BatchForwarding* fwd) {
-  FG_CHECK(stages.size() >= (read_back ? 1u : 2u), "a batch runs at least two block kernels");
-  static const std::string kPlaceholder = "FGBATCHNAME";
-  std::ostringstream src, params, body;
-  src << kPrelude;
-  std::set<std::string> defined;
+// The batch's part of a launch: stage bodies appended to `src` (each body
+// once), parameters a<first_arg>... appended to `params`, and the statements
+// that run the stages (LDS hand-off arrays, barriers, stage calls, copies of
+// forwarded outputs, the read-back) appended to `body`.
+static void batch_part(const std::vector<const RenderedKernel*>& stages, bool read_back, const BatchForwarding* fwd,
+                       size_t first_arg, std::set<std::string>& defined, std::ostringstream& src,
+                       std::ostringstream& params, std::ostringstream& body) {
   size_t nargs = 0;
   for (auto* st : stages) nargs += st->stage_types.size();
   FG_CHECK(!fwd || fwd->arg_buffer.size() == nargs, "batch forwarding: one entry per argument");
@@ -3200,7 +3200,7 @@ RenderedKernel render_block_batch(const std::vector<const RenderedKernel*>& stag
       body << "  __shared__ __attribute__((aligned(16))) " << ctype(fwd->dtypes[k]) << " fg_fwd" << k << "["
            << fwd->numels[k] << "];\n";
   }
-  size_t n = 0;
+  size_t n = first_arg, j_all = 0;
   for (size_t i = 0; i < stages.size(); i++) {
     const RenderedKernel& st = *stages[i];
     FG_CHECK(!st.stage_fn.empty(), "kernel " + st.name + " is not a block kernel");
@@ -3208,9 +3208,9 @@ RenderedKernel render_block_batch(const std::vector<const RenderedKernel*>& stag
     const bool barrier = fwd && !fwd->barrier.empty() ? fwd->barrier[i] != 0 : i > 0;
     if (barrier) body << "  __syncthreads();\n";
     body << "  " << st.stage_fn << "(";
-    for (size_t j = 0; j < st.stage_types.size(); j++, n++) {
+    for (size_t j = 0; j < st.stage_types.size(); j++, n++, j_all++) {
       params << (n ? ", " : "") << st.stage_types[j] << " a" << n;
-      const int k = fwd ? fwd->arg_buffer[n] : -1;
+      const int k = fwd ? fwd->arg_buffer[j_all] : -1;
       body << (j ? ", " : "") << (k >= 0 ? "fg_fwd" + std::to_string(k) : "a" + std::to_string(n));
     }
     body << ");\n";
@@ -3220,29 +3220,95 @@ RenderedKernel render_block_batch(const std::vector<const RenderedKernel*>& stag
     body << "  __syncthreads();\n";
     for (size_t k = 0; k < fwd->dtypes.size(); k++)
       body << "  for (int i = threadIdx.x; i < " << fwd->numels[k] << "; i += " << kBlockThreads << ") a"
-           << fwd->out_arg[k] << "[i] = fg_fwd" << k << "[i];\n";
+           << first_arg + fwd->out_arg[k] << "[i] = fg_fwd" << k << "[i];\n";
   }
   if (read_back) {
     params << ", unsigned int* rb_dst, const unsigned int* rb_src, int rb_words";
     body << "  __syncthreads();\n"
          << "  for (int i = threadIdx.x; i < rb_words; i += " << kBlockThreads << ") rb_dst[i] = rb_src[i];\n";
   }
-  src << "extern \"C\" __global__ void __launch_bounds__(" << kBlockThreads << ") " << kPlaceholder << "("
-      << params.str() << ") {\n" << body.str() << "}\n";
-  RenderedKernel rk;
-  rk.source = src.str();
+}
+
+// Names a rendered launch by a hash of its source (the placeholder replaced).
+static void name_by_hash(RenderedKernel& rk, const std::string& placeholder, const char* cls) {
   uint64_t h = 1469598103934665603ULL;
   for (unsigned char c : rk.source) {
     h ^= c;
     h *= 1099511628211ULL;
   }
   char hex[40];
-  std::snprintf(hex, sizeof(hex), "k%012llx_batch", static_cast<unsigned long long>(h & 0xffffffffffffULL));
-  for (size_t p = rk.source.find(kPlaceholder); p != std::string::npos; p = rk.source.find(kPlaceholder, p))
-    rk.source.replace(p, kPlaceholder.size(), hex);
+  std::snprintf(hex, sizeof(hex), "k%012llx_%s", static_cast<unsigned long long>(h & 0xffffffffffffULL), cls);
+  for (size_t p = rk.source.find(placeholder); p != std::string::npos; p = rk.source.find(placeholder, p))
+    rk.source.replace(p, placeholder.size(), hex);
   rk.name = hex;
+}
+
+RenderedKernel render_block_batch(const std::vector<const RenderedKernel*>& stages, bool read_back,
+                                  const BatchForwarding* fwd) {
+  FG_CHECK(stages.size() >= (read_back ? 1u : 2u), "a batch runs at least two block kernels");
+  static const std::string kPlaceholder = "FGBATCHNAME";
+  std::ostringstream src, params, body;
+  src << kPrelude;
+  std::set<std::string> defined;
+  batch_part(stages, read_back, fwd, 0, defined, src, params, body);
+  src << "extern \"C\" __global__ void __launch_bounds__(" << kBlockThreads << ") " << kPlaceholder << "("
+      << params.str() << ") {\n" << body.str() << "}\n";
+  RenderedKernel rk;
+  rk.source = src.str();
+  name_by_hash(rk, kPlaceholder, "batch");
   rk.kind = "block_batch";
   rk.block[0] = kBlockThreads;
+  return rk;
+}
+
+RenderedKernel render_hbatch(const std::vector<const RenderedKernel*>& hb,
+                             const std::vector<const RenderedKernel*>& stages, bool read_back,
+                             const BatchForwarding* fwd) {
+  FG_CHECK(!hb.empty() && hb.size() <= 2 && !stages.empty(), "render_hbatch: one or two kernels and a batch");
+  static const std::string kPlaceholder = "FGHBATCHNAME";
+  std::ostringstream src, params, body, dispatch;
+  src << kPrelude;
+  std::set<std::string> defined;
+  size_t n = 0;
+  unsigned g0 = 0;
+  dispatch << "  if (blockIdx.x != 0u) {\n    const unsigned fg_hbid = blockIdx.x - 1u;\n";
+  for (size_t i = 0; i < hb.size(); i++) {
+    const RenderedKernel& k = *hb[i];
+    FG_CHECK(!k.hbody_fn.empty() && k.launches.empty() && k.scratch_bytes == 0,
+             "render_hbatch: " + k.name + " has no block-index body");
+    FG_CHECK(k.block[1] == 1 && k.block[2] == 1 && k.grid[1] == 1 && k.grid[2] == 1 && k.block[0] % 64 == 0 &&
+                 k.block[0] <= static_cast<unsigned>(kBlockThreads),
+             "render_hbatch: " + k.name + " is not a 1-D launch of whole waves within a block kernel's workgroup");
+    FG_CHECK(k.source.find(k.hbody_fn + "(") != std::string::npos,
+             "render_hbatch: a body is not the one its kernel calls");
+    if (defined.insert(k.hbody_fn).second) src << k.hbody_src;
+    else
+      FG_CHECK(hb[0]->hbody_src == k.hbody_src, "render_hbatch: two different bodies named " + k.hbody_fn);
+    std::ostringstream call;
+    call << k.hbody_fn << "(";
+    for (auto& t : k.hbody_types) {
+      params << (n ? ", " : "") << t << " a" << n;
+      call << "a" << n++ << ", ";
+    }
+    // Waves past the kernel's own workgroup size end at once; the body's
+    // barriers count the waves that run it.
+    const std::string run = "if (threadIdx.x < " + std::to_string(k.block[0]) + "u) " + call.str();
+    if (i + 1 < hb.size())
+      dispatch << "    if (fg_hbid < " << g0 + k.grid[0] << "u) { " << run << "fg_hbid - " << g0 << "u); }\n    else ";
+    else
+      dispatch << (i ? "{ " : "    { ") << run << "fg_hbid - " << g0 << "u); }\n";
+    g0 += k.grid[0];
+  }
+  dispatch << "    return;\n  }\n";
+  batch_part(stages, read_back, fwd, n, defined, src, params, body);
+  src << "extern \"C\" __global__ void __launch_bounds__(" << kBlockThreads << ") " << kPlaceholder << "("
+      << params.str() << ") {\n" << dispatch.str() << body.str() << "}\n";
+  RenderedKernel rk;
+  rk.source = src.str();
+  name_by_hash(rk, kPlaceholder, "hbatch");
+  rk.kind = "hbatch";
+  rk.block[0] = kBlockThreads;
+  rk.grid[0] = 1 + g0;
   return rk;
 }
 
@@ -3291,6 +3357,96 @@ RenderedKernel render_hfused(const RenderedKernel& a, const RenderedKernel& b) {
   rk.block[0] = a.block[0];
   rk.grid[0] = a.grid[0] + b.grid[0];
   return rk;
+}
+
+bool kernels_independent(const std::vector<const RenderedKernel*>& kernels,
+                         const std::vector<std::vector<BatchArg>>& args, const std::vector<size_t>& a,
+                         const std::vector<size_t>& b) {
+  auto sets = [&](const std::vector<size_t>& side, std::set<const void*>& reads, std::set<const void*>& writes) {
+    for (size_t i : side) {
+      FG_CHECK(i < kernels.size() && i < args.size(), "kernels_independent: position out of range");
+      const RenderedKernel& m = *kernels[i];
+      for (size_t j = 0; j < args[i].size(); j++) {
+        if (!args[i][j].id) continue;
+        const bool out = j < m.params.size() && m.params[j].first == m.out_slot;
+        (out ? writes : reads).insert(args[i][j].id);
+        if (out) reads.insert(args[i][j].id);
+      }
+    }
+  };
+  std::set<const void*> ra, wa, rb, wb;
+  sets(a, ra, wa);
+  sets(b, rb, wb);
+  for (const void* w : wa)
+    if (rb.count(w) || wb.count(w)) return false;
+  for (const void* w : wb)
+    if (ra.count(w)) return false;
+  return true;
+}
+
+bool hbatch_member(const RenderedKernel& k) {
+  return !k.hbody_fn.empty() && k.launches.empty() && k.scratch_bytes == 0 && k.block[1] == 1 && k.block[2] == 1 &&
+         k.grid[1] == 1 && k.grid[2] == 1 && k.block[0] % 64 == 0 && k.block[0] <= static_cast<unsigned>(kBlockThreads);
+}
+
+std::vector<HBatchRun> hbatch_runs(const std::vector<const RenderedKernel*>& kernels,
+                                   const std::vector<std::vector<BatchArg>>& args,
+                                   const std::vector<std::pair<size_t, size_t>>& groups,
+                                   const std::vector<size_t>& pair_firsts, size_t extra) {
+  FG_CHECK(kernels.size() == args.size(), "hbatch_runs: one argument list per kernel");
+  const size_t n = kernels.size();
+  // The sequence's launch units in order: (first, count, group index or -1).
+  struct Unit {
+    size_t first, count;
+    long group;
+  };
+  std::vector<Unit> units;
+  for (size_t i = 0; i < n;) {
+    long g = -1;
+    for (size_t k = 0; k < groups.size(); k++)
+      if (groups[k].first == i) g = static_cast<long>(k);
+    if (g >= 0) {
+      units.push_back({i, groups[g].second, g});
+      i += groups[g].second;
+    } else if (std::find(pair_firsts.begin(), pair_firsts.end(), i) != pair_firsts.end() && i + 1 < n) {
+      units.push_back({i, 2, -1});
+      i += 2;
+    } else {
+      units.push_back({i, 1, -1});
+      i++;
+    }
+  }
+  auto hb_unit = [&](const Unit& u) {
+    if (u.group >= 0) return false;
+    for (size_t j = u.first; j < u.first + u.count; j++)
+      if (!hbatch_member(*kernels[j])) return false;
+    return true;
+  };
+  auto nargs = [&](const Unit& u) {
+    size_t t = 0;
+    for (size_t j = u.first; j < u.first + u.count; j++) t += args[j].size();
+    return t;
+  };
+  std::vector<bool> used(units.size(), false);
+  std::vector<HBatchRun> out;
+  for (size_t u = 0; u < units.size(); u++) {
+    if (units[u].group < 0) continue;
+    for (long d : {-1L, 1L}) {
+      const long v = static_cast<long>(u) + d;
+      if (v < 0 || v >= static_cast<long>(units.size()) || used[v] || !hb_unit(units[v])) continue;
+      if (nargs(units[u]) + nargs(units[v]) + extra > FG_MAX_LAUNCH_ARGS) continue;
+      std::vector<size_t> hb, st;
+      for (size_t j = units[v].first; j < units[v].first + units[v].count; j++) hb.push_back(j);
+      for (size_t j = units[u].first; j < units[u].first + units[u].count; j++) st.push_back(j);
+      if (!kernels_independent(kernels, args, hb, st)) continue;
+      used[u] = used[v] = true;
+      out.push_back({hb, static_cast<size_t>(units[u].group)});
+      break;
+    }
+  }
+  std::sort(out.begin(), out.end(),
+            [](const HBatchRun& a, const HBatchRun& b) { return a.hb.front() < b.hb.front(); });
+  return out;
 }
 
 std::vector<size_t> pair_runs(const std::vector<const RenderedKernel*>& kernels,

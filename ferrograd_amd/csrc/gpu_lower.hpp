@@ -122,6 +122,45 @@ RenderedKernel render_block_batch(const std::vector<const RenderedKernel*>& stag
 // bodies, hbody_fn). Both must have the same 1-D workgroup size; the launch
 // takes a's arguments, then b's.
 RenderedKernel render_hfused(const RenderedKernel& a, const RenderedKernel& b);
+// One launch that runs one or two kernels with block-index bodies (hbody_fn:
+// the one-pass small GEMMs, alone or as a pair) beside a batch of block
+// kernels they share no written buffer with: workgroup 0 runs the batch (its
+// stages, LDS hand-off and read-back exactly as render_block_batch renders
+// them), the next hb[0].grid workgroups hb[0]'s body, then hb[1]'s. The
+// launch has the block kernels' workgroup size (1024); in the other
+// workgroups the waves past a body's own workgroup size end at once. The
+// launch takes each hb kernel's arguments, then the batch's.
+RenderedKernel render_hbatch(const std::vector<const RenderedKernel*>& hb,
+                             const std::vector<const RenderedKernel*>& stages, bool read_back = false,
+                             const BatchForwarding* fwd = nullptr);
+// Whether the kernels at positions `a` and those at positions `b` are
+// independent: no buffer one side writes is read or written by the other
+// (buffers by identity; a kernel's output counts as read too, for in-place
+// updates).
+bool kernels_independent(const std::vector<const RenderedKernel*>& kernels,
+                         const std::vector<std::vector<BatchArg>>& args, const std::vector<size_t>& a,
+                         const std::vector<size_t>& b);
+// Whether kernel i can run beside a batch in one launch (render_hbatch): a
+// one-launch kernel with a block-index body, no scratch, and a 1-D workgroup
+// of whole waves no larger than a block kernel's.
+bool hbatch_member(const RenderedKernel& k);
+// A launch of render_hbatch in a sequence: the kernels with block-index
+// bodies (one, or the two of a pair, in sequence order) and the batch (an
+// index into the sequence's batch runs) they run beside.
+struct HBatchRun {
+  std::vector<size_t> hb;
+  size_t group = 0;
+};
+// The hbatch launches of a sequence whose batches are `groups` (first,
+// count) and whose pairs start at `pair_firsts`: each batch joins the launch
+// unit right before it, or else the one right after it, when that unit is a
+// pair or a single kernel of hbatch_member kernels, not already joined,
+// independent of every stage of the batch, and the launch's arguments (plus
+// `extra` for a read-back) fit in FG_MAX_LAUNCH_ARGS. In sequence order.
+std::vector<HBatchRun> hbatch_runs(const std::vector<const RenderedKernel*>& kernels,
+                                   const std::vector<std::vector<BatchArg>>& args,
+                                   const std::vector<std::pair<size_t, size_t>>& groups,
+                                   const std::vector<size_t>& pair_firsts, size_t extra = 3);
 // Adjacent kernels of a sequence that can share one launch: both one-launch
 // kernels with a block-index body (hbody_fn) and no scratch, the same
 // workgroup size, neither marked in `excluded` (kernels in a batch), at most

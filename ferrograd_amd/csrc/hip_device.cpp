@@ -8,6 +8,7 @@
 
 #include "../../include/ferrograd_hip.h"
 #include "device.hpp"
+#include "hip_internal.hpp"
 #include "gpu_lower.hpp"
 #include "tensor.hpp"
 
@@ -223,6 +224,16 @@ class HipDevice : public Device {
   }
 
  private:
+  // A launch running small GEMMs beside a batch (render_hbatch): the GEMM
+  // programs (launch order), the batch's programs, the programs the launch
+  // covers, and its launch.
+  struct HBatch {
+    std::vector<size_t> hb;
+    size_t stage_first = 0, stage_count = 0;
+    size_t span_first = 0, span_count = 0;
+    std::shared_ptr<Program> prog;
+  };
+
   struct Readback {
     void* dst;        // device address of a pinned read-back slot
     const void* src;  // the result's device buffer
@@ -266,6 +277,13 @@ class HipDevice : public Device {
       // rb_first (in launch order) to the end.
       std::shared_ptr<Program> rb_batch;
       size_t rb_first = 0;
+      // With the read-back launch running a small GEMM (or a pair) beside
+      // its batch (render_hbatch): those programs, and the batch's first.
+      std::vector<size_t> rb_hb;
+      size_t rb_stage_first = 0;
+      // Launches that run a small GEMM or a pair of them beside an
+      // independent batch (render_hbatch).
+      std::vector<HBatch> hbatches;
       ~Replay() { fg_hip_graph_free(graph); }
     };
     if (!state) state = std::make_shared<Replay>();
@@ -288,6 +306,7 @@ class HipDevice : public Device {
       }
       group_blocks(ordered, ordered_args, r->groups, r->batches);
       if (pairs_on()) pair_kernels(ordered, ordered_args, r->groups, r->pair_first, r->pairs);
+      if (hbatch_on()) hbatch_kernels(ordered, ordered_args, r->groups, r->pair_first, r->hbatches);
     }
     auto prog_at = [&](size_t i) -> Program* { return r->order.empty() ? progs[i] : progs[r->order[i]]; };
     auto args_at = [&](size_t i) -> std::vector<KernelArg>& { return r->order.empty() ? args[i] : args[r->order[i]]; };
@@ -316,8 +335,31 @@ class HipDevice : public Device {
           ordered_args.push_back(args_at(j));
         }
         const BatchForwarding fwd = forwarding_of(ordered, ordered_args, first, count);
-        r->rb_batch = compile(render_block_batch(stages, true, forwarding_on() ? &fwd : nullptr), total);
-        r->rb_first = first;
+        // The batch's planned hbatch, when its small GEMM part comes first:
+        // the read-back launch runs that part too.
+        for (const HBatch& h : r->hbatches) {
+          if (h.stage_first != first || h.stage_count != count || h.hb.back() >= first) continue;
+          std::vector<const RenderedKernel*> hbm;
+          size_t hb_args = 0;
+          for (size_t j : h.hb) {
+            hbm.push_back(&ordered[j]->meta);
+            hb_args += ordered_args[j].size();
+          }
+          if (total + hb_args > FG_MAX_LAUNCH_ARGS) break;
+          auto prog = compile(render_hbatch(hbm, stages, true, forwarding_on() ? &fwd : nullptr), total + hb_args);
+          if (!fits_resident(static_cast<HipProgram&>(*prog))) break;
+          r->rb_batch = prog;
+          r->rb_first = h.hb.front();
+          r->rb_hb = h.hb;
+          r->rb_stage_first = first;
+          break;
+        }
+        if (!r->rb_batch) {
+          r->rb_batch = compile(render_block_batch(stages, true, forwarding_on() ? &fwd : nullptr), total);
+          r->rb_first = first;
+          r->rb_stage_first = first;
+          r->rb_hb.clear();
+        }
       }
     }
     const bool fold_rb = rb && r->rb_batch;
@@ -344,19 +386,38 @@ class HipDevice : public Device {
       nargs.push_back(static_cast<int>(a.size()));
       all.insert(all.end(), a.begin(), a.end());
     };
-    size_t next_group = 0, next_pair = 0;
+    size_t next_group = 0, next_pair = 0, next_hbatch = 0;
+    auto append = [&](std::vector<fg_arg>& a, size_t j) {
+      std::vector<fg_arg> aj = marshal(static_cast<HipProgram&>(*prog_at(j)), args_at(j));
+      a.insert(a.end(), aj.begin(), aj.end());
+    };
     for (size_t i = 0; i < progs.size(); i++) {
       if (fold_rb && i == r->rb_first) {
         std::vector<fg_arg> a;
-        for (size_t j = i; j < progs.size(); j++) {
-          std::vector<fg_arg> aj = marshal(static_cast<HipProgram&>(*prog_at(j)), args_at(j));
-          a.insert(a.end(), aj.begin(), aj.end());
-        }
+        for (size_t j : r->rb_hb) append(a, j);
+        for (size_t j = r->rb_stage_first; j < progs.size(); j++) append(a, j);
         std::vector<fg_arg> ra = rb_args();
         a.insert(a.end(), ra.begin(), ra.end());
         auto& bp = static_cast<HipProgram&>(*r->rb_batch);
         add(bp.prog, bp.meta.grid, bp.meta.block, bp.meta.lds_bytes, a);
         break;
+      }
+      while (next_hbatch < r->hbatches.size() && r->hbatches[next_hbatch].span_first < i) next_hbatch++;
+      if (next_hbatch < r->hbatches.size() && r->hbatches[next_hbatch].span_first == i) {
+        const HBatch& h = r->hbatches[next_hbatch++];
+        const size_t end = h.span_first + h.span_count;
+        // The sequence's last batch carries the read-back instead.
+        if (!(fold_rb && end == progs.size())) {
+          std::vector<fg_arg> a;
+          for (size_t j : h.hb) append(a, j);
+          for (size_t j = h.stage_first; j < h.stage_first + h.stage_count; j++) append(a, j);
+          auto& hp = static_cast<HipProgram&>(*h.prog);
+          add(hp.prog, hp.meta.grid, hp.meta.block, hp.meta.lds_bytes, a);
+          while (next_group < r->groups.size() && r->groups[next_group].first < end) next_group++;
+          while (next_pair < r->pair_first.size() && r->pair_first[next_pair] < end) next_pair++;
+          i = end - 1;
+          continue;
+        }
       }
       if (next_group < r->groups.size() && r->groups[next_group].first == i) {
         const size_t n = r->groups[next_group].second;
@@ -448,6 +509,65 @@ class HipDevice : public Device {
     for (size_t i : pair_runs(metas, info, grouped)) {
       pairs.push_back(compile(render_hfused(progs[i]->meta, progs[i + 1]->meta), args[i].size() + args[i + 1].size()));
       pair_first.push_back(i);
+    }
+  }
+
+  // FG_HBATCH=0 launches small GEMMs apart from the batches (read once);
+  // hbatches also need the batch pass (OPT).
+  static bool hbatch_on() {
+    static const bool on = [] {
+      const char* e = std::getenv("FG_HBATCH");
+      return !(e && std::strcmp(e, "0") == 0);
+    }();
+    return on && gpu_passes().batch;
+  }
+
+  // Whether every workgroup of a launch is resident at once, so the batch's
+  // workgroup and the small GEMM's run side by side in one round.
+  bool fits_resident(HipProgram& p) {
+    long cap = 0;
+    check(fg_hip_program_resident(ctx(), p.prog, p.meta.block[0], p.meta.lds_bytes, &cap), "fg_hip_program_resident");
+    return cap >= static_cast<long>(p.meta.grid[0]);
+  }
+
+  // Batches that run beside an adjacent independent small GEMM or pair in one
+  // launch (hbatch_runs, render_hbatch), each kept only when all of its
+  // workgroups fit on the device at once.
+  void hbatch_kernels(const std::vector<Program*>& progs, std::vector<std::vector<KernelArg>>& args,
+                      const std::vector<std::pair<size_t, size_t>>& groups, const std::vector<size_t>& pair_first,
+                      std::vector<HBatch>& out) {
+    std::vector<const RenderedKernel*> metas;
+    std::vector<std::vector<BatchArg>> info;
+    for (size_t i = 0; i < progs.size(); i++) {
+      metas.push_back(&progs[i]->meta);
+      info.emplace_back();
+      for (auto& a : args[i])
+        info.back().push_back(a.kind == KernelArg::Kind::Buffer ? BatchArg{a.buffer.get(), a.buffer->numel}
+                                                                 : BatchArg{});
+    }
+    for (const HBatchRun& run : hbatch_runs(metas, info, groups, pair_first)) {
+      const auto [first, count] = groups[run.group];
+      std::vector<const RenderedKernel*> hbm, stages;
+      size_t total = 0;
+      for (size_t j : run.hb) {
+        hbm.push_back(metas[j]);
+        total += args[j].size();
+      }
+      for (size_t j = first; j < first + count; j++) {
+        stages.push_back(metas[j]);
+        total += args[j].size();
+      }
+      const BatchForwarding fwd = forwarding_of(progs, args, first, count);
+      auto prog = compile(render_hbatch(hbm, stages, false, forwarding_on() ? &fwd : nullptr), total);
+      if (!fits_resident(static_cast<HipProgram&>(*prog))) continue;
+      HBatch h;
+      h.hb = run.hb;
+      h.stage_first = first;
+      h.stage_count = count;
+      h.span_first = std::min(run.hb.front(), first);
+      h.span_count = run.hb.size() + count;
+      h.prog = prog;
+      out.push_back(std::move(h));
     }
   }
 

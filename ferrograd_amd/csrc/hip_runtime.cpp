@@ -571,6 +571,15 @@ int fg_hip_launch_direct(fg_ctx* c, fg_prog* p, const fg_arg* args, int nargs, c
 
 int fg_hip_context_device(const fg_ctx* c) { return c ? c->device : -1; }
 
+int fg_hip_program_resident(fg_ctx* c, fg_prog* p, unsigned block, unsigned lds, long* out) {
+  if (!c || !p || !out || block == 0) return set_err(FG_ERR_INVALID, "fg_hip_program_resident: null argument");
+  int per_cu = 0, cus = 0;
+  HIP_TRY(hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, p->func, static_cast<int>(block), lds));
+  HIP_TRY(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, c->device));
+  *out = static_cast<long>(per_cu) * cus;
+  return FG_OK;
+}
+
 int fg_hip_launch(fg_ctx* c, fg_prog* p, const fg_arg* args, int nargs, const unsigned grid[3],
                   const unsigned block[3], unsigned lds) {
   if (int rc = check_launch(c, p, nargs, grid, block)) return rc;

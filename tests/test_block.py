@@ -154,8 +154,9 @@ print(json.dumps({"passes": fg.gpu_passes(), "losses": losses, "launches": launc
 """
 
 
-def run_steps(opt):
+def run_steps(opt, extra_env=None):
     env = {k: v for k, v in os.environ.items() if k != "OPT"}
+    env.update(extra_env or {})
     if opt is not None:
         env["OPT"] = opt
     print(f"C4 steps with OPT={opt}", flush=True)
@@ -185,6 +186,22 @@ def test_batched_launches_give_the_same_bits_as_one_by_one(fg, hip):
     # paired launch: six.
     assert batched["native_launches"] <= 6, batched["native_launches"]
     assert single["native_launches"] >= 7, single["native_launches"]
+
+
+@pytest.mark.gpu
+def test_small_gemms_beside_a_batch_give_the_same_bits(fg, hip):
+    # The C4 step's last launch runs the paired weight-gradient GEMMs beside
+    # the batch of bias updates, the loss and its read-back (render_hbatch):
+    # five launches per captured step, and the same losses and parameters,
+    # bit for bit, as with the two launched apart.
+    merged = run_steps(None)
+    apart = run_steps(None, {"FG_HBATCH": "0"})
+    assert merged["losses"] == apart["losses"]
+    for a, b in zip(merged["params"], apart["params"]):
+        assert np.array_equal(np.asarray(a, np.float32), np.asarray(b, np.float32))
+    assert merged["native_readback_kernels"] == 0 and apart["native_readback_kernels"] == 0
+    assert merged["native_launches"] <= 5 and apart["native_launches"] == merged["native_launches"] + 1, (
+        merged["native_launches"], apart["native_launches"])
 
 
 def test_reference_partition_small_kernels_compile_as_blocks(fg, cpu):
@@ -403,3 +420,67 @@ def test_batch_stages_sharing_a_body_keep_their_barriers(fg, cpu):
     for (first, n), bk in zip(plan["batches"], plan["batch_kernels"]):
         body = bk["source"][bk["source"].index('extern "C"'):]
         assert body.count("__syncthreads();") == (n - 1) + (1 if bk["forwarded"] else 0)
+
+
+def gemm_beside_blocks(fg, dev, seed=0, dependent=False):
+    """A C4-sized one-pass small GEMM, y = a·bᵀ ([256, 784]·[128, 784]ᵀ), and
+    two small reductions that become block kernels: of independent inputs,
+    or (dependent) of y's first rows."""
+    r = np.random.default_rng(seed)
+    ah, bh = r.standard_normal((256, 784)).astype(np.float32), r.standard_normal((128, 784)).astype(np.float32)
+    ch, dh = r.standard_normal((8, 16)).astype(np.float32), r.standard_normal((8, 16)).astype(np.float32)
+    a, b = fg.Tensor.new(ah, [256, 784], dev), fg.Tensor.new(bh, [128, 784], dev)
+    c, d = fg.Tensor.new(ch, [8, 16], dev), fg.Tensor.new(dh, [8, 16], dev)
+    y = a.matmul(b.permute([1, 0]))
+    if dependent:
+        c = y.narrow(0, 0, 8).narrow(1, 0, 16)
+    s1 = c.sum([1])
+    s2 = d.mul(fg.Tensor.scalar(2.0, dev)).max([1])
+    return (ah, bh, ch, dh), y, s1, s2
+
+
+def test_small_gemm_runs_beside_an_independent_batch(fg, cpu):
+    # A one-pass small GEMM next to a batch of block kernels it shares no
+    # buffer with: one launch of 1024-thread workgroups, the first running
+    # the batch and the others the GEMM's tiles, whose waves past the GEMM's
+    # own 832 threads end at once.
+    from hipcompile import compile_sources
+
+    _, y, s1, s2 = gemm_beside_blocks(fg, cpu)
+    p = fg.debug_plan([y, s1, s2], fuse=True, render_hip=True)
+    items = p["items"]
+    assert [it["class"] for it in items] == ["gemm_mfma_f32", "block", "block"]
+    assert p["batches"] == [[1, 2]] and len(p["hbatches"]) == 1
+    h = p["hbatches"][0]
+    assert h["hb"] == [0] and h["batch"] == 0
+    assert h["grid"] == 1 + items[0]["grid"][0]
+    src = h["source"]
+    gemm = items[0]["name"]
+    assert "__launch_bounds__(1024)" in src and f"if (threadIdx.x < {items[0]['block'][0]}u) {gemm}_hb(" in src
+    assert "if (blockIdx.x != 0u)" in src and src.count(gemm + "_hb(") == 2
+    for it in items[1:]:
+        assert it["name"] + "_body(" in src
+    compile_sources({src: h["name"]}, limit_s=120)
+
+
+def test_small_gemm_does_not_run_beside_a_batch_that_reads_it(fg, cpu):
+    _, y, s1, s2 = gemm_beside_blocks(fg, cpu, dependent=True)
+    p = fg.debug_plan([y, s1, s2], fuse=True, render_hip=True)
+    assert p["hbatches"] == []
+
+
+@pytest.mark.gpu
+def test_small_gemm_beside_a_batch_on_hip(fg, hip):
+    # Realised together three times (recorded, replayed as the merged launch,
+    # replayed as a graph): the product within 1e-4 of sum|terms| of float64,
+    # the sum likewise, and the max bit for bit.
+    print("small gemm beside a batch", flush=True)
+    for rep in range(3):
+        (ah, bh, ch, dh), y, s1, s2 = gemm_beside_blocks(fg, hip, seed=40 + rep)
+        fg.Tensor.realize_many([y, s1, s2])
+        a64, b64 = ah.astype(np.float64), bh.astype(np.float64)
+        got = y.numpy().astype(np.float64).reshape(256, 128)
+        assert np.all(np.abs(got - a64 @ b64.T) <= 1e-4 * (np.abs(a64) @ np.abs(b64).T)), rep
+        c64 = ch.astype(np.float64)
+        assert np.all(np.abs(s1.numpy().reshape(8) - c64.sum(1)) <= 1e-4 * np.abs(c64).sum(1)), rep
+        assert np.array_equal(s2.numpy().reshape(8), (dh * np.float32(2.0)).max(1)), rep
