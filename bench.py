@@ -275,18 +275,19 @@ def bench_batched_loop(fg, model, opt, batch, dims, steps, nbatches=234):
             "dataset_rows": batch * nbatches, "losses_finite": bool(np.all(np.isfinite(losses))),
             "caller": "fg_mlp_train_batches: examples/mnist.rs:84-98 with batch i = rows narrow(0, 256*i, 256) of a "
                       "resident [59904, 784] set, one call for all timed steps; captured steps take the batch start "
-                      "as a kernel argument of the replayed graph"}
+                      "as a kernel argument of their replayed launches"}
 
 
 def bench_mlp(fg, ctx, steps, warmup, batch, dims, native_steps=None, batched=False):
     from ferrograd_amd.mlp import mlp_setup, train_steps_native
 
     # The first step runs while the biases still hold allocate()'s zeros (a
-    # plan of its own); the steady-state plan then schedules and compiles, is
-    # replayed once (its block kernels batched and compiled), and is recorded
-    # as a HIP graph on its second replay. Six steps keep all of that out of
-    # the timed region, and the native warm-up call also captures its step
-    # and replays it, compiling the captured sequence's batches.
+    # plan of its own); the steady-state plan then schedules and compiles, and
+    # is replayed (its block kernels batched and compiled on the first replay;
+    # with FG_HIP_GRAPHS=1 recorded as a HIP graph on the second). Six steps
+    # keep all of that out of the timed region, and the native warm-up call
+    # also captures its step and replays it, compiling the captured
+    # sequence's batches.
     warmup = max(warmup, 6)
     step, (model, opt, x, t) = mlp_setup(fg, "hip", batch=batch, dims=dims, with_state=True)
     losses = []
@@ -322,7 +323,8 @@ def bench_mlp(fg, ctx, steps, warmup, batch, dims, native_steps=None, batched=Fa
     return {"ms_per_step": ms_native, "steps_per_s": 1e3 / ms_native,
             "caller": "native loop on one fixed resident batch (fg_mlp_train_steps: the loop body of "
                       "examples/mnist.rs:90-98, one call for all timed steps; steps after the first repeated ones "
-                      "launch from the step capture as one HIP graph); *_python: the same steps driven op by op "
+                      "launch from the step capture as one sequence of direct launches, or one HIP graph with "
+                      "FG_HIP_GRAPHS=1); *_python: the same steps driven op by op "
                       "from Python; narrowed_batches: the mnist.rs loop with a new narrow()ed batch every step",
             "narrowed_batches": narrowed,
             "native_steps": native_steps, "native_steps_from_capture": replayed,

@@ -468,8 +468,10 @@ def plan_cache(enabled: bool) -> None:
 
 
 def graph_min_launches(n: int) -> int:
-    """Record replayed plans of at least `n` launches (n >= 2) as HIP graphs;
-    shorter ones launch one by one. Returns the previous threshold."""
+    """Record replayed plans of at least `n` launches (n >= 2) as HIP graphs,
+    shorter ones launching one by one; n = 0 (the default unless
+    FG_HIP_GRAPHS=1) launches every plan one by one. Returns the previous
+    threshold."""
     prev = ctypes.c_int()
     _check(lib().fg_set_graph_min_launches(int(n), ctypes.byref(prev)))
     return prev.value

@@ -16,7 +16,13 @@ namespace fg {
 
 namespace {
 
-int g_graph_min_launches = 2;
+// Replayed sequences of at least this many launches are recorded as HIP
+// graphs; 0 launches every sequence directly (the default, FG_HIP_GRAPHS=1
+// sets 2). See graphs_enabled().
+int g_graph_min_launches = [] {
+  const char* e = std::getenv("FG_HIP_GRAPHS");
+  return e && std::strcmp(e, "1") == 0 ? 2 : 0;
+}();
 
 void check(int rc, const char* what) {
   if (rc != FG_OK) fail(std::string(what) + ": " + fg_hip_last_error());
@@ -677,21 +683,16 @@ class HipDevice : public Device {
     }
   }
 
-  // FG_HIP_GRAPHS=0 launches replayed plans one by one, and so are sequences
-  // shorter than graph_min_launches() (default 2: every multi-launch plan).
-  // On MI355X a graph launch costs about 20 us of host time plus well under
-  // 1 us per node, a direct launch 2.5-3 us; but a direct launch queued right
-  // behind a graph launch waited about as long as the graph ran on the device:
-  // with the C4 train step's 2-kernel loss plan launched directly after its
-  // 19-kernel update plan's graph, C4 ran at 4057-4455 steps/s, against
-  // 5178-5511 with both plans as graphs.
-  static bool graphs_enabled() {
-    static const bool on = [] {
-      const char* e = std::getenv("FG_HIP_GRAPHS");
-      return !(e && std::strcmp(e, "0") == 0);
-    }();
-    return on;
-  }
+  // Replayed sequences launch kernel by kernel unless graphs are on
+  // (graph_min_launches() >= 2: FG_HIP_GRAPHS=1, or fg_set_graph_min_launches).
+  // Measured on MI355X, queued behind a spinning kernel so the host does not
+  // matter: a dependent direct launch costs the device 1.5-1.75 us, a kernel
+  // node of a replayed graph 2.8-3.0 us. On the host a direct launch costs
+  // about 2.5 us, a graph launch about 20 us plus under 1 us per node. C4
+  // (five launches per step) on one box: 24.2-28.3K steps/s direct against
+  // 21.8-22.7K as graphs, 8.6-8.8K against 6.3-6.5K driven from Python; C5
+  // (24 launches, 6.9 ms) 144.6-144.8 against 143.8-144.5.
+  static bool graphs_enabled() { return graph_min_launches() >= 2; }
 
  public:
   void synchronize() override {
@@ -723,7 +724,8 @@ Device* make_hip_device() { return new HipDevice(); }
 int graph_min_launches() { return g_graph_min_launches; }
 
 int set_graph_min_launches(int n) {
-  FG_CHECK(n >= 2, "graph_min_launches: a recorded graph needs at least 2 launches, got " + std::to_string(n));
+  FG_CHECK(n == 0 || n >= 2,
+           "graph_min_launches: 0 (no graphs) or a recorded graph of at least 2 launches, got " + std::to_string(n));
   int prev = g_graph_min_launches;
   g_graph_min_launches = n;
   return prev;

@@ -165,10 +165,11 @@ int fg_clear_caches(void);
 int fg_plan_cache_enable(int on);
 int fg_plan_cache_stats(uint64_t* hits, uint64_t* misses, uint64_t* entries);
 
-/* HIP-graph replay threshold: a replayed plan with at least n kernel launches
- * (n >= 2; default 2) is recorded once as a HIP graph and relaunched as one;
- * shorter plans are launched one by one. *previous (may be NULL) receives the
- * old value. No reference counterpart. */
+/* HIP-graph replay threshold: with n >= 2 a replayed plan of at least n
+ * kernel launches is recorded once as a HIP graph and relaunched as one, and
+ * shorter plans are launched one by one; n = 0 launches every plan one by one
+ * (the default, unless FG_HIP_GRAPHS=1 sets 2). Other values fail. *previous
+ * (may be NULL) receives the old value. No reference counterpart. */
 int fg_set_graph_min_launches(int n, int* previous);
 
 /* Inspection for tests and tooling: schedule the roots (without running

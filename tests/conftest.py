@@ -1,6 +1,7 @@
 """Shared test setup: the `gpu` marker, the oracle CPU device and helpers."""
 from __future__ import annotations
 
+import contextlib
 import os
 import sys
 
@@ -94,3 +95,20 @@ def check_recorded_steps(steps, lr=0.01):
         rep = f64ref.check_mlp_step(x, t, p0, p1, loss, hidden, logits, lr)
         assert rep["ok"], (i, rep)
     return [s[4] for s in steps]
+
+
+@contextlib.contextmanager
+def graphs_on(fg, n=2):
+    """HIP-graph replay of sequences of `n` or more launches (the device's
+    default launches them one by one), restored afterwards."""
+    prev = fg.graph_min_launches(n)
+    try:
+        yield
+    finally:
+        fg.graph_min_launches(prev)
+
+
+@pytest.fixture
+def graphs(fg):
+    with graphs_on(fg):
+        yield

@@ -54,11 +54,14 @@ def test_graph_threshold_knob(fg):
     # Host-side setting only: no device is touched.
     prev = fg.graph_min_launches(5)
     try:
-        assert prev == 2  # the default: every multi-launch plan is graphed
+        # The default: every plan launches kernel by kernel (FG_HIP_GRAPHS=1: 2).
+        assert prev == (2 if os.environ.get("FG_HIP_GRAPHS") == "1" else 0)
         assert fg.graph_min_launches(3) == 5
-        with pytest.raises(fg.FerrogradError, match="at least 2 launches"):
-            fg.graph_min_launches(1)
-        assert fg.graph_min_launches(3) == 3  # a rejected value leaves the setting alone
+        for bad in (1, -1):
+            with pytest.raises(fg.FerrogradError, match="at least 2 launches"):
+                fg.graph_min_launches(bad)
+        assert fg.graph_min_launches(0) == 3  # a rejected value leaves the setting alone
+        assert fg.graph_min_launches(2) == 0
     finally:
         fg.graph_min_launches(prev)
 

@@ -376,13 +376,16 @@ def test_dependent_gemms_do_not_pair(fg, cpu):
 
 @pytest.mark.gpu
 def test_paired_small_gemms_on_hip(fg, cpu, hip):
-    # The two products realised together three times (recorded, replayed with
-    # the pair, replayed as a graph), each time against the oracle within
-    # 1e-4 of sum|terms|.
+    # The two products realised together four times (recorded, replayed with
+    # the pair, then with graphs on recorded as a graph and replayed through
+    # it), each time against the oracle within 1e-4 of sum|terms|.
+    from conftest import graphs_on
+
     print("paired small gemms", flush=True)
-    for rep in range(3):
+    for rep in range(4):
         (a, b, c, d), y1, y2 = two_products(fg, hip, seed=30 + rep)
-        fg.Tensor.realize_many([y1, y2])
+        with graphs_on(fg, 2 if rep >= 2 else 0):
+            fg.Tensor.realize_many([y1, y2])
         for y, (l, r) in ((y1, (a, b)), (y2, (c, d))):
             want = l.astype(np.float64) @ r.astype(np.float64)
             scale = np.abs(l.astype(np.float64)) @ np.abs(r.astype(np.float64))
@@ -471,13 +474,17 @@ def test_small_gemm_does_not_run_beside_a_batch_that_reads_it(fg, cpu):
 
 @pytest.mark.gpu
 def test_small_gemm_beside_a_batch_on_hip(fg, hip):
-    # Realised together three times (recorded, replayed as the merged launch,
-    # replayed as a graph): the product within 1e-4 of sum|terms| of float64,
-    # the sum likewise, and the max bit for bit.
+    # Realised together four times (recorded, replayed as the merged launch,
+    # then with graphs on recorded as a graph and replayed through it): the
+    # product within 1e-4 of sum|terms| of float64, the sum likewise, and the
+    # max bit for bit.
+    from conftest import graphs_on
+
     print("small gemm beside a batch", flush=True)
-    for rep in range(3):
+    for rep in range(4):
         (ah, bh, ch, dh), y, s1, s2 = gemm_beside_blocks(fg, hip, seed=40 + rep)
-        fg.Tensor.realize_many([y, s1, s2])
+        with graphs_on(fg, 2 if rep >= 2 else 0):
+            fg.Tensor.realize_many([y, s1, s2])
         a64, b64 = ah.astype(np.float64), bh.astype(np.float64)
         got = y.numpy().astype(np.float64).reshape(256, 128)
         assert np.all(np.abs(got - a64 @ b64.T) <= 1e-4 * (np.abs(a64) @ np.abs(b64).T)), rep

@@ -188,8 +188,8 @@ def test_in_place_update_on_hip_matches_the_oracle(fg, cpu, hip, name, n):
 
 @pytest.mark.gpu
 def test_in_place_update_replayed_on_hip(fg, cpu, hip):
-    # The same in-place program three times: recorded, replayed, replayed as
-    # a graph; each call continues from the previous one's result.
+    # The same in-place program three times: recorded, then replayed twice
+    # from the plan cache; each call continues from the previous one's result.
     print("in-place transpose_add replayed", flush=True)
     n = 12
     a = np.random.default_rng(9).uniform(-1, 1, (n, n)).astype(F)

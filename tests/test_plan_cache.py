@@ -112,10 +112,10 @@ def test_disabling_drops_recorded_plans(fg, cpu, fresh_plans):
 
 
 @pytest.mark.gpu
-def test_graph_replays_match_direct_launches_hip(fg, hip, fresh_plans):
-    # From its second replay a plan runs as one HIP graph. Every step (with
-    # the loss read back, i.e. a synchronisation, between replays) must match
-    # scheduling afresh with direct launches, bit for bit.
+def test_graph_replays_match_direct_launches_hip(fg, hip, fresh_plans, graphs):
+    # With graphs on, from its second replay a plan runs as one HIP graph.
+    # Every step (with the loss read back, i.e. a synchronisation, between
+    # replays) must match scheduling afresh with direct launches, bit for bit.
     before = fg.stats()["graph_replays"]
     l_on, p_on = train(fg, hip, 8, True)
     replays = fg.stats()["graph_replays"] - before
@@ -128,7 +128,7 @@ def test_graph_replays_match_direct_launches_hip(fg, hip, fresh_plans):
 
 
 @pytest.mark.gpu
-def test_graph_replay_with_changing_input_buffers_hip(fg, hip, fresh_plans):
+def test_graph_replay_with_changing_input_buffers_hip(fg, hip, fresh_plans, graphs):
     # The same two-kernel plan (transpose copy + GEMM with a relu epilogue)
     # over three different input buffers in turn: each replay updates the
     # graph's arguments and is checked against float64.
@@ -148,7 +148,7 @@ def test_graph_replay_with_changing_input_buffers_hip(fg, hip, fresh_plans):
 
 
 @pytest.mark.gpu
-def test_steady_state_graph_replays_keep_their_arguments_hip(fg, hip, fresh_plans):
+def test_steady_state_graph_replays_keep_their_arguments_hip(fg, hip, fresh_plans, graphs):
     # A replayed plan asks the allocator for the blocks its outputs had last
     # time; once the previous step's tensors are gone it gets them back, so the
     # recorded graph launches with no argument updates.

@@ -187,17 +187,21 @@ def test_large_random_program_on_hip(fg, hip, seed):
 @pytest.mark.gpu
 @pytest.mark.parametrize("seed,large", [(s, False) for s in SEEDS] + [(s, True) for s in LARGE_SEEDS])
 def test_random_program_replayed_on_hip(fg, hip, seed, large):
-    # The same program three times, each against float64: scheduled and run
+    # The same program four times, each against float64: scheduled and run
     # kernel by kernel, then replayed from the plan cache (runs of block
     # kernels batched with their stage outputs handed on through LDS,
-    # adjacent independent small GEMMs paired, all built on this replay),
-    # then replayed as one HIP graph.
-    print(f"random program {seed} (large={large}) three times", flush=True)
+    # adjacent independent small GEMMs paired or run beside a batch, all
+    # built on this replay), then with graphs on recorded as one HIP graph
+    # and replayed through it.
+    from conftest import graphs_on
+
+    print(f"random program {seed} (large={large}) four times", flush=True)
     before = fg.plan_stats()["hits"]
-    for rep in range(3):
-        nodes = randprog.random_program(fg, hip, seed, large=large)
-        assert randprog.check(nodes, fg) <= 1.0, rep
-    assert fg.plan_stats()["hits"] - before >= 2
+    for rep in range(4):
+        with graphs_on(fg, 2 if rep >= 2 else 0):
+            nodes = randprog.random_program(fg, hip, seed, large=large)
+            assert randprog.check(nodes, fg) <= 1.0, rep
+    assert fg.plan_stats()["hits"] - before >= 3
 
 
 def _program_gradients(fg, dev, seed, large):

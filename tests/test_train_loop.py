@@ -104,16 +104,25 @@ def test_steps_in_flight_setting(fg, cpu, depth, ok):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("graph_min", [0, 2])
 @pytest.mark.parametrize("batch,dims", [(256, (784, 128, 10)), (64, (96, 64, 32, 10))])
-def test_native_loop_matches_python_loop_hip(fg, cpu, batch, dims):
+def test_native_loop_matches_python_loop_hip(fg, cpu, batch, dims, graph_min):
+    # The captured steps launched kernel by kernel (graph_min 0, the default)
+    # or as one HIP graph each (2).
+    from conftest import graphs_on
+
+    print(f"native loop B={batch} dims={dims} graph_min={graph_min}", flush=True)
     l_py, p_py = run(fg, "hip", dims, batch, 9, native=False)
     before = fg.stats()
-    l_nat, p_nat = run(fg, "hip", dims, batch, 9, native=True)
+    with graphs_on(fg, graph_min):
+        l_nat, p_nat = run(fg, "hip", dims, batch, 9, native=True)
     assert fg.stats()["steps_replayed"] - before["steps_replayed"] >= 4
+    assert (fg.stats()["graph_replays"] > before["graph_replays"]) == (graph_min > 0)
     assert l_nat == l_py
     for a, b in zip(p_nat, p_py):
         assert np.array_equal(a, b)
-    l_ch, p_ch = run(fg, "hip", dims, batch, 9, native=True, chunks=[2, 7])
+    with graphs_on(fg, graph_min):
+        l_ch, p_ch = run(fg, "hip", dims, batch, 9, native=True, chunks=[2, 7])
     assert l_ch == l_py and all(np.array_equal(a, b) for a, b in zip(p_ch, p_py))
     # The loop's steps are the recorded steps' kernels: each step of the
     # Python-driven loop, product by product against float64 on the device's
@@ -191,19 +200,26 @@ def test_native_batched_loop_errors(fg, cpu):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("graph_min", [0, 2])
 @pytest.mark.parametrize("batch,dims", [(256, (784, 128, 10)), (64, (96, 64, 32, 10))])
-def test_native_batched_loop_matches_python_loop_hip(fg, cpu, batch, dims):
+def test_native_batched_loop_matches_python_loop_hip(fg, cpu, batch, dims, graph_min):
     # The mnist.rs loop with a new batch every step: captured steps take the
-    # batch start as a changed kernel argument of the replayed graph.
-    print(f"batched native loop B={batch} dims={dims}", flush=True)
+    # batch start as a kernel argument, launched kernel by kernel (graph_min
+    # 0, the default) or as a changed argument of the replayed graph (2).
+    from conftest import graphs_on
+
+    print(f"batched native loop B={batch} dims={dims} graph_min={graph_min}", flush=True)
     l_py, p_py = run_batches(fg, "hip", dims, batch, 7, 16, native=False)
     before = fg.stats()
-    l_nat, p_nat = run_batches(fg, "hip", dims, batch, 7, 16, native=True)
+    with graphs_on(fg, graph_min):
+        l_nat, p_nat = run_batches(fg, "hip", dims, batch, 7, 16, native=True)
     # steps 4 to 14: steps 0-3 record (zero biases, then the steady plan twice), 15 runs in full
     assert fg.stats()["steps_replayed"] - before["steps_replayed"] >= 11
+    assert (fg.stats()["graph_replays"] > before["graph_replays"]) == (graph_min > 0)
     assert l_nat == l_py
     assert all(np.array_equal(a, b) for a, b in zip(p_nat, p_py))
-    l_ch, p_ch = run_batches(fg, "hip", dims, batch, 7, 16, native=True, chunks=[3, 13])
+    with graphs_on(fg, graph_min):
+        l_ch, p_ch = run_batches(fg, "hip", dims, batch, 7, 16, native=True, chunks=[3, 13])
     assert l_ch == l_py and all(np.array_equal(a, b) for a, b in zip(p_ch, p_py))
     l_cpu, _ = run_batches(fg, cpu, dims, batch, 7, 16, native=True)
     assert np.allclose(l_nat, l_cpu, rtol=1e-4, atol=1e-6)
