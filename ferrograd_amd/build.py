@@ -26,7 +26,7 @@ HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 CXXFLAGS = ["-O2", "-g0", "-fPIC", "-std=c++17", "-Wall", "-Wno-unused-function",
             "--offload-arch=gfx950", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
             "-I" + os.path.join(ROOT, "include"), "-I" + CSRC]
-LDFLAGS = ["-shared", "-L/opt/rocm/lib", "-lhiprtc", "-lamdhip64", "-ldl",
+LDFLAGS = ["-shared", "-L/opt/rocm/lib", "-lhiprtc", "-lamdhip64", "-lhsa-runtime64", "-ldl",
            "-Wl,-rpath,/opt/rocm/lib"]
 
 

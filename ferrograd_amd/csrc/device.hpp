@@ -147,6 +147,11 @@ class Device {
     read_async(result, slot);
   }
   virtual void synchronize() {}
+  // Brackets a loop that only replays recorded sequences (the native train
+  // loop's captured steps): a device may launch them on a faster path in
+  // between. Everything queued is ordered as without the brackets.
+  virtual void begin_replay_loop() {}
+  virtual void end_replay_loop() {}
   // Whether schedule-time value-preserving fusion (shared elementwise
   // subexpressions inlined into one kernel, zero buffers folded) is enabled.
   virtual bool fuse_elementwise() const { return false; }

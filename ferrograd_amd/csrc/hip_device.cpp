@@ -223,7 +223,7 @@ class HipDevice : public Device {
     }
     void* dst = nullptr;
     check(fg_hip_read_slot(ctx(), slot, &dst), "fg_hip_read_slot");
-    Readback rb{dst, result->storage, static_cast<int>(nb / 4)};
+    Readback rb{dst, result->storage, static_cast<int>(nb / 4), slot};
     run_sequence(progs, args, state, &rb);
     check(fg_hip_read_queued(ctx(), slot, nb), "fg_hip_read_queued");
     read_bytes_[slot] = nb;
@@ -244,6 +244,7 @@ class HipDevice : public Device {
     void* dst;        // device address of a pinned read-back slot
     const void* src;  // the result's device buffer
     int words;        // 32-bit words to copy
+    int slot;         // the read-back slot
   };
 
   // The kernel that copies a read-back into its slot: lane-indexed 32-bit
@@ -457,6 +458,20 @@ class HipDevice : public Device {
     if (rb && !fold_rb) {
       HipProgram& p = readback_program();
       add(p.prog, p.meta.grid, p.meta.block, 0, rb_args());
+    }
+    if (aql_on_) {
+      // The replay loop's direct queue: one AQL packet per launch, the last
+      // one completing the read-back slot when the sequence stores into it.
+      size_t off = 0;
+      for (size_t i = 0; i < lp.size(); i++) {
+        const int sig = rb && i + 1 == lp.size() ? rb->slot : -1;
+        int rc = fg_hip_aql_launch(ctx(), lp[i], all.data() + off, nargs[i], &grids[3 * i], &blocks[3 * i], lds[i], sig);
+        if (rc == FG_AQL_UNSUPPORTED)
+          rc = fg_hip_launch(ctx(), lp[i], all.data() + off, nargs[i], &grids[3 * i], &blocks[3 * i], lds[i]);
+        check(rc, "execution failed");
+        off += static_cast<size_t>(nargs[i]);
+      }
+      return;
     }
     if (graphs_enabled() && !r->failed && !r->graph && r->uses >= 2 &&
         lp.size() >= static_cast<size_t>(graph_min_launches())) {
@@ -699,6 +714,28 @@ class HipDevice : public Device {
     if (ctx_) check(fg_hip_sync(ctx_), "fg_hip_sync");
   }
 
+  // FG_AQL=0 keeps the replay loop on hipModuleLaunchKernel (read once). On
+  // a context whose HSA queue cannot be opened the loop keeps it too.
+  void begin_replay_loop() override {
+    static const bool on = [] {
+      const char* e = std::getenv("FG_AQL");
+      return !(e && std::strcmp(e, "0") == 0);
+    }();
+    if (!on || aql_failed_ || aql_on_) return;
+    if (fg_hip_aql_begin(ctx()) != FG_OK) {
+      aql_failed_ = true;
+      if (debug_level() >= 1) std::fprintf(stderr, "*** HIP direct queue unavailable: %s\n", fg_hip_last_error());
+      return;
+    }
+    aql_on_ = true;
+  }
+
+  void end_replay_loop() override {
+    if (!aql_on_) return;
+    aql_on_ = false;
+    check(fg_hip_aql_end(ctx()), "fg_hip_aql_end");
+  }
+
   bool shares_relu_zeros() const override { return true; }
 
   // FG_FUSE=0, or an OPT list without "fuse", keeps the reference's kernel
@@ -713,6 +750,7 @@ class HipDevice : public Device {
 
  private:
   fg_ctx* ctx_ = nullptr;
+  bool aql_on_ = false, aql_failed_ = false;
   size_t read_bytes_[FG_READ_SLOTS] = {};
   std::shared_ptr<Program> readback_;
 };

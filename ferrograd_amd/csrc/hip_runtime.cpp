@@ -6,10 +6,13 @@
 #include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <hip/hiprtc.h>
+#include <hsa/hsa.h>
+#include <hsa/hsa_ext_amd.h>
 #include <sys/stat.h>
 #include <unistd.h>
 
 #include <algorithm>
+#include <chrono>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
@@ -112,9 +115,27 @@ std::string hiprtc_version() {
 
 }  // namespace
 
+struct AqlQueue;
+// The context's AQL queue while a replay loop runs on it (one HIP context per
+// process in practice); a module loaded into it is destroyed only once the
+// queue has drained.
+AqlQueue* g_active_aql = nullptr;
+void aql_drain_before_unload();
+
 struct ModuleRef {
   hipModule_t module = nullptr;
+  // The code object again, loaded by the context's own HSA queue on its
+  // first dispatch from the module (fg_hip_aql_launch).
+  std::vector<char> code;
+  bool hsa_loaded = false;
+  hsa_code_object_reader_t reader{};
+  hsa_executable_t exe{};
   ~ModuleRef() {
+    if (hsa_loaded) {
+      aql_drain_before_unload();
+      (void)hsa_executable_destroy(exe);
+      (void)hsa_code_object_reader_destroy(reader);
+    }
     if (module) (void)hipModuleUnload(module);
   }
 };
@@ -124,6 +145,29 @@ struct fg_prog {
   hipFunction_t func = nullptr;
   int num_args = 0;
   std::string name;
+  // The kernel as the HSA queue dispatches it: its descriptor and segment
+  // sizes (read on the first dispatch).
+  bool aql_loaded = false;
+  uint64_t kernel_object = 0;
+  uint32_t kernarg_size = 0, group_size = 0, private_size = 0;
+};
+
+// The context's own HSA queue, written directly by the host: a kernel launch
+// is one 64-byte AQL packet and its arguments, about 0.5 us of host time on
+// MI355X against 2.5-4 us for hipModuleLaunchKernel, for the same device
+// cost per dependent launch (1.7 us) when the arguments sit in device memory
+// and the packets fence at agent scope.
+struct AqlQueue {
+  hsa_agent_t gpu{}, cpu{};
+  hsa_queue_t* q = nullptr;
+  char* kargs = nullptr;  // a ring of argument slots in fine-grained device memory, one per queue entry
+  hsa_signal_t slot_signal[FG_READ_SLOTS] = {};
+  uint64_t slot_packet[FG_READ_SLOTS] = {};
+  bool slot_pending[FG_READ_SLOTS] = {};
+  hsa_signal_t drain{};
+  uint64_t done = 0;         // every packet below this index has completed
+  bool active = false;
+  bool first = true;         // the next packet is the first since the HIP stream ran
 };
 
 struct fg_ctx {
@@ -153,6 +197,8 @@ struct fg_ctx {
   hipEvent_t async_events[FG_READ_SLOTS] = {};
   size_t async_bytes[FG_READ_SLOTS] = {};
   bool async_pending[FG_READ_SLOTS] = {};
+  // Direct AQL dispatch (fg_hip_aql_begin / fg_hip_aql_end); null until used.
+  AqlQueue* aql = nullptr;
   // Launch profiling.
   bool profiling = false;
   std::vector<hipEvent_t> event_pool;
@@ -189,6 +235,11 @@ constexpr size_t kReadbackBytes = 1 << 20;
 constexpr size_t kMaxCachedBytes = size_t(96) << 30;
 
 size_t round_up(size_t n) { return (n + kAllocGranule - 1) / kAllocGranule * kAllocGranule; }
+// Before a HIP-stream operation while the context's AQL queue is active: the
+// queue's packets complete first (defined with the queue below).
+int aql_interlude(fg_ctx* c);
+int aql_wait(hsa_signal_t sg);
+void aql_close(AqlQueue* a);
 }  // namespace
 
 extern "C" {
@@ -226,6 +277,11 @@ int fg_hip_init(int ordinal, fg_ctx** out) {
 int fg_hip_destroy(fg_ctx* c) {
   if (!c) return FG_OK;
   // Teardown: errors here have nowhere to go, so they are not checked.
+  if (c->aql) {
+    (void)fg_hip_aql_end(c);
+    aql_close(c->aql);
+    c->aql = nullptr;
+  }
   (void)hipStreamSynchronize(c->stream);
   fg_hip_trim(c);
   for (auto& ev : c->events) (void)hipEventDestroy(ev);
@@ -271,7 +327,10 @@ int fg_hip_alloc_hint(fg_ctx* c, size_t nbytes, int zero, void* hint, void** dpt
     }
     c->sizes[p] = sz;
   }
-  if (zero) HIP_TRY(hipMemsetAsync(p, 0, sz, c->stream));
+  if (zero) {
+    if (int rc = aql_interlude(c)) return rc;
+    HIP_TRY(hipMemsetAsync(p, 0, sz, c->stream));
+  }
   *dptr = p;
   return FG_OK;
 }
@@ -283,6 +342,7 @@ int fg_hip_free(fg_ctx* c, void* p) {
   if (it == c->sizes.end()) return set_err(FG_ERR_INVALID, "fg_hip_free: pointer was not allocated by fg_hip_alloc");
   size_t sz = it->second;
   if (c->cached_bytes + sz > kMaxCachedBytes) {
+    if (int rc = aql_interlude(c)) return rc;
     HIP_TRY(hipStreamSynchronize(c->stream));
     c->sizes.erase(it);
     HIP_TRY(hipFree(p));
@@ -295,6 +355,7 @@ int fg_hip_free(fg_ctx* c, void* p) {
 
 int fg_hip_trim(fg_ctx* c) {
   if (!c) return FG_OK;
+  if (int rc = aql_interlude(c)) return rc;
   HIP_TRY(hipStreamSynchronize(c->stream));
   for (auto& kv : c->free_blocks) {
     for (void* p : kv.second) {
@@ -309,6 +370,7 @@ int fg_hip_trim(fg_ctx* c) {
 
 int fg_hip_copy_h2d(fg_ctx* c, void* dst, const void* src, size_t n) {
   if (!c || (!dst && n) || (!src && n)) return set_err(FG_ERR_INVALID, "fg_hip_copy_h2d: null argument");
+  if (int rc = aql_interlude(c)) return rc;
   if (n == 0) return FG_OK;
   if (n <= kSmallCopy) {
     // Stage through pinned memory so the copy can stay asynchronous.
@@ -331,6 +393,7 @@ int fg_hip_copy_h2d(fg_ctx* c, void* dst, const void* src, size_t n) {
 
 int fg_hip_copy_d2h(fg_ctx* c, void* dst, const void* src, size_t n) {
   if (!c || (!dst && n) || (!src && n)) return set_err(FG_ERR_INVALID, "fg_hip_copy_d2h: null argument");
+  if (int rc = aql_interlude(c)) return rc;
   if (n == 0) return fg_hip_sync(c);
   if (n <= kReadbackBytes) {
     HIP_TRY(hipMemcpyAsync(c->readback, src, n, hipMemcpyDeviceToHost, c->stream));
@@ -345,6 +408,7 @@ int fg_hip_copy_d2h(fg_ctx* c, void* dst, const void* src, size_t n) {
 
 int fg_hip_read_async(fg_ctx* c, int slot, const void* src, size_t n) {
   if (!c || (!src && n)) return set_err(FG_ERR_INVALID, "fg_hip_read_async: null argument");
+  if (int rc = aql_interlude(c)) return rc;
   if (slot < 0 || slot >= FG_READ_SLOTS)
     return set_err(FG_ERR_INVALID, "fg_hip_read_async: slot " + std::to_string(slot) + " outside 0.." +
                                        std::to_string(FG_READ_SLOTS - 1));
@@ -365,7 +429,14 @@ int fg_hip_read_slot(fg_ctx* c, int slot, void** device_ptr) {
   if (slot < 0 || slot >= FG_READ_SLOTS)
     return set_err(FG_ERR_INVALID, "fg_hip_read_slot: slot " + std::to_string(slot) + " outside 0.." +
                                        std::to_string(FG_READ_SLOTS - 1));
-  if (c->async_pending[slot]) HIP_TRY(hipEventSynchronize(c->async_events[slot]));  // its last read landed
+  if (c->aql && c->aql->slot_pending[slot]) {
+    // Its last read-back, written by a packet of the AQL queue, landed.
+    if (int rc = aql_wait(c->aql->slot_signal[slot])) return rc;
+    c->aql->slot_pending[slot] = false;
+    c->aql->done = std::max(c->aql->done, c->aql->slot_packet[slot] + 1);
+  } else if (c->async_pending[slot]) {
+    HIP_TRY(hipEventSynchronize(c->async_events[slot]));  // its last read landed
+  }
   c->async_pending[slot] = false;
   HIP_TRY(hipHostGetDevicePointer(device_ptr, c->async_read + static_cast<size_t>(slot) * FG_READ_SLOT_BYTES, 0));
   return FG_OK;
@@ -379,7 +450,12 @@ int fg_hip_read_queued(fg_ctx* c, int slot, size_t n) {
   if (n > FG_READ_SLOT_BYTES)
     return set_err(FG_ERR_INVALID, "fg_hip_read_queued: " + std::to_string(n) + " bytes exceed a slot's " +
                                        std::to_string(FG_READ_SLOT_BYTES));
-  HIP_TRY(hipEventRecord(c->async_events[slot], c->stream));
+  // A read-back stored by a packet of the AQL queue is signalled by that
+  // packet; otherwise the stream's event marks it.
+  if (!(c->aql && c->aql->slot_pending[slot])) {
+    if (int rc = aql_interlude(c)) return rc;
+    HIP_TRY(hipEventRecord(c->async_events[slot], c->stream));
+  }
   c->async_bytes[slot] = n;
   c->async_pending[slot] = true;
   return FG_OK;
@@ -393,7 +469,13 @@ int fg_hip_read_wait(fg_ctx* c, int slot, void* dst, size_t n) {
     return set_err(FG_ERR_INVALID, "fg_hip_read_wait: slot " + std::to_string(slot) + " holds " +
                                        std::to_string(c->async_bytes[slot]) + " bytes, " + std::to_string(n) +
                                        " asked for");
-  HIP_TRY(hipEventSynchronize(c->async_events[slot]));
+  if (c->aql && c->aql->slot_pending[slot]) {
+    if (int rc = aql_wait(c->aql->slot_signal[slot])) return rc;
+    c->aql->slot_pending[slot] = false;
+    c->aql->done = std::max(c->aql->done, c->aql->slot_packet[slot] + 1);
+  } else {
+    HIP_TRY(hipEventSynchronize(c->async_events[slot]));
+  }
   c->async_pending[slot] = false;
   if (n) std::memcpy(dst, c->async_read + static_cast<size_t>(slot) * FG_READ_SLOT_BYTES, n);
   return FG_OK;
@@ -401,6 +483,7 @@ int fg_hip_read_wait(fg_ctx* c, int slot, void* dst, size_t n) {
 
 int fg_hip_copy_d2d(fg_ctx* c, void* dst, const void* src, size_t n) {
   if (!c) return set_err(FG_ERR_INVALID, "fg_hip_copy_d2d: null context");
+  if (int rc = aql_interlude(c)) return rc;
   if (n == 0) return FG_OK;
   HIP_TRY(hipMemcpyAsync(dst, src, n, hipMemcpyDeviceToDevice, c->stream));
   return FG_OK;
@@ -482,6 +565,7 @@ int fg_hip_compile(fg_ctx* c, const char* source, const char* func, int num_args
     delete p;
     return set_err(FG_ERR_SYMBOL, std::string("symbol '") + func + "' not found: " + hipGetErrorString(e));
   }
+  p->module->code = std::move(code);
   *out = p;
   return FG_OK;
 }
@@ -562,6 +646,7 @@ int check_launch(const fg_ctx* c, const fg_prog* p, int nargs, const unsigned gr
 int fg_hip_launch_direct(fg_ctx* c, fg_prog* p, const fg_arg* args, int nargs, const unsigned grid[3],
                          const unsigned block[3], unsigned lds) {
   if (int rc = check_launch(c, p, nargs, grid, block)) return rc;
+  if (int rc = aql_interlude(c)) return rc;
   void* params[FG_MAX_LAUNCH_ARGS];
   if (int rc = marshal_args(args, nargs, params)) return rc;
   HIP_TRY(hipModuleLaunchKernel(p->func, grid[0], grid[1], grid[2], block[0], block[1], block[2], lds, c->stream,
@@ -570,6 +655,334 @@ int fg_hip_launch_direct(fg_ctx* c, fg_prog* p, const fg_arg* args, int nargs, c
 }
 
 int fg_hip_context_device(const fg_ctx* c) { return c ? c->device : -1; }
+
+// ── Direct AQL dispatch ─────────────────────────────────────────────────────
+namespace {
+constexpr uint32_t kAqlQueueSize = 4096;  // packets (a power of two)
+constexpr size_t kAqlArgBytes = 1024;     // argument bytes per packet
+constexpr double kAqlWaitSeconds = 120.0;
+
+int hsa_err(hsa_status_t st, const char* what) {
+  const char* m = nullptr;
+  hsa_status_string(st, &m);
+  return set_err(FG_ERR_HIP, std::string(what) + ": " + (m ? m : "HSA error"));
+}
+#define HSA_TRY(expr, what)                          \
+  do {                                               \
+    hsa_status_t _st = (expr);                       \
+    if (_st != HSA_STATUS_SUCCESS) return hsa_err(_st, what); \
+  } while (0)
+
+struct AgentSearch {
+  uint32_t bdf = 0, domain = 0;
+  hsa_agent_t gpu{}, cpu{};
+  bool have_gpu = false, have_cpu = false;
+};
+
+hsa_status_t find_agents(hsa_agent_t a, void* data) {
+  auto* s = static_cast<AgentSearch*>(data);
+  hsa_device_type_t t;
+  if (hsa_agent_get_info(a, HSA_AGENT_INFO_DEVICE, &t) != HSA_STATUS_SUCCESS) return HSA_STATUS_SUCCESS;
+  if (t == HSA_DEVICE_TYPE_CPU && !s->have_cpu) {
+    s->cpu = a;
+    s->have_cpu = true;
+  }
+  if (t == HSA_DEVICE_TYPE_GPU && !s->have_gpu) {
+    uint32_t bdf = 0, domain = 0;
+    hsa_agent_get_info(a, static_cast<hsa_agent_info_t>(HSA_AMD_AGENT_INFO_BDFID), &bdf);
+    hsa_agent_get_info(a, static_cast<hsa_agent_info_t>(HSA_AMD_AGENT_INFO_DOMAIN), &domain);
+    if (bdf == s->bdf && domain == s->domain) {
+      s->gpu = a;
+      s->have_gpu = true;
+    }
+  }
+  return HSA_STATUS_SUCCESS;
+}
+
+hsa_status_t find_fine_pool(hsa_amd_memory_pool_t p, void* data) {
+  hsa_amd_segment_t seg;
+  if (hsa_amd_memory_pool_get_info(p, HSA_AMD_MEMORY_POOL_INFO_SEGMENT, &seg) != HSA_STATUS_SUCCESS ||
+      seg != HSA_AMD_SEGMENT_GLOBAL)
+    return HSA_STATUS_SUCCESS;
+  uint32_t flags = 0;
+  hsa_amd_memory_pool_get_info(p, HSA_AMD_MEMORY_POOL_INFO_GLOBAL_FLAGS, &flags);
+  auto* out = static_cast<std::pair<bool, hsa_amd_memory_pool_t>*>(data);
+  if ((flags & HSA_AMD_MEMORY_POOL_GLOBAL_FLAG_FINE_GRAINED) && !out->first) *out = {true, p};
+  return HSA_STATUS_SUCCESS;
+}
+
+void aql_close(AqlQueue* a) {
+  if (!a) return;
+  if (a->kargs) (void)hsa_amd_memory_pool_free(a->kargs);
+  for (auto& sg : a->slot_signal)
+    if (sg.handle) (void)hsa_signal_destroy(sg);
+  if (a->drain.handle) (void)hsa_signal_destroy(a->drain);
+  if (a->q) (void)hsa_queue_destroy(a->q);
+  delete a;
+  (void)hsa_shut_down();
+}
+
+int aql_open(fg_ctx* c) {
+  if (c->aql) return FG_OK;
+  HSA_TRY(hsa_init(), "hsa_init");  // reference-counted: the HIP runtime holds its own
+  auto* a = new AqlQueue();
+  auto fail = [&](int rc) {
+    aql_close(a);
+    return rc;
+  };
+  hipDeviceProp_t prop;
+  hipError_t he = hipGetDeviceProperties(&prop, c->device);
+  if (he != hipSuccess) return fail(set_err(FG_ERR_HIP, std::string("hipGetDeviceProperties: ") + hipGetErrorString(he)));
+  AgentSearch s;
+  s.bdf = (static_cast<uint32_t>(prop.pciBusID) << 8) | (static_cast<uint32_t>(prop.pciDeviceID) << 3);
+  s.domain = static_cast<uint32_t>(prop.pciDomainID);
+  if (hsa_status_t st = hsa_iterate_agents(find_agents, &s); st != HSA_STATUS_SUCCESS)
+    return fail(hsa_err(st, "hsa_iterate_agents"));
+  if (!s.have_gpu || !s.have_cpu)
+    return fail(set_err(FG_ERR_HIP, "fg_hip_aql_begin: no HSA agent matches HIP device " + std::to_string(c->device)));
+  a->gpu = s.gpu;
+  a->cpu = s.cpu;
+  std::pair<bool, hsa_amd_memory_pool_t> pool{false, {}};
+  if (hsa_status_t st = hsa_amd_agent_iterate_memory_pools(a->gpu, find_fine_pool, &pool); st != HSA_STATUS_SUCCESS)
+    return fail(hsa_err(st, "hsa_amd_agent_iterate_memory_pools"));
+  if (!pool.first) return fail(set_err(FG_ERR_HIP, "fg_hip_aql_begin: the device has no fine-grained memory pool"));
+  if (hsa_status_t st = hsa_queue_create(a->gpu, kAqlQueueSize, HSA_QUEUE_TYPE_SINGLE, nullptr, nullptr, UINT32_MAX,
+                                         UINT32_MAX, &a->q);
+      st != HSA_STATUS_SUCCESS)
+    return fail(hsa_err(st, "hsa_queue_create"));
+  if (hsa_status_t st = hsa_amd_memory_pool_allocate(pool.second, kAqlQueueSize * kAqlArgBytes, 0,
+                                                     reinterpret_cast<void**>(&a->kargs));
+      st != HSA_STATUS_SUCCESS)
+    return fail(hsa_err(st, "hsa_amd_memory_pool_allocate"));
+  if (hsa_status_t st = hsa_amd_agents_allow_access(1, &a->cpu, nullptr, a->kargs); st != HSA_STATUS_SUCCESS)
+    return fail(hsa_err(st, "hsa_amd_agents_allow_access"));
+  std::memset(a->kargs, 0, kAqlQueueSize * kAqlArgBytes);
+  for (auto& sg : a->slot_signal)
+    if (hsa_status_t st = hsa_signal_create(0, 0, nullptr, &sg); st != HSA_STATUS_SUCCESS)
+      return fail(hsa_err(st, "hsa_signal_create"));
+  if (hsa_status_t st = hsa_signal_create(0, 0, nullptr, &a->drain); st != HSA_STATUS_SUCCESS)
+    return fail(hsa_err(st, "hsa_signal_create"));
+  c->aql = a;
+  return FG_OK;
+}
+
+// Waits (spinning) until `sg` drops below 1, for at most kAqlWaitSeconds.
+int aql_wait(hsa_signal_t sg) {
+  const auto deadline = std::chrono::steady_clock::now() + std::chrono::duration<double>(kAqlWaitSeconds);
+  while (hsa_signal_wait_scacquire(sg, HSA_SIGNAL_CONDITION_LT, 1, 1000000, HSA_WAIT_STATE_ACTIVE) >= 1)
+    if (std::chrono::steady_clock::now() > deadline)
+      return set_err(FG_ERR_HIP, "fg_hip_aql: a dispatched kernel did not complete within " +
+                                     std::to_string(static_cast<int>(kAqlWaitSeconds)) + " s");
+  return FG_OK;
+}
+
+// The next queue entry, once the packet processor has a free one and, with
+// `arg_slot`, the argument slot it shares an index with is no longer read
+// (the packet a whole queue earlier has completed).
+int aql_reserve(AqlQueue& a, uint64_t* idx, bool arg_slot);
+
+// Everything queued so far completes, its writes made visible to the host
+// and to other queues (a barrier-AND packet with system-scope fences).
+int aql_drain(AqlQueue& a) {
+  uint64_t idx = 0;
+  if (int rc = aql_reserve(a, &idx, false)) return rc;
+  auto* p = reinterpret_cast<hsa_barrier_and_packet_t*>(a.q->base_address) + (idx & (kAqlQueueSize - 1));
+  std::memset(reinterpret_cast<char*>(p) + 4, 0, sizeof(*p) - 4);
+  hsa_signal_store_relaxed(a.drain, 1);
+  p->completion_signal = a.drain;
+  const uint16_t header = (HSA_PACKET_TYPE_BARRIER_AND << HSA_PACKET_HEADER_TYPE) | (1 << HSA_PACKET_HEADER_BARRIER) |
+                          (HSA_FENCE_SCOPE_SYSTEM << HSA_PACKET_HEADER_SCACQUIRE_FENCE_SCOPE) |
+                          (HSA_FENCE_SCOPE_SYSTEM << HSA_PACKET_HEADER_SCRELEASE_FENCE_SCOPE);
+  __atomic_store_n(reinterpret_cast<uint32_t*>(p), static_cast<uint32_t>(header), __ATOMIC_RELEASE);
+  hsa_signal_store_screlease(a.q->doorbell_signal, static_cast<hsa_signal_value_t>(idx));
+  if (int rc = aql_wait(a.drain)) return rc;
+  a.done = idx + 1;
+  return FG_OK;
+}
+
+int aql_reserve(AqlQueue& a, uint64_t* idx, bool arg_slot) {
+  uint64_t w = hsa_queue_load_write_index_relaxed(a.q);
+  if (arg_slot && w >= a.done + kAqlQueueSize) {
+    // A whole queue of packets since the last one known complete: wait for
+    // all of them (only reached without read-backs to observe completions).
+    if (int rc = aql_drain(a)) return rc;
+    w = hsa_queue_load_write_index_relaxed(a.q);
+  }
+  const auto deadline = std::chrono::steady_clock::now() + std::chrono::duration<double>(kAqlWaitSeconds);
+  while (w - hsa_queue_load_read_index_scacquire(a.q) >= kAqlQueueSize)
+    if (std::chrono::steady_clock::now() > deadline)
+      return set_err(FG_ERR_HIP, "fg_hip_aql: the device read no packet for " +
+                                     std::to_string(static_cast<int>(kAqlWaitSeconds)) + " s");
+  *idx = hsa_queue_add_write_index_relaxed(a.q, 1);
+  return FG_OK;
+}
+
+// Loads the program's module into the HSA queue's agent (once per module)
+// and reads the kernel's descriptor and segment sizes.
+int aql_load(AqlQueue& a, fg_prog* p) {
+  if (p->aql_loaded) return FG_OK;
+  ModuleRef& m = *p->module;
+  if (!m.hsa_loaded) {
+    if (m.code.empty()) return set_err(FG_ERR_INVALID, "fg_hip_aql_launch: no code object for " + p->name);
+    HSA_TRY(hsa_code_object_reader_create_from_memory(m.code.data(), m.code.size(), &m.reader),
+            "hsa_code_object_reader_create_from_memory");
+    if (hsa_status_t st = hsa_executable_create_alt(HSA_PROFILE_FULL, HSA_DEFAULT_FLOAT_ROUNDING_MODE_DEFAULT, nullptr,
+                                                    &m.exe);
+        st != HSA_STATUS_SUCCESS) {
+      (void)hsa_code_object_reader_destroy(m.reader);
+      return hsa_err(st, "hsa_executable_create_alt");
+    }
+    hsa_status_t st = hsa_executable_load_agent_code_object(m.exe, a.gpu, m.reader, nullptr, nullptr);
+    if (st == HSA_STATUS_SUCCESS) st = hsa_executable_freeze(m.exe, nullptr);
+    if (st != HSA_STATUS_SUCCESS) {
+      (void)hsa_executable_destroy(m.exe);
+      (void)hsa_code_object_reader_destroy(m.reader);
+      return hsa_err(st, "hsa_executable_load_agent_code_object");
+    }
+    m.hsa_loaded = true;
+  }
+  hsa_executable_symbol_t sym;
+  HSA_TRY(hsa_executable_get_symbol_by_name(m.exe, (p->name + ".kd").c_str(), &a.gpu, &sym),
+          "hsa_executable_get_symbol_by_name");
+  HSA_TRY(hsa_executable_symbol_get_info(sym, HSA_EXECUTABLE_SYMBOL_INFO_KERNEL_OBJECT, &p->kernel_object),
+          "kernel object");
+  HSA_TRY(hsa_executable_symbol_get_info(sym, HSA_EXECUTABLE_SYMBOL_INFO_KERNEL_KERNARG_SEGMENT_SIZE, &p->kernarg_size),
+          "kernarg segment size");
+  HSA_TRY(hsa_executable_symbol_get_info(sym, HSA_EXECUTABLE_SYMBOL_INFO_KERNEL_GROUP_SEGMENT_SIZE, &p->group_size),
+          "group segment size");
+  HSA_TRY(hsa_executable_symbol_get_info(sym, HSA_EXECUTABLE_SYMBOL_INFO_KERNEL_PRIVATE_SEGMENT_SIZE, &p->private_size),
+          "private segment size");
+  p->aql_loaded = true;
+  return FG_OK;
+}
+
+// The explicit arguments at their natural alignment (the AMDGPU kernel ABI:
+// pointers at multiples of 8, i32/f32 of 4, bool of 1); returns the end
+// offset, or 0 with `ok` false when they do not fit in `cap` bytes.
+size_t aql_pack(const fg_arg* args, int nargs, char* out, size_t cap, bool* ok) {
+  size_t off = 0;
+  *ok = true;
+  for (int i = 0; i < nargs; i++) {
+    size_t sz = 0;
+    const void* v = nullptr;
+    switch (args[i].kind) {
+      case FG_ARG_PTR: sz = 8; v = &args[i].v.p; break;
+      case FG_ARG_I32: sz = 4; v = &args[i].v.i; break;
+      case FG_ARG_F32: sz = 4; v = &args[i].v.f; break;
+      default: sz = 1; v = &args[i].v.b; break;
+    }
+    off = (off + sz - 1) / sz * sz;
+    if (off + sz > cap) {
+      *ok = false;
+      return 0;
+    }
+    if (out) std::memcpy(out + off, v, sz);
+    off += sz;
+  }
+  return off;
+}
+
+// Before a HIP-stream operation while the queue is active: everything the
+// queue holds completes first, and the queue's next packet waits for the
+// stream (fg_hip_aql_launch synchronises it).
+int aql_interlude(fg_ctx* c) {
+  if (!c || !c->aql || !c->aql->active) return FG_OK;
+  if (c->aql->first) return FG_OK;  // nothing queued since the stream last ran
+  if (int rc = aql_drain(*c->aql)) return rc;
+  c->aql->first = true;
+  return FG_OK;
+}
+}  // namespace
+
+}  // extern "C"
+
+void aql_drain_before_unload() {
+  if (g_active_aql && !g_active_aql->first) (void)aql_drain(*g_active_aql);
+}
+
+extern "C" {
+
+int fg_hip_aql_begin(fg_ctx* c) {
+  if (!c) return set_err(FG_ERR_INVALID, "fg_hip_aql_begin: null context");
+  if (int rc = aql_open(c)) return rc;
+  c->aql->active = true;
+  c->aql->first = true;
+  g_active_aql = c->aql;
+  return FG_OK;
+}
+
+int fg_hip_aql_end(fg_ctx* c) {
+  if (!c || !c->aql || !c->aql->active) return FG_OK;
+  int rc = c->aql->first ? FG_OK : aql_drain(*c->aql);
+  c->aql->active = false;
+  c->aql->first = true;
+  if (g_active_aql == c->aql) g_active_aql = nullptr;
+  return rc;
+}
+
+int fg_hip_aql_active(const fg_ctx* c) { return c && c->aql && c->aql->active ? 1 : 0; }
+
+int fg_hip_aql_launch(fg_ctx* c, fg_prog* p, const fg_arg* args, int nargs, const unsigned grid[3],
+                      const unsigned block[3], unsigned lds, int signal_slot) {
+  if (int rc = check_launch(c, p, nargs, grid, block)) return rc;
+  if (!c->aql || !c->aql->active) return set_err(FG_ERR_INVALID, "fg_hip_aql_launch: no active queue");
+  if (c->profiling) return FG_AQL_UNSUPPORTED;  // profiled launches keep their dispatch-attached events
+  if (signal_slot >= FG_READ_SLOTS) return set_err(FG_ERR_INVALID, "fg_hip_aql_launch: read-back slot out of range");
+  AqlQueue& a = *c->aql;
+  if (int rc = aql_load(a, p)) return rc;
+  bool fits = false;
+  const size_t end = aql_pack(args, nargs, nullptr, kAqlArgBytes, &fits);
+  // Kernels reading hidden arguments (a kernarg segment beyond the explicit
+  // ones) and oversized argument lists take the HIP path.
+  if (!fits || p->kernarg_size > kAqlArgBytes || p->kernarg_size > (end + 15) / 16 * 16) return FG_AQL_UNSUPPORTED;
+  if (a.first) {
+    // The stream's work (copies, zero fills, launches) precedes this packet.
+    HIP_TRY(hipStreamSynchronize(c->stream));
+  }
+  uint64_t idx = 0;
+  if (int rc = aql_reserve(a, &idx, true)) return rc;
+  char* karg = a.kargs + (idx & (kAqlQueueSize - 1)) * kAqlArgBytes;
+  bool ok = false;
+  aql_pack(args, nargs, karg, kAqlArgBytes, &ok);
+  if (p->kernarg_size > end) std::memset(karg + end, 0, p->kernarg_size - end);
+  auto* pk = reinterpret_cast<hsa_kernel_dispatch_packet_t*>(a.q->base_address) + (idx & (kAqlQueueSize - 1));
+  pk->workgroup_size_x = static_cast<uint16_t>(block[0]);
+  pk->workgroup_size_y = static_cast<uint16_t>(block[1]);
+  pk->workgroup_size_z = static_cast<uint16_t>(block[2]);
+  pk->reserved0 = 0;
+  pk->grid_size_x = grid[0] * block[0];
+  pk->grid_size_y = grid[1] * block[1];
+  pk->grid_size_z = grid[2] * block[2];
+  pk->private_segment_size = p->private_size;
+  pk->group_segment_size = p->group_size + lds;
+  pk->kernel_object = p->kernel_object;
+  pk->kernarg_address = karg;
+  pk->reserved2 = 0;
+  hsa_fence_scope_t release = HSA_FENCE_SCOPE_AGENT;
+  pk->completion_signal = hsa_signal_t{0};
+  if (signal_slot >= 0) {
+    // The sequence's read-back: its store into pinned host memory is made
+    // visible to the host before the slot's signal drops.
+    hsa_signal_store_relaxed(a.slot_signal[signal_slot], 1);
+    pk->completion_signal = a.slot_signal[signal_slot];
+    a.slot_packet[signal_slot] = idx;
+    a.slot_pending[signal_slot] = true;
+    release = HSA_FENCE_SCOPE_SYSTEM;
+  }
+  const hsa_fence_scope_t acquire = a.first ? HSA_FENCE_SCOPE_SYSTEM : HSA_FENCE_SCOPE_AGENT;
+  a.first = false;
+  // The arguments sit in write-combined device memory: flush them before the
+  // packet becomes valid.
+  __builtin_ia32_sfence();
+  const uint16_t dims = grid[2] * block[2] > 1 ? 3 : grid[1] * block[1] > 1 ? 2 : 1;
+  const uint16_t setup = static_cast<uint16_t>(dims << HSA_KERNEL_DISPATCH_PACKET_SETUP_DIMENSIONS);
+  const uint16_t header = (HSA_PACKET_TYPE_KERNEL_DISPATCH << HSA_PACKET_HEADER_TYPE) |
+                          (1 << HSA_PACKET_HEADER_BARRIER) | (acquire << HSA_PACKET_HEADER_SCACQUIRE_FENCE_SCOPE) |
+                          (release << HSA_PACKET_HEADER_SCRELEASE_FENCE_SCOPE);
+  __atomic_store_n(reinterpret_cast<uint32_t*>(pk), header | (static_cast<uint32_t>(setup) << 16), __ATOMIC_RELEASE);
+  hsa_signal_store_screlease(a.q->doorbell_signal, static_cast<hsa_signal_value_t>(idx));
+  return FG_OK;
+}
 
 int fg_hip_program_resident(fg_ctx* c, fg_prog* p, unsigned block, unsigned lds, long* out) {
   if (!c || !p || !out || block == 0) return set_err(FG_ERR_INVALID, "fg_hip_program_resident: null argument");
@@ -583,6 +996,7 @@ int fg_hip_program_resident(fg_ctx* c, fg_prog* p, unsigned block, unsigned lds,
 int fg_hip_launch(fg_ctx* c, fg_prog* p, const fg_arg* args, int nargs, const unsigned grid[3],
                   const unsigned block[3], unsigned lds) {
   if (int rc = check_launch(c, p, nargs, grid, block)) return rc;
+  if (int rc = aql_interlude(c)) return rc;
   void* params[FG_MAX_LAUNCH_ARGS];
   if (int rc = marshal_args(args, nargs, params)) return rc;
   if (c->profiling) {
@@ -670,6 +1084,7 @@ int fg_hip_graph_create(fg_ctx* c, int n, fg_prog* const* progs, const unsigned*
 
 int fg_hip_graph_launch(fg_ctx* c, fg_graph* g, const fg_arg* args, int* updated) {
   if (!c || !g || !args) return set_err(FG_ERR_INVALID, "fg_hip_graph_launch: null argument");
+  if (int rc = aql_interlude(c)) return rc;
   size_t off = 0;
   if (updated) *updated = 0;
   if (c->profiling) {
@@ -737,6 +1152,7 @@ int fg_hip_profile_read(fg_ctx* c, char* buf, size_t len, size_t* needed) {
 
 int fg_hip_sync(fg_ctx* c) {
   if (!c) return set_err(FG_ERR_INVALID, "fg_hip_sync: null context");
+  if (int rc = aql_interlude(c)) return rc;
   HIP_TRY(hipStreamSynchronize(c->stream));
   return FG_OK;
 }

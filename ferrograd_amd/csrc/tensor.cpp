@@ -1426,13 +1426,37 @@ std::vector<float> train_steps(const std::vector<const Linear*>& layers, const S
   std::unique_ptr<CapturedStep> cap;
   std::vector<ReplayRecord> prev;
   bool prev_valid = false;
+  // The captured steps run between the device's replay-loop brackets (the
+  // HIP device's direct queue); a step built in full runs outside them.
+  struct ReplayLoop {
+    Device& d;
+    bool on = false;
+    void begin() {
+      if (!on) d.begin_replay_loop();
+      on = true;
+    }
+    void end() {
+      if (on) {
+        on = false;
+        d.end_replay_loop();
+      }
+    }
+    ~ReplayLoop() {
+      try {
+        end();
+      } catch (...) {
+      }
+    }
+  } loop{dev};
   for (int i = 0; i < steps; i++) {
     if (cap && i + 1 < steps) {
+      loop.begin();
       replay_step(dev, *cap, slot(i), start_of(i));
       realize_stats().steps_replayed++;
       if (i >= in_flight - 1) collect(i - (in_flight - 1));
       continue;
     }
+    loop.end();
     StepRecorder rec;
     {
       RecorderScope scope(capture && !cap ? &rec : nullptr);
@@ -1457,6 +1481,7 @@ std::vector<float> train_steps(const std::vector<const Linear*>& layers, const S
     }
     if (i >= in_flight - 1) collect(i - (in_flight - 1));
   }
+  loop.end();
   for (int i = std::max(0, steps - (in_flight - 1)); i < steps; i++) collect(i);
   return losses;
 }

@@ -189,6 +189,18 @@ def test_batched_launches_give_the_same_bits_as_one_by_one(fg, hip):
 
 
 @pytest.mark.gpu
+def test_direct_queue_gives_the_same_bits(fg, hip):
+    # The native loop's captured steps dispatched as AQL packets into the
+    # context's own HSA queue (the default) against hipModuleLaunchKernel
+    # (FG_AQL=0): the same losses and parameters, bit for bit.
+    aql = run_steps(None)
+    hip_launches = run_steps(None, {"FG_AQL": "0"})
+    assert aql["losses"] == hip_launches["losses"]
+    for a, b in zip(aql["params"], hip_launches["params"]):
+        assert np.array_equal(np.asarray(a, np.float32), np.asarray(b, np.float32))
+
+
+@pytest.mark.gpu
 def test_small_gemms_beside_a_batch_give_the_same_bits(fg, hip):
     # The C4 step's last launch runs the paired weight-gradient GEMMs beside
     # the batch of bias updates, the loss and its read-back (render_hbatch):

@@ -107,8 +107,9 @@ def test_steps_in_flight_setting(fg, cpu, depth, ok):
 @pytest.mark.parametrize("graph_min", [0, 2])
 @pytest.mark.parametrize("batch,dims", [(256, (784, 128, 10)), (64, (96, 64, 32, 10))])
 def test_native_loop_matches_python_loop_hip(fg, cpu, batch, dims, graph_min):
-    # The captured steps launched kernel by kernel (graph_min 0, the default)
-    # or as one HIP graph each (2).
+    # With replayed plans launched kernel by kernel (graph_min 0, the
+    # default) or as HIP graphs (2): the steps built in full differ, the
+    # captured steps go through the direct queue either way.
     from conftest import graphs_on
 
     print(f"native loop B={batch} dims={dims} graph_min={graph_min}", flush=True)
@@ -204,8 +205,8 @@ def test_native_batched_loop_errors(fg, cpu):
 @pytest.mark.parametrize("batch,dims", [(256, (784, 128, 10)), (64, (96, 64, 32, 10))])
 def test_native_batched_loop_matches_python_loop_hip(fg, cpu, batch, dims, graph_min):
     # The mnist.rs loop with a new batch every step: captured steps take the
-    # batch start as a kernel argument, launched kernel by kernel (graph_min
-    # 0, the default) or as a changed argument of the replayed graph (2).
+    # batch start as a kernel argument; replayed plans launch kernel by kernel
+    # (graph_min 0, the default) or as HIP graphs (2).
     from conftest import graphs_on
 
     print(f"batched native loop B={batch} dims={dims} graph_min={graph_min}", flush=True)
