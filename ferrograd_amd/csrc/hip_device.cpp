@@ -199,10 +199,13 @@ class HipDevice : public Device {
     }
   }
 
-  // A replayed plan: launched one by one the first time, then recorded once
-  // as a HIP graph and replayed through it (one graph launch, with only the
-  // changed launch arguments updated). A sequence whose graph cannot be built
-  // keeps launching one by one.
+  // A replayed plan: its runs of block kernels batched, independent small
+  // GEMMs paired or run beside a batch, then launched kernel by kernel (in
+  // the native loop's replay brackets, as packets of the context's own AQL
+  // queue); with graphs on, recorded once as a HIP graph from its second use
+  // and replayed through it (one graph launch, with only the changed launch
+  // arguments updated; a sequence whose graph cannot be built keeps
+  // launching one by one).
   void execute_sequence(const std::vector<Program*>& progs, std::vector<std::vector<KernelArg>>& args,
                         std::shared_ptr<void>& state) override {
     run_sequence(progs, args, state, nullptr);

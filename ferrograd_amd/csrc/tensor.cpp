@@ -1385,8 +1385,10 @@ void Sgd::step() const {  // optim.rs:60-71
 //   host work overlaps the device's.
 // - Step capture: once two consecutive steps replayed the same recorded plans
 //   over the same parameter and input buffers, the following steps launch
-//   that kernel sequence directly, as one device sequence (one HIP graph),
-//   without rebuilding the lazy graphs; only their losses are read. The last
+//   that kernel sequence directly, as one device sequence (on the HIP device
+//   written as AQL packets into its own queue between the replay-loop
+//   brackets), without rebuilding the lazy graphs; only their losses are
+//   read. The last
 //   step always runs in full, so the parameters, their gradients and every
 //   live tensor end as after `steps` ordinary steps.
 std::vector<float> train_steps(const std::vector<const Linear*>& layers, const Sgd& opt, const Tensor& x,
