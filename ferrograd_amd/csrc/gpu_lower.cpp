@@ -3112,6 +3112,23 @@ RenderedKernel render_hip(const UOp& kernel, const std::string& name, int force_
                                                          " outputs; kernel indexes are int32 (at most 2^31-1)");
   FG_CHECK(!nests_reduce_over_same_range(kernel),
            "kernel nests a reduction inside another over the same range; it must be materialised first");
+  std::vector<std::pair<int, DType>> params;
+  for (auto& [slot, p] : ki.params) params.emplace_back(slot, p.dtype());
+  if (total_outputs(ki) == 0) {
+    // An output axis of extent 0: no element to compute, as the reference's
+    // loop nest runs no iteration. One launch that does nothing keeps the
+    // sequence uniform (the classes' launch shapes assume an output).
+    RenderedKernel rk;
+    rk.name = name + "_empty";
+    rk.kind = "empty";
+    rk.source = std::string(kPrelude) + signature(ki, rk.name, 64) + " {}\n";
+    rk.block[0] = 64;
+    rk.grid[0] = 1;
+    rk.params = params;
+    rk.out_slot = static_cast<int>(ki.out_param.arg().a);
+    rk.out_count = 0;
+    return rk;
+  }
   // An in-place update that reads its destination at another index has one
   // valid order, the reference's sequential one, whatever class is asked for.
   KernelClass k = reads_dest_elsewhere(ki)  ? KernelClass::Sequential
@@ -3121,8 +3138,6 @@ RenderedKernel render_hip(const UOp& kernel, const std::string& name, int force_
   // The symbol carries the lowering class so profiles name what ran.
   static const char* suffix[] = {"_gemm", "_ew", "_rowred", "_colred", "_serial", "_ngemm", "_blk", "_seq"};
   const std::string sym = name + suffix[static_cast<int>(k)];
-  std::vector<std::pair<int, DType>> params;
-  for (auto& [slot, p] : ki.params) params.emplace_back(slot, p.dtype());
   RenderedKernel rk;
   switch (k) {
     case KernelClass::Gemm: {
