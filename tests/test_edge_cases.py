@@ -72,3 +72,59 @@ def test_empty_axes_on_hip_match_the_oracle(fg, cpu, hip, name):
     want, _ = run(fg, cpu, name)
     got, _ = run(fg, hip, name)
     assert np.array_equal(got, want)
+
+
+# Ragged shapes: extents that are not multiples of the 4-wide lanes, of the
+# workgroup tiles or of the MFMA tiles, at sizes above the one-workgroup
+# limits. Elementwise results and maxima are bit-exact against the oracle;
+# sums and products are within 1e-4 of the sum of their terms' magnitudes.
+RAGGED = {
+    "add_67x131": ((67, 131), (67, 131), lambda x, y: x.add(y), lambda a, b: a + b, "exact"),
+    "relu_mul_4099": ((4099,), (4099,), lambda x, y: x.mul(y).relu(), lambda a, b: np.maximum(a * b, 0), "exact"),
+    "max_rows_67x4099": ((67, 4099), None, lambda x, y: x.max([1]), lambda a, b: a.max(1, keepdims=True), "exact"),
+    "sum_rows_67x4099": ((67, 4099), None, lambda x, y: x.sum([1]), lambda a, b: a.sum(1, keepdims=True),
+                         lambda a, b: np.abs(a).sum(1, keepdims=True)),
+    "sum_cols_4099x67": ((4099, 67), None, lambda x, y: x.sum([0]), lambda a, b: a.sum(0, keepdims=True),
+                         lambda a, b: np.abs(a).sum(0, keepdims=True)),
+    "matmul_257x131x263": ((257, 131), (131, 263), lambda x, y: x.matmul(y), lambda a, b: a @ b,
+                           lambda a, b: np.abs(a) @ np.abs(b)),
+    "matmul_1031x517x33": ((1031, 517), (517, 33), lambda x, y: x.matmul(y), lambda a, b: a @ b,
+                           lambda a, b: np.abs(a) @ np.abs(b)),
+}
+
+
+def ragged_run(fg, dev, name, seed=5):
+    sa, sb, op, _, _ = RAGGED[name]
+    r = np.random.default_rng(seed)
+    a = r.uniform(-1, 1, sa).astype(F)
+    b = r.uniform(-1, 1, sb).astype(F) if sb else None
+    x = fg.Tensor.new(a, list(sa), dev)
+    y = fg.Tensor.new(b, list(sb), dev) if sb else None
+    return a, b, np.asarray(op(x, y).to_vec(), F)
+
+
+@pytest.mark.parametrize("name", sorted(RAGGED))
+def test_ragged_shapes_on_the_oracle(fg, cpu, name):
+    a, b, got = ragged_run(fg, cpu, name)
+    _, _, _, ref, tol = RAGGED[name]
+    a64, b64 = a.astype(np.float64), (b.astype(np.float64) if b is not None else None)
+    want = np.asarray(ref(a64, b64)).reshape(-1)
+    if tol == "exact":
+        assert np.array_equal(got, np.asarray(ref(a, b), F).reshape(-1))
+    else:
+        assert np.all(np.abs(got - want) <= 1e-4 * np.asarray(tol(a64, b64)).reshape(-1) + 1e-30)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("name", sorted(RAGGED))
+def test_ragged_shapes_on_hip_match_the_oracle(fg, cpu, hip, name):
+    print(f"ragged case {name}", flush=True)
+    a, b, want = ragged_run(fg, cpu, name)
+    _, _, got = ragged_run(fg, hip, name)
+    tol = RAGGED[name][4]
+    if tol == "exact":
+        assert np.array_equal(got, want)
+    else:
+        a64, b64 = a.astype(np.float64), (b.astype(np.float64) if b is not None else None)
+        scale = np.asarray(tol(a64, b64)).reshape(-1)
+        assert np.all(np.abs(got.astype(np.float64) - want) <= 1e-4 * scale + 1e-30)
