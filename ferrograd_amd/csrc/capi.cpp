@@ -515,7 +515,7 @@ int fg_debug_plan(fg_tensor** roots, int n, int fuse, int render, char* buf, siz
         if (render) {
           fg::UOp rangeified = fg::rangeify(it.sink);
           os << ", \"kernel\": \"" << json_escape(fg::kernel_to_text(rangeified)) << "\"";
-          fg::UOp k = fg::gpu_optimize(rangeified);
+          fg::UOp k = fg::with_all_params(fg::gpu_optimize(rangeified), it.sink);
           auto rk = fg::render_hip_stable(k);
           os << ", \"name\": \"" << rk.name << "\", \"class\": \"" << rk.kind << "\", \"base_class\": \""
              << fg::kernel_class_name(fg::base_class(k)) << "\", \"grid\": [" << rk.grid[0] << ", " << rk.grid[1] << ", "

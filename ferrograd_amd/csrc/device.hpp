@@ -128,6 +128,12 @@ class Device {
 
   // Kernel pipeline after rangeify.
   virtual UOp optimize(const UOp& rangeified) = 0;
+  // The optimized kernel made ready to render against the scheduled one it
+  // came from (the HIP device keeps every parameter in its signature).
+  virtual UOp bind_params(const UOp& optimized, const UOp& scheduled) {
+    (void)scheduled;
+    return optimized;
+  }
   virtual RenderedKernel render(const UOp& optimized, const std::string& name) = 0;
   virtual std::shared_ptr<Program> compile(const RenderedKernel& rk, size_t num_args) = 0;
   virtual void execute(Program& p, std::vector<KernelArg>& args) = 0;

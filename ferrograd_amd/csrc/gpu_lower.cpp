@@ -109,7 +109,10 @@ const char* kernel_class_name(KernelClass k) {
 }
 
 KernelInfo analyze_kernel(const UOp& sink) {
-  FG_CHECK(sink.op() == Op::Sink && sink.srcs().size() == 1, "kernel must be Sink(one effect)");
+  FG_CHECK(sink.op() == Op::Sink && !sink.srcs().empty(), "kernel must be Sink(one effect)");
+  for (size_t i = 1; i < sink.srcs().size(); i++)
+    FG_CHECK(sink.src(i).op() == Op::ParamBuffer || sink.src(i).op() == Op::ParamScalar,
+             "kernel must be Sink(one effect, kernel parameters)");
   KernelInfo ki;
   UOp n = sink.src(0);
   while (n.op() == Op::End) {
@@ -133,6 +136,18 @@ KernelInfo analyze_kernel(const UOp& sink) {
     if (x.op() == Op::ParamBuffer || x.op() == Op::ParamScalar) ps[static_cast<int>(x.arg().a)] = x;
   for (auto& p : ps) ki.params.emplace_back(p.first, p.second);
   return ki;
+}
+
+UOp with_all_params(const UOp& kernel, const UOp& scheduled) {
+  std::map<int64_t, UOp> want;
+  for (auto& x : scheduled.toposort())
+    if (x.op() == Op::ParamBuffer || x.op() == Op::ParamScalar) want.emplace(x.arg().a, x);
+  for (auto& x : kernel.toposort())
+    if (x.op() == Op::ParamBuffer || x.op() == Op::ParamScalar) want.erase(x.arg().a);
+  if (want.empty()) return kernel;
+  std::vector<UOp> srcs = kernel.srcs();
+  for (auto& [slot, p] : want) srcs.push_back(p);
+  return UOp::make_new(Op::Sink, kernel.dtype(), srcs, kernel.arg());
 }
 
 // ── OPT: pass selection (src/optimize/mod.rs:85-112) ───────────────────────

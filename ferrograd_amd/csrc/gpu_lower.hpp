@@ -60,6 +60,14 @@ GpuPasses parse_gpu_passes(const char* raw);
 // OPT as read once per process.
 const GpuPasses& gpu_passes();
 
+// `kernel` (lowered from the scheduled kernel `scheduled`) with every kernel
+// parameter `scheduled` has: one that index simplification or a fold took out
+// of the body (a Shrink start times the zero stride of an extent-0 axis, a
+// load multiplied by 0) rides along as an extra source of the Sink, so the
+// rendered kernel still declares it and its launch arguments keep their
+// slots. (The reference renders only the parameters left in the body and
+// passes every argument, cpu.rs:338-357.)
+UOp with_all_params(const UOp& kernel, const UOp& scheduled);
 // Symbolic cleanup (when enabled) plus the GPU range retagging (size-1 reduce
 // ranges become the constant 0; output ranges become GLOBAL).
 UOp gpu_optimize(const UOp& rangeified);

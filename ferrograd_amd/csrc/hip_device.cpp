@@ -116,6 +116,9 @@ class HipDevice : public Device {
   }
 
   UOp optimize(const UOp& rangeified) override { return gpu_optimize(rangeified); }
+  UOp bind_params(const UOp& optimized, const UOp& scheduled) override {
+    return with_all_params(optimized, scheduled);
+  }
 
   RenderedKernel render(const UOp& optimized, const std::string& name) override {
     (void)name;  // symbols are content-named so code objects cache across runs

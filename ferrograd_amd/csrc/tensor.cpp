@@ -440,7 +440,7 @@ static std::shared_ptr<Program> execute_item(const ScheduleItem& item) {
     if (debug >= 3) std::fprintf(stderr, "━━━ rangeify [before] ━━━\n%s", item.sink.dump().c_str());
     UOp rangeified = rangeify(item.sink);
     if (debug >= 3) std::fprintf(stderr, "━━━ optimize [before] ━━━\n%s", rangeified.dump().c_str());
-    UOp optimized = backend.optimize(rangeified);
+    UOp optimized = backend.bind_params(backend.optimize(rangeified), item.sink);
     if (debug >= 3) std::fprintf(stderr, "━━━ codegen [before] ━━━\n%s", optimized.dump().c_str());
     assert_kernel_ready(optimized);
     program = backend.cached_program(optimized);

@@ -128,3 +128,39 @@ def test_ragged_shapes_on_hip_match_the_oracle(fg, cpu, hip, name):
         a64, b64 = a.astype(np.float64), (b.astype(np.float64) if b is not None else None)
         scale = np.asarray(tol(a64, b64)).reshape(-1)
         assert np.all(np.abs(got.astype(np.float64) - want) <= 1e-4 * scale + 1e-30)
+
+
+def narrowed_empty_sum(fg, dev):
+    """A narrow() of a tensor with an extent-0 axis, summed over that axis and
+    scaled: the narrow's start becomes a kernel parameter (schedule.rs:
+    217-239) that the index arithmetic then drops (it multiplies the zero
+    stride of the empty axis)."""
+    x = fg.Tensor.new(np.zeros((5, 0), F), [5, 0], dev)
+    y = fg.Tensor.new(np.arange(1, 5, dtype=F).reshape(4, 1), [4, 1], dev)
+    return x.narrow(0, 1, 4).sum([1]).mul(y)
+
+
+def test_a_parameter_the_body_drops_stays_in_the_signature(fg, cpu):
+    # The kernel is launched with every scheduled argument in slot order, so
+    # its HIP signature declares the dropped start too (an unused int).
+    from hipcompile import compile_sources
+
+    items = fg.debug_plan([narrowed_empty_sum(fg, cpu)], fuse=True, render_hip=True)["items"]
+    assert len(items) == 1
+    it = items[0]
+    assert {"i32": 1} in it["inputs"]
+    sig = next(l for l in it["source"].splitlines() if "__global__" in l)
+    assert sig.count("data") == len(it["inputs"]) + 1 and "int data2" in sig, sig
+    compile_sources({it["source"]: it["name"]}, limit_s=120)
+
+
+@pytest.mark.gpu
+def test_a_parameter_the_body_drops_on_hip(fg, hip):
+    # Against the closed form (a sum over the empty axis is 0.0, times y):
+    # the oracle, like the reference, keys its program cache by the lowered
+    # kernel, which lost the parameter, so a cached twin with one argument
+    # fewer can be handed this launch and fail its argument count.
+    print("narrowed empty sum", flush=True)
+    for _ in range(2):  # scheduled, then replayed
+        got = narrowed_empty_sum(fg, hip).to_vec()
+        assert np.array_equal(np.asarray(got, F), np.zeros(4, F))
