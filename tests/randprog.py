@@ -27,6 +27,9 @@ SHAPES = [(4, 6), (6, 4), (3, 4, 5), (8, 16), (16, 8), (2, 3, 4, 2), (32,), (5, 
 # Above the small-kernel limits (4096 outputs), so the row-reduce,
 # column-reduce, elementwise and GEMM kernel classes render too.
 LARGE_SHAPES = [(64, 96), (96, 64), (128, 48), (16, 24, 20), (256, 32), (32, 256), (6, 8, 10, 12), (5000,)]
+# Unit axes and extents off every lane, tile and workgroup multiple, on both
+# sides of the one-workgroup limits.
+ODD_SHAPES = [(1, 7), (7, 1), (1, 1), (3, 1, 5), (33, 17), (1, 4099), (4099, 1), (1031, 3), (3, 1031), (65, 65), (1,)]
 
 
 class Node:
@@ -49,14 +52,14 @@ def _scalar(fg, dev, c):
     return fg.Tensor.scalar(float(np.float32(c)), dev)
 
 
-def random_program(fg, dev, seed, depth=7, large=False, leaves=None):
+def random_program(fg, dev, seed, depth=7, large=False, leaves=None, odd=False):
     """Build a random program; returns the nodes to realise (the last one and
-    up to two earlier ones). `large` draws from LARGE_SHAPES; `leaves`, a
-    list, receives the program's input nodes."""
+    up to two earlier ones). `large` draws from LARGE_SHAPES, `odd` from
+    ODD_SHAPES; `leaves`, a list, receives the program's input nodes."""
     rng = np.random.default_rng(seed)
     _LEAVES.clear()
-    shapes = LARGE_SHAPES if large else SHAPES
-    widths = [3, 64, 96, 130] if large else [3, 5, 8]
+    shapes = ODD_SHAPES if odd else LARGE_SHAPES if large else SHAPES
+    widths = [1, 3, 33] if odd else [3, 64, 96, 130] if large else [3, 5, 8]
     pool = [leaf(fg, dev, rng, shapes[rng.integers(len(shapes))]) for _ in range(2)]
     for _ in range(depth):
         x = pool[rng.integers(len(pool))]

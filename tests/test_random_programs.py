@@ -167,8 +167,12 @@ def test_every_random_program_compiles_for_gfx950(fg, cpu):
     sources = {}
     programs = [(s, False) for s in SEEDS] + [(s, True) for s in LARGE_SEEDS + list(range(1000, 1140))]
     programs += [(s, False) for s in range(60)] + [(s, True) for s in range(2000, 2040)]
+    programs += [(s, "odd") for s in range(3000, 3040)]
     for seed, large in programs:
-        nodes = randprog.random_program(fg, cpu, seed, large=large)
+        if large == "odd":
+            nodes = randprog.random_program(fg, cpu, seed, odd=True)
+        else:
+            nodes = randprog.random_program(fg, cpu, seed, large=large)
         for it in fg.debug_plan([n.t for n in nodes], fuse=True, render_hip=True)["items"]:
             sources[it["source"]] = it["name"]
     timings = compile_sources(sources, limit_s=300)
@@ -237,3 +241,24 @@ def test_random_program_gradients_on_hip_match_the_oracle(fg, cpu, hip, seed, la
         leaf = float(np.abs(w).max())
         bound = 1e-4 * leaf + 1e-6 * top
         assert np.all(np.abs(g - w) <= bound), (seed, i, float(np.max(np.abs(g - w))), leaf, top)
+
+
+ODD_SEEDS = list(range(3000, 3040))
+
+
+@pytest.mark.parametrize("seed", ODD_SEEDS)
+def test_odd_shaped_random_program_on_the_oracle(fg, cpu, seed):
+    nodes = randprog.random_program(fg, cpu, seed, odd=True)
+    fg.debug_plan([n.t for n in nodes], fuse=True, render_hip=True)
+    assert randprog.check(nodes, fg) <= 1.0
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("seed", ODD_SEEDS)
+def test_odd_shaped_random_program_on_hip(fg, hip, seed):
+    # Unit axes and ragged extents: every class's edge handling (clamped
+    # loads, partial tiles, partial lanes), twice (scheduled, then replayed).
+    print(f"odd-shaped random program {seed}", flush=True)
+    for _ in range(2):
+        nodes = randprog.random_program(fg, hip, seed, odd=True)
+        assert randprog.check(nodes, fg) <= 1.0
