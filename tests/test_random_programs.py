@@ -213,7 +213,10 @@ def _program_gradients(fg, dev, seed, large):
     import numpy as np
 
     leaves = []
-    nodes = randprog.random_program(fg, dev, seed, large=large, leaves=leaves)
+    if large == "odd":
+        nodes = randprog.random_program(fg, dev, seed, odd=True, leaves=leaves)
+    else:
+        nodes = randprog.random_program(fg, dev, seed, large=large, leaves=leaves)
     last = nodes[-1].t
     loss = last.sum(list(range(len(last.shape))))
     grads = loss.gradient([n.t for n in leaves])
@@ -222,7 +225,8 @@ def _program_gradients(fg, dev, seed, large):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("seed,large", [(s, False) for s in range(60)] + [(s, True) for s in range(2000, 2040)])
+@pytest.mark.parametrize("seed,large", [(s, False) for s in range(60)] + [(s, True) for s in range(2000, 2040)] +
+                         [(s, "odd") for s in range(3000, 3020)])
 def test_random_program_gradients_on_hip_match_the_oracle(fg, cpu, hip, seed, large):
     # The backward graphs (expand-sums, relu and max masks, matmul
     # transposes, log_softmax's) of the random programs: HIP against the
