@@ -221,10 +221,11 @@ int fg_tensor_realize_many(fg_tensor** ts, int n) {
 
 int fg_tensor_read(fg_tensor* t, void* dst, size_t nbytes) {
   return guard([&] {
-    auto bytes = t->t.to_bytes();
-    FG_CHECK(bytes.size() == nbytes,
-             "fg_tensor_read: expected " + std::to_string(bytes.size()) + " bytes, got " + std::to_string(nbytes));
-    std::memcpy(dst, bytes.data(), nbytes);
+    fg::Buffer b = t->t.realized_buffer();
+    FG_CHECK(b->nbytes() == nbytes,
+             "fg_tensor_read: expected " + std::to_string(b->nbytes()) + " bytes, got " + std::to_string(nbytes));
+    FG_CHECK(dst || nbytes == 0, "fg_tensor_read: null destination");
+    fg::get_device(b->device).copy_to_host_into(b, dst, nbytes);
   });
 }
 

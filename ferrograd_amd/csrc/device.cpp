@@ -3,8 +3,16 @@
 
 #include <atomic>
 #include <cstdlib>
+#include <cstring>
 
 namespace fg {
+
+void Device::copy_to_host_into(const Buffer& b, void* dst, size_t nbytes) {
+  std::vector<uint8_t> v = copy_to_host(b);
+  FG_CHECK(v.size() == nbytes, "copy_to_host: expected " + std::to_string(v.size()) + " bytes, got " +
+                                   std::to_string(nbytes));
+  if (nbytes) std::memcpy(dst, v.data(), nbytes);
+}
 
 size_t next_buffer_id() {  // device.rs:230-234
   static std::atomic<size_t> next{0};

@@ -119,6 +119,9 @@ class Device {
   virtual void release(BufferInner& b) = 0;
   virtual void copy_from_host(const Buffer& b, const void* src, size_t nbytes) = 0;
   virtual std::vector<uint8_t> copy_to_host(const Buffer& b) = 0;
+  // copy_to_host into the caller's `nbytes` (which must be the buffer's
+  // size), with no intermediate vector.
+  virtual void copy_to_host_into(const Buffer& b, void* dst, size_t nbytes);
   // A read-back that need not finish before the caller queues more work:
   // read_async takes the buffer's bytes (as copy_to_host would) into `slot`
   // once the device has run what is already queued; read_wait returns them.

@@ -99,6 +99,18 @@ class HipDevice : public Device {
     return out;
   }
 
+  void copy_to_host_into(const Buffer& b, void* dst, size_t nbytes) override {
+    FG_CHECK(b->device == DeviceId::Hip, "HIP backend received non-HIP buffer " + std::to_string(b->id));
+    FG_CHECK(nbytes == b->nbytes(), "copy_to_host: expected " + std::to_string(b->nbytes()) + " bytes, got " +
+                                        std::to_string(nbytes));
+    if (!b->realized && b->zero_init) {  // allocated zeros, never materialised
+      if (nbytes) std::memset(dst, 0, nbytes);
+      return;
+    }
+    FG_CHECK(b->realized, "copy_to_host called on unrealized or non-HIP buffer");
+    check(fg_hip_copy_d2h(ctx(), dst, b->storage, nbytes), "fg_hip_copy_d2h");
+  }
+
   void read_async(const Buffer& b, int slot) override {
     FG_CHECK(b->device == DeviceId::Hip, "HIP backend received non-HIP buffer " + std::to_string(b->id));
     FG_CHECK(slot >= 0 && slot < FG_READ_SLOTS, "read_async: slot " + std::to_string(slot) + " out of range");

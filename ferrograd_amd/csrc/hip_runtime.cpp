@@ -13,6 +13,9 @@
 
 #include <algorithm>
 #include <chrono>
+#include <condition_variable>
+#include <functional>
+#include <thread>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
@@ -199,6 +202,12 @@ struct fg_ctx {
   bool async_pending[FG_READ_SLOTS] = {};
   // Direct AQL dispatch (fg_hip_aql_begin / fg_hip_aql_end); null until used.
   AqlQueue* aql = nullptr;
+  // Large host<->device copies: two pinned chunks, each with the event of
+  // its last DMA, so the host copies one chunk while the other is in flight
+  // (allocated on the first large copy).
+  char* chunk[2] = {nullptr, nullptr};
+  hipEvent_t chunk_event[2] = {};
+  bool chunk_pending[2] = {false, false};
   // Launch profiling.
   bool profiling = false;
   std::vector<hipEvent_t> event_pool;
@@ -235,6 +244,91 @@ constexpr size_t kReadbackBytes = 1 << 20;
 constexpr size_t kMaxCachedBytes = size_t(96) << 30;
 
 size_t round_up(size_t n) { return (n + kAllocGranule - 1) / kAllocGranule * kAllocGranule; }
+
+// Copies of at least kChunkedCopy bytes go through the pinned chunks: into
+// or out of pinned memory a DMA runs at about 57 GB/s each way on MI355X,
+// from or to pageable memory at 15-25 GB/s, and several host threads move
+// 70-90 GB/s between pageable and pinned memory where one moves 20.
+constexpr size_t kChunkedCopy = size_t(4) << 20;
+constexpr size_t kChunkBytes = size_t(16) << 20;
+
+// A few host threads for those memcpys (created on first use; the caller
+// takes a share too).
+class CopyPool {
+ public:
+  static CopyPool& get() {
+    static CopyPool* p = new CopyPool();
+    return *p;
+  }
+  // dst[0, n) = src[0, n), split over the pool.
+  void copy(void* dst, const void* src, size_t n) {
+    const size_t parts = std::max<size_t>(1, std::min<size_t>(workers_.size() + 1, n >> 20));
+    if (parts == 1) {
+      std::memcpy(dst, src, n);
+      return;
+    }
+    const size_t piece = ((n + parts - 1) / parts + 63) / 64 * 64;  // parts * piece >= n
+    auto part = [=](size_t i) {
+      const size_t off = std::min(n, i * piece), end = std::min(n, off + piece);
+      if (end > off) std::memcpy(static_cast<char*>(dst) + off, static_cast<const char*>(src) + off, end - off);
+    };
+    {
+      std::lock_guard<std::mutex> lk(m_);
+      job_ = part;
+      next_ = 1;
+      total_ = parts;
+      left_ = parts - 1;
+      gen_++;
+    }
+    cv_.notify_all();
+    part(0);
+    for (;;) {  // the caller helps with what the workers have not started
+      size_t i;
+      {
+        std::lock_guard<std::mutex> lk(m_);
+        if (next_ >= total_) break;
+        i = next_++;
+      }
+      part(i);
+      std::lock_guard<std::mutex> lk(m_);
+      left_--;
+    }
+    std::unique_lock<std::mutex> lk(m_);
+    done_.wait(lk, [&] { return left_ == 0; });
+  }
+
+ private:
+  CopyPool() {
+    const unsigned hw = std::thread::hardware_concurrency();
+    const unsigned n = std::min(7u, hw > 2 ? hw / 2 - 1 : 0u);
+    for (unsigned i = 0; i < n; i++)
+      workers_.emplace_back([this] {
+        uint64_t seen = 0;
+        std::unique_lock<std::mutex> lk(m_);
+        for (;;) {
+          cv_.wait(lk, [&] { return gen_ != seen && next_ < total_; });
+          seen = gen_;
+          while (next_ < total_) {
+            const size_t i = next_++;
+            auto job = job_;
+            lk.unlock();
+            job(i);
+            lk.lock();
+            if (--left_ == 0) done_.notify_all();
+          }
+        }
+      });
+    for (auto& w : workers_) w.detach();
+  }
+  std::vector<std::thread> workers_;
+  std::mutex m_;
+  std::condition_variable cv_, done_;
+  std::function<void(size_t)> job_;
+  size_t next_ = 0, total_ = 0, left_ = 0;
+  uint64_t gen_ = 0;
+};
+
+int ensure_chunks(fg_ctx* c);
 // Before a HIP-stream operation while the context's AQL queue is active: the
 // queue's packets complete first (defined with the queue below).
 int aql_interlude(fg_ctx* c);
@@ -274,6 +368,17 @@ int fg_hip_init(int ordinal, fg_ctx** out) {
   return FG_OK;
 }
 
+namespace {
+int ensure_chunks(fg_ctx* c) {
+  for (int b = 0; b < 2; b++) {
+    if (c->chunk[b]) continue;
+    HIP_TRY(hipHostMalloc(reinterpret_cast<void**>(&c->chunk[b]), kChunkBytes, hipHostMallocDefault));
+    HIP_TRY(hipEventCreateWithFlags(&c->chunk_event[b], hipEventDisableTiming));
+  }
+  return FG_OK;
+}
+}  // namespace
+
 int fg_hip_destroy(fg_ctx* c) {
   if (!c) return FG_OK;
   // Teardown: errors here have nowhere to go, so they are not checked.
@@ -289,6 +394,10 @@ int fg_hip_destroy(fg_ctx* c) {
   (void)hipHostFree(c->staging);
   (void)hipHostFree(c->readback);
   (void)hipHostFree(c->async_read);
+  for (int b = 0; b < 2; b++) {
+    if (c->chunk[b]) (void)hipHostFree(c->chunk[b]);
+    if (c->chunk_event[b]) (void)hipEventDestroy(c->chunk_event[b]);
+  }
   for (auto& ev : c->async_events) (void)hipEventDestroy(ev);
   (void)hipStreamDestroy(c->stream);
   delete c;
@@ -386,6 +495,20 @@ int fg_hip_copy_h2d(fg_ctx* c, void* dst, const void* src, size_t n) {
     c->staging_event_pending = true;
     return FG_OK;
   }
+  if (n >= kChunkedCopy) {
+    // Pinned chunks in turn: the host fills one while the other's DMA runs.
+    if (int rc = ensure_chunks(c)) return rc;
+    for (size_t off = 0, i = 0; off < n; off += kChunkBytes, i++) {
+      const int b = static_cast<int>(i % 2);
+      const size_t len = std::min(kChunkBytes, n - off);
+      if (c->chunk_pending[b]) HIP_TRY(hipEventSynchronize(c->chunk_event[b]));
+      CopyPool::get().copy(c->chunk[b], static_cast<const char*>(src) + off, len);
+      HIP_TRY(hipMemcpyAsync(static_cast<char*>(dst) + off, c->chunk[b], len, hipMemcpyHostToDevice, c->stream));
+      HIP_TRY(hipEventRecord(c->chunk_event[b], c->stream));
+      c->chunk_pending[b] = true;
+    }
+    return FG_OK;
+  }
   HIP_TRY(hipMemcpyAsync(dst, src, n, hipMemcpyHostToDevice, c->stream));
   HIP_TRY(hipStreamSynchronize(c->stream));
   return FG_OK;
@@ -400,6 +523,31 @@ int fg_hip_copy_d2h(fg_ctx* c, void* dst, const void* src, size_t n) {
     HIP_TRY(hipStreamSynchronize(c->stream));
     std::memcpy(dst, c->readback, n);
     return FG_OK;
+  }
+  if (n >= kChunkedCopy) {
+    // The DMA of chunk i+1 runs while the host copies chunk i out.
+    if (int rc = ensure_chunks(c)) return rc;
+    const size_t nch = (n + kChunkBytes - 1) / kChunkBytes;
+    auto drain = [&](size_t i) -> int {
+      const int b = static_cast<int>(i % 2);
+      HIP_TRY(hipEventSynchronize(c->chunk_event[b]));
+      c->chunk_pending[b] = false;
+      const size_t off = i * kChunkBytes;
+      CopyPool::get().copy(static_cast<char*>(dst) + off, c->chunk[b], std::min(kChunkBytes, n - off));
+      return FG_OK;
+    };
+    for (size_t i = 0; i < nch; i++) {
+      const int b = static_cast<int>(i % 2);
+      if (c->chunk_pending[b]) HIP_TRY(hipEventSynchronize(c->chunk_event[b]));  // an upload's last use
+      const size_t off = i * kChunkBytes;
+      HIP_TRY(hipMemcpyAsync(c->chunk[b], static_cast<const char*>(src) + off, std::min(kChunkBytes, n - off),
+                             hipMemcpyDeviceToHost, c->stream));
+      HIP_TRY(hipEventRecord(c->chunk_event[b], c->stream));
+      c->chunk_pending[b] = true;
+      if (i > 0)
+        if (int rc = drain(i - 1)) return rc;
+    }
+    return drain(nch - 1);
   }
   HIP_TRY(hipMemcpyAsync(dst, src, n, hipMemcpyDeviceToHost, c->stream));
   HIP_TRY(hipStreamSynchronize(c->stream));
@@ -489,6 +637,7 @@ int fg_hip_copy_d2d(fg_ctx* c, void* dst, const void* src, size_t n) {
   return FG_OK;
 }
 
+extern "C++" {
 namespace {
 // hiprtc compile of `source` into `code`.
 int rtc_compile(const char* source, const char* func, std::vector<char>* code) {
@@ -523,6 +672,7 @@ std::string cache_path(const char* source) {
   return cache_dir() + "/" + hex + ".co";
 }
 }  // namespace
+}  // extern "C++"
 
 int fg_hip_compile(fg_ctx* c, const char* source, const char* func, int num_args, fg_prog** out) {
   if (!source || !func || !out) return set_err(FG_ERR_INVALID, "fg_hip_compile: null argument");

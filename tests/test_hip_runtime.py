@@ -124,16 +124,31 @@ def test_alloc_is_zeroed(ctx):  # device.rs:366-377, cpu.rs:277-280
     assert not _download(ctx, q, 1024).any()
 
 
-@pytest.mark.parametrize("nbytes", [4, (1 << 20) - 4, 1 << 20, (1 << 20) + 4, 3 << 20])
+@pytest.mark.parametrize("nbytes", [4, (1 << 20) - 4, 1 << 20, (1 << 20) + 4, 3 << 20, (4 << 20) - 4, 4 << 20,
+                                    (5 << 20) + 4, (16 << 20) + 4, (40 << 20) + 12])
 def test_copies_round_trip_on_both_sides_of_the_staging_limits(ctx, nbytes):
     # Host->device copies up to 64 KiB go through a pinned staging ring and
-    # device->host reads up to 1 MiB land in a pinned buffer; larger ones go
-    # direct. Every size must round-trip exactly.
+    # device->host reads up to 1 MiB land in a pinned buffer; from 4 MiB both
+    # go through two pinned 16 MiB chunks in turn (partial last chunk
+    # included); the sizes between go direct. Every size must round-trip
+    # exactly.
     n = nbytes // 4
     a = np.random.default_rng(nbytes).standard_normal(n).astype(np.float32)
     p = _upload(ctx, a)
     assert np.array_equal(_download(ctx, p, n), a)
     ctx.free(p)
+
+
+def test_chunked_copies_back_to_back(ctx):
+    # Three uploads through the pinned chunks queued without a wait between
+    # them (each refills a chunk only once its previous DMA has finished),
+    # then the reads, each against its source.
+    sizes = [(24 << 20) + 8, (5 << 20) + 4, 33 << 20]
+    arrays = [np.random.default_rng(i).standard_normal(n // 4).astype(np.float32) for i, n in enumerate(sizes)]
+    ptrs = [_upload(ctx, a) for a in arrays]
+    for p, a in zip(ptrs, arrays):
+        assert np.array_equal(_download(ctx, p, a.size), a)
+        ctx.free(p)
 
 
 def test_bad_source_is_compile_error(ctx):  # cpu.rs:484-497, 639-649
