@@ -105,12 +105,13 @@ sys.exit(0 if max(errs.values()) <= 1.0 else 1)
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("tile", ["256,160,16,4,1,3,3", "160,256,32,1,4,2", "256,160,16,4,1,0,3", "128,128,32,2,2,0",
-                                  "192,96,32,2,1,2", "96,192,32,1,2,0"])
+                                  "192,96,32,2,1,2", "96,192,32,1,2,0", "256,256,8,2,2,1", "64,64,24,2,2,1"])
 def test_forced_160_wide_tiles_against_float64(tile):
     # Tiles the model rarely picks (16-wide k-tiles with three LDS stages; a
     # 160-row tile on every orientation; stream-K, split count 0, with those
     # stages and with two workgroups per CU on ragged 128x128 tiles; waves of
-    # three 32-wide tiles, [k][row] stages as a chunk of two and one of one),
+    # three 32-wide tiles, [k][row] stages as a chunk of two and one of one;
+    # k-tiles of one and of three 8-k groups),
     # fixed with the FG_GEMM_TILE tuning override in a process of their own,
     # as it holds for every GEMM.
     import os
