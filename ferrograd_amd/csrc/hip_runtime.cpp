@@ -260,8 +260,10 @@ class CopyPool {
     static CopyPool* p = new CopyPool();
     return *p;
   }
-  // dst[0, n) = src[0, n), split over the pool.
+  // dst[0, n) = src[0, n), split over the pool. Calls from several threads
+  // (contexts used on different threads) take turns: the pool runs one job.
   void copy(void* dst, const void* src, size_t n) {
+    std::lock_guard<std::mutex> one(call_m_);
     const size_t parts = std::max<size_t>(1, std::min<size_t>(workers_.size() + 1, n >> 20));
     if (parts == 1) {
       std::memcpy(dst, src, n);
@@ -321,7 +323,7 @@ class CopyPool {
     for (auto& w : workers_) w.detach();
   }
   std::vector<std::thread> workers_;
-  std::mutex m_;
+  std::mutex call_m_, m_;
   std::condition_variable cv_, done_;
   std::function<void(size_t)> job_;
   size_t next_ = 0, total_ = 0, left_ = 0;

@@ -151,6 +151,36 @@ def test_chunked_copies_back_to_back(ctx):
         ctx.free(p)
 
 
+def test_chunked_copies_from_two_threads(ctx):
+    # Two contexts used on two threads at once: both copy through the host
+    # copy pool (one job at a time) and get their own bytes back.
+    import threading
+
+    from ferrograd_amd.hip import Context
+
+    ctx2 = Context(0)
+    arrays = [np.random.default_rng(10 + i).standard_normal((12 << 20) // 4 + i).astype(np.float32) for i in range(2)]
+    got, errors = [None, None], []
+
+    def run(i, c):
+        try:
+            for _ in range(3):
+                p = _upload(c, arrays[i])
+                got[i] = _download(c, p, arrays[i].size)
+                c.free(p)
+        except Exception as e:  # reported below, on the test's thread
+            errors.append(e)
+
+    threads = [threading.Thread(target=run, args=(i, c)) for i, c in enumerate((ctx, ctx2))]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join()
+    assert not errors, errors
+    for i in range(2):
+        assert np.array_equal(got[i], arrays[i])
+
+
 def test_bad_source_is_compile_error(ctx):  # cpu.rs:484-497, 639-649
     from ferrograd_amd.hip import FG_ERR_COMPILE, HipError
 
