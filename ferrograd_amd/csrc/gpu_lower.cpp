@@ -2038,15 +2038,21 @@ RenderedKernel render_gemm(const KernelInfo& ki, const GemmMatch& g, const std::
   s << R"(  // Operand stages, double-buffered, rows padded by 4 floats; then per-wave
   // 32 x WN staging tiles for the epilogue.
   constexpr int WM = BM / (NT / 64 / WGN), WN = BN / WGN;
+  // A [row][k] stage of 16-wide k-tiles is unpadded, its 16-byte chunks
+  // XOR-swizzled by row: chunk c of row r sits at c ^ ((r >> 1) & 3). Eight
+  // lanes of a stage write (two rows) and of a fragment read (eight rows, one
+  // chunk) then fall on distinct banks; rows padded to 20 floats put two rows'
+  // writes on the same banks.
+#define FG_SWZ(r, c) (BK == 16 ? ((c) ^ ((((r) >> 1) & 3) << 2)) : (c))
 #if A_KM
   constexpr int SA_R = BK, SA_C = BM + 4;
 #else
-  constexpr int SA_R = BM, SA_C = BK + 4;
+  constexpr int SA_R = BM, SA_C = BK == 16 ? BK : BK + 4;
 #endif
 #if B_KM
   constexpr int SB_R = BK, SB_C = BN + 4;
 #else
-  constexpr int SB_R = BN, SB_C = BK + 4;
+  constexpr int SB_R = BN, SB_C = BK == 16 ? BK : BK + 4;
 #endif
   constexpr int SA = 2 * SA_R * SA_C, SB = 2 * SB_R * SB_C, EPS = WN + 4, SE = (NT / 64) * 32 * EPS;
   __shared__ __attribute__((aligned(16))) float smem[(SA + SB) > SE ? (SA + SB) : SE];
@@ -2220,13 +2226,13 @@ RenderedKernel render_gemm(const KernelInfo& ki, const GemmMatch& g, const std::
     }
     const std::string sguard = guard ? "if (idx < " + std::to_string(st.groups) + ") " : "";
     if (st.md == 0) {
-      l << "      " << sguard << "*(fg_f4*)(&" << SX << "[buf][r][kk]) = fg_f4{v[0], v[1], v[2], v[3]};\n";
+      l << "      " << sguard << "*(fg_f4*)(&" << SX << "[buf][r][FG_SWZ(r, kk)]) = fg_f4{v[0], v[1], v[2], v[3]};\n";
     } else if (st.md == 1) {
       l << "      " << sguard << "*(fg_f4*)(&" << SX << "[buf][kk][r]) = fg_f4{v[0], v[1], v[2], v[3]};\n";
     } else if (st.km) {
       l << "      " << sguard << SX << "[buf][kk][r] = v[0];\n";
     } else {
-      l << "      " << sguard << SX << "[buf][r][kk] = v[0];\n";
+      l << "      " << sguard << SX << "[buf][r][FG_SWZ(r, kk)] = v[0];\n";
     }
     l << "    }\n  };\n";
     return l.str();
@@ -2277,7 +2283,7 @@ RenderedKernel render_gemm(const KernelInfo& ki, const GemmMatch& g, const std::
 )" << km_frag("As", "wm", "fra", TM) << R"(#else
     #pragma unroll
     for (int i = 0; i < TM; i++) {
-      const fg_f4 v = *(const fg_f4*)&As[buf][wm + 32 * i + r32][8 * g + 4 * h];
+      const fg_f4 v = *(const fg_f4*)&As[buf][wm + 32 * i + r32][FG_SWZ(wm + 32 * i + r32, 8 * g + 4 * h)];
       fra[i][0] = v.x; fra[i][1] = v.y; fra[i][2] = v.z; fra[i][3] = v.w;
     }
 #endif
@@ -2285,7 +2291,7 @@ RenderedKernel render_gemm(const KernelInfo& ki, const GemmMatch& g, const std::
 )" << km_frag("Bs", "wn", "frb", TN) << R"(#else
     #pragma unroll
     for (int j = 0; j < TN; j++) {
-      const fg_f4 v = *(const fg_f4*)&Bs[buf][wn + 32 * j + r32][8 * g + 4 * h];
+      const fg_f4 v = *(const fg_f4*)&Bs[buf][wn + 32 * j + r32][FG_SWZ(wn + 32 * j + r32, 8 * g + 4 * h)];
       frb[j][0] = v.x; frb[j][1] = v.y; frb[j][2] = v.z; frb[j][3] = v.w;
     }
 #endif
