@@ -331,6 +331,7 @@ class CopyPool {
 };
 
 int ensure_chunks(fg_ctx* c);
+int release_chunks(fg_ctx* c);
 // Before a HIP-stream operation while the context's AQL queue is active: the
 // queue's packets complete first (defined with the queue below).
 int aql_interlude(fg_ctx* c);
@@ -376,6 +377,24 @@ int ensure_chunks(fg_ctx* c) {
     if (c->chunk[b]) continue;
     HIP_TRY(hipHostMalloc(reinterpret_cast<void**>(&c->chunk[b]), kChunkBytes, hipHostMallocDefault));
     HIP_TRY(hipEventCreateWithFlags(&c->chunk_event[b], hipEventDisableTiming));
+  }
+  return FG_OK;
+}
+
+// The chunks are given back at the end of each copy that used them. Held in
+// the process, they made its host code slower afterwards: C1's realise path
+// (graph key, live-tensor rewrite) ran 2-4x longer after C2's copies, 2.9
+// against 5.6 TB/s per realise, and re-allocating them costs the host-buffer
+// C2 leg 52.7 -> 49.0 GB/s.
+int release_chunks(fg_ctx* c) {
+  for (int b = 0; b < 2; b++) {
+    if (!c->chunk[b]) continue;
+    if (c->chunk_pending[b]) HIP_TRY(hipEventSynchronize(c->chunk_event[b]));
+    HIP_TRY(hipHostFree(c->chunk[b]));
+    HIP_TRY(hipEventDestroy(c->chunk_event[b]));
+    c->chunk[b] = nullptr;
+    c->chunk_event[b] = nullptr;
+    c->chunk_pending[b] = false;
   }
   return FG_OK;
 }
@@ -509,7 +528,7 @@ int fg_hip_copy_h2d(fg_ctx* c, void* dst, const void* src, size_t n) {
       HIP_TRY(hipEventRecord(c->chunk_event[b], c->stream));
       c->chunk_pending[b] = true;
     }
-    return FG_OK;
+    return release_chunks(c);
   }
   HIP_TRY(hipMemcpyAsync(dst, src, n, hipMemcpyHostToDevice, c->stream));
   HIP_TRY(hipStreamSynchronize(c->stream));
@@ -540,7 +559,6 @@ int fg_hip_copy_d2h(fg_ctx* c, void* dst, const void* src, size_t n) {
     };
     for (size_t i = 0; i < nch; i++) {
       const int b = static_cast<int>(i % 2);
-      if (c->chunk_pending[b]) HIP_TRY(hipEventSynchronize(c->chunk_event[b]));  // an upload's last use
       const size_t off = i * kChunkBytes;
       HIP_TRY(hipMemcpyAsync(c->chunk[b], static_cast<const char*>(src) + off, std::min(kChunkBytes, n - off),
                              hipMemcpyDeviceToHost, c->stream));
@@ -549,7 +567,8 @@ int fg_hip_copy_d2h(fg_ctx* c, void* dst, const void* src, size_t n) {
       if (i > 0)
         if (int rc = drain(i - 1)) return rc;
     }
-    return drain(nch - 1);
+    if (int rc = drain(nch - 1)) return rc;
+    return release_chunks(c);
   }
   HIP_TRY(hipMemcpyAsync(dst, src, n, hipMemcpyDeviceToHost, c->stream));
   HIP_TRY(hipStreamSynchronize(c->stream));
