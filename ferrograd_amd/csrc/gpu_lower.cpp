@@ -2039,11 +2039,14 @@ RenderedKernel render_gemm(const KernelInfo& ki, const GemmMatch& g, const std::
   // 32 x WN staging tiles for the epilogue.
   constexpr int WM = BM / (NT / 64 / WGN), WN = BN / WGN;
   // A [row][k] stage of 16-wide k-tiles is unpadded, its 16-byte chunks
-  // XOR-swizzled by row: chunk c of row r sits at c ^ ((r >> 1) & 3). Eight
-  // lanes of a stage write (two rows) and of a fragment read (eight rows, one
-  // chunk) then fall on distinct banks; rows padded to 20 floats put two rows'
-  // writes on the same banks.
-#define FG_SWZ(r, c) (BK == 16 ? ((c) ^ ((((r) >> 1) & 3) << 2)) : (c))
+  // XOR-swizzled by row: chunk c of row r sits at c ^ ((r >> 2) & 3). The 16
+  // lanes a fragment read serves at once (16 rows, one chunk, over 64 banks)
+  // and the 8 lanes of a stage write (two rows, over 32) then fall on distinct
+  // banks: PMC SQ_LDS_BANK_CONFLICT 0 for C5's K = 784 forward, against
+  // 6.5e6 cycles per dispatch with rows padded to 20 floats (which put two
+  // rows' writes on the same banks) and with c ^ ((r >> 1) & 3) (which put
+  // rows r and r + 8 of a read on the same banks).
+#define FG_SWZ(r, c) (BK == 16 ? ((c) ^ ((((r) >> 2) & 3) << 2)) : (c))
 #if A_KM
   constexpr int SA_R = BK, SA_C = BM + 4;
 #else
