@@ -383,9 +383,9 @@ int ensure_chunks(fg_ctx* c) {
 
 // The chunks are given back at the end of each copy that used them. Held in
 // the process, they made its host code slower afterwards: C1's realise path
-// (graph key, live-tensor rewrite) ran 2-4x longer after C2's copies, 2.9
-// against 5.6 TB/s per realise, and re-allocating them costs the host-buffer
-// C2 leg 52.7 -> 49.0 GB/s.
+// (graph key, live-tensor rewrite) ran 2-4x longer after C2's copies in most
+// runs, 2.9-4.2 against 5.5-5.7 TB/s per realise, and re-allocating them
+// costs the host-buffer C2 leg 52.7 -> 49.0 GB/s.
 int release_chunks(fg_ctx* c) {
   for (int b = 0; b < 2; b++) {
     if (!c->chunk[b]) continue;
