@@ -104,7 +104,9 @@ int fg_hip_read_slot(fg_ctx* ctx, int slot, void** device_ptr);
 int fg_hip_read_queued(fg_ctx* ctx, int slot, size_t nbytes);
 
 /* Compile HIP source for gfx950 with hiprtc and load kernel `func`. The code
- * object is cached on disk keyed by a hash of source, options and target. */
+ * object is cached on disk keyed by a hash of source, options and target, and
+ * a context keeps the modules it loaded (the 1024 most recent): the same
+ * source compiled again on it reuses its loaded module. */
 int fg_hip_compile(fg_ctx* ctx, const char* source, const char* func, int num_args, fg_prog** out);
 int fg_hip_program_free(fg_prog* prog);
 int fg_hip_program_num_args(const fg_prog* prog);
