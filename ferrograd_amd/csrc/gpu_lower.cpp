@@ -2109,9 +2109,10 @@ RenderedKernel render_gemm(const KernelInfo& ki, const GemmMatch& g, const std::
     // start in the scalar offset, so the k loop computes no addresses and
     // holds one register per load instead of a 64-bit address. Each load must
     // read a 4-byte element of a buffer under 2 GiB at an affine index whose
-    // terms are all non-negative (the per-lane part is then a valid offset on
-    // its own), and k must need no bounds check (the k-tile's start is not
-    // clamped). Measured on C5's kernels alone (same box, same bits): the
+    // terms are all ranges or constants with non-negative coefficients (the
+    // per-lane part is then a valid offset on its own; a kernel scalar, such
+    // as a narrow() start, could be negative for all the renderer knows), and
+    // k must need no bounds check (the k-tile's start is not clamped). Measured on C5's kernels alone (same box, same bits): the
     // 8192x4096, K 4096 products 1.4-2.0% faster (forward with the relu of its
     // input, dH with the relu mask, dW with the SGD update), dW1's stream-K
     // pass 1.7%, the K 784 forward within 0.6%.
@@ -2124,7 +2125,7 @@ RenderedKernel render_gemm(const KernelInfo& ki, const GemmMatch& g, const std::
       Affine a = affine_of(ix.src(1));
       if (!a.ok || a.c0 < 0) bufl = false;
       for (auto& t : a.terms)
-        if (t.second < 0) bufl = false;
+        if (t.second < 0 || t.first.op() != Op::Range) bufl = false;
     }
     std::map<const UOpInner*, std::string> rsrc;
     std::ostringstream decl;

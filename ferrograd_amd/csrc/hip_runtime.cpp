@@ -212,7 +212,7 @@ struct fg_ctx {
   AqlQueue* aql = nullptr;
   // Large host<->device copies: two pinned chunks, each with the event of
   // its last DMA, so the host copies one chunk while the other is in flight
-  // (allocated on the first large copy).
+  // (allocated for each large copy and given back at its end).
   char* chunk[2] = {nullptr, nullptr};
   hipEvent_t chunk_event[2] = {};
   bool chunk_pending[2] = {false, false};
@@ -258,11 +258,12 @@ size_t round_up(size_t n) { return (n + kAllocGranule - 1) / kAllocGranule * kAl
 // from or to pageable memory at 15-25 GB/s, and several host threads move
 // 70-90 GB/s between pageable and pinned memory where one moves 20.
 constexpr size_t kChunkedCopy = size_t(4) << 20;
+constexpr size_t kChunkBytes = size_t(16) << 20;
+
 // Modules a context keeps loaded for sources compiled again. A native train
 // loop's first replay compiled its batch kernels again in every call: 1.9 ms
 // per call, against 0.4 ms for three steps run in full.
 constexpr size_t kLoadedModules = 1024;
-constexpr size_t kChunkBytes = size_t(16) << 20;
 
 // A few host threads for those memcpys (created on first use; the caller
 // takes a share too).

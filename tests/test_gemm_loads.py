@@ -2,13 +2,14 @@
 
 The stages load through raw buffer loads: each lane's 32-bit byte offset is
 the same in every k-tile and the k-tile's start goes in the scalar offset.
-That needs every term of the operand's index to be non-negative and the
-buffer to stay under 2 GiB; otherwise the stage keeps 64-bit global loads.
-These cases cover an operand read through narrow() views (the starts are
-kernel scalars inside the lane offset, and a start that is not a multiple of
-4 turns the 16-byte loads into one-element loads), the same view read
-transposed (the [k][row] stage), and an operand of exactly 2 GiB (the
-fallback). Each product is checked per element within 1e-4·Σ|terms| of
+That needs every term of the operand's index to be a range with a
+non-negative coefficient and the buffer to stay under 2 GiB; otherwise the
+stage keeps 64-bit global loads. These cases cover an operand read through
+narrow() views (its starts are kernel scalars, whose sign the renderer does
+not know, so it keeps global loads, one element at a time for a start that
+is not a multiple of 4) beside a contiguous one that takes buffer loads, the
+same view read transposed (the [k][row] stage), and an operand of exactly
+2 GiB. Each product is checked per element within 1e-4·Σ|terms| of
 float64 (matmul as tensor.rs:771-777)."""
 from __future__ import annotations
 
@@ -29,13 +30,13 @@ def _narrowed(fg, dev, X, W):
     return x, w
 
 
-def test_narrowed_operand_renders_scalar_buffer_loads(fg, cpu):
+def test_narrowed_operand_keeps_global_loads(fg, cpu):
     X = np.ones((3000, 1100), np.float32)
     W = np.ones((768, 1024), np.float32)
     x, w = _narrowed(fg, cpu, X, W)
     (src,) = _sources(fg, x.matmul(w.permute([1, 0])))
-    # The row and column starts are kernel scalars inside the lane offset.
-    assert "__builtin_amdgcn_raw_buffer_load_b32(fg_rs_data1" in src
+    # The row and column starts are kernel scalars: data1 keeps global loads.
+    assert "fg_rs_data1" not in src and "data1[" in src
     assert "__builtin_amdgcn_raw_buffer_load_b128(fg_rs_" in src  # the contiguous operand
 
 
