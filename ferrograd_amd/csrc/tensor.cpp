@@ -961,6 +961,57 @@ std::unique_ptr<CapturedStep> capture_step(const std::vector<ReplayRecord>& prev
   return cap;
 }
 
+// The device's replay state of the last captured step, kept across native
+// loop calls: a call whose capture launches the same programs over the same
+// wiring (the same persistent buffers, outputs and values in every argument)
+// reuses it instead of grouping, rendering and loading the step's batch
+// kernels again on its first replay (0.23 ms per C4 call). The entry holds
+// the step's plans, so the program pointers it compares stay valid; buffers
+// are compared by address only (equal addresses give the same aliasing, so
+// the same launch decisions). Never freed: it may hold programs of a device
+// the process tears down at exit.
+struct CaptureReuse {
+  const Device* dev = nullptr;
+  std::vector<std::shared_ptr<CachedPlan>> plans;
+  std::vector<uint64_t> shape;
+  std::shared_ptr<void> device_state;
+};
+
+CaptureReuse& capture_reuse() {
+  static CaptureReuse* r = new CaptureReuse();
+  return *r;
+}
+
+std::vector<uint64_t> capture_shape(const CapturedStep& cap) {
+  std::vector<uint64_t> v{cap.kernels.size(), cap.result_kernel};
+  auto ptr = [](const void* p) { return static_cast<uint64_t>(reinterpret_cast<uintptr_t>(p)); };
+  for (const CapturedStep::Kernel& k : cap.kernels) {
+    v.push_back(ptr(k.prog));
+    v.push_back(k.has_output);
+    v.push_back(k.out_numel);
+    v.push_back((static_cast<uint64_t>(k.out_dtype.kind) << 16) | k.out_dtype.vcount);
+    v.push_back(k.args.size());
+    for (const CapturedStep::Arg& a : k.args) {
+      v.push_back(a.kind);
+      if (a.kind == CapturedStep::Arg::Persistent) {
+        v.push_back(ptr(a.buf.get()));
+      } else if (a.kind == CapturedStep::Arg::Output) {
+        v.push_back(a.out);
+      } else if (a.kind == CapturedStep::Arg::Value) {
+        const KernelArg& x = a.value;
+        v.push_back(static_cast<uint64_t>(x.kind));
+        uint32_t fbits = 0;
+        std::memcpy(&fbits, &x.f, sizeof(fbits));
+        v.push_back(x.kind == KernelArg::Kind::Buffer ? ptr(x.buffer.get())
+                    : x.kind == KernelArg::Kind::F32  ? fbits
+                    : x.kind == KernelArg::Kind::Bool ? static_cast<uint64_t>(x.b)
+                                                      : static_cast<uint64_t>(static_cast<uint32_t>(x.i)));
+      }
+    }
+  }
+  return v;
+}
+
 // Launches every kernel of a captured step as one sequence (a single HIP
 // graph from its second run on), with the step's result (the loss) read back
 // into `slot` (Device::read_async) behind it.
@@ -1475,8 +1526,12 @@ std::vector<float> train_steps(const std::vector<const Linear*>& layers, const S
       Buffer lb = loss.realized_buffer();
       dev.read_async(lb, slot(i));  // the loss's read-back, queued behind the step
       if (capture && !cap) {
-        if (rec.valid && prev_valid && (cap = capture_step(prev, rec.records, lb, start_of(i - 1), start_of(i))))
+        if (rec.valid && prev_valid && (cap = capture_step(prev, rec.records, lb, start_of(i - 1), start_of(i)))) {
           realize_stats().steps_captured++;
+          CaptureReuse& reuse = capture_reuse();
+          if (reuse.dev == &dev && reuse.device_state && reuse.shape == capture_shape(*cap))
+            cap->device_state = reuse.device_state;
+        }
         prev = cap ? std::vector<ReplayRecord>() : std::move(rec.records);
         prev_valid = !cap && rec.valid;
       }
@@ -1485,6 +1540,13 @@ std::vector<float> train_steps(const std::vector<const Linear*>& layers, const S
   }
   loop.end();
   for (int i = std::max(0, steps - (in_flight - 1)); i < steps; i++) collect(i);
+  if (cap && cap->device_state) {
+    CaptureReuse& reuse = capture_reuse();
+    reuse.dev = &dev;
+    reuse.plans = cap->plans;
+    reuse.shape = capture_shape(*cap);
+    reuse.device_state = cap->device_state;
+  }
   return losses;
 }
 
