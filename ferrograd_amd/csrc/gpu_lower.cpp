@@ -1475,9 +1475,11 @@ int64_t gemm_tile_residency(const GemmTile& t) {
 //   up to about two workgroups per CU: the 8192x10 (K 4096) forward took 59 us
 //   with BK 32 and 8 splits, 45 with BK 16 and 16 splits.
 // - K of at most 32: the kernel is one pass over its output and epilogue
-//   operands. 64x64 tiles put many workgroups' loads and stores in flight:
-//   8192x4096 with K 10 took 91 us with 256x256 tiles, 54 with 128x128, 50 with
-//   64x64.
+//   operands. Small tiles put many workgroups' loads and stores in flight:
+//   8192x4096 with K 10 (C5's dH2, relu mask) took 91 us with 256x256 tiles, 54
+//   with 128x128, 50 with 64x64; in a later same-box run 53.5 with 64x64 (four
+//   waves), 51.5 with 32x64 (two), 52-53 with 128x64, 58 with 64x128 and 32x32,
+//   65 with 64x32.
 // FG_GEMM_TILE="BM,BN,BK,WGM,WGN,S[,NBUF]" fixes the tile, split count (0:
 // stream-K over the chip's CUs) and LDS stage count (2 or 3) of every
 // GEMM in the process: a tuning override for measuring alternatives to the
@@ -1571,7 +1573,7 @@ GemmTile choose_gemm_tile(int64_t M, int64_t N, int64_t K) {
     const int64_t nt = tiles(t);
     return with_splits(t, std::max<int64_t>(1, std::min(smax, (2 * kComputeUnits + nt - 1) / nt)));
   }
-  if (K <= 32) return with_splits(GemmTile{64, 64, K <= 16 ? 16 : 32, 2, 2}, 1);
+  if (K <= 32) return with_splits(GemmTile{32, 64, K <= 16 ? 16 : 32, 1, 2}, 1);
   constexpr double kCuFlops = 157.3e12 / kComputeUnits;  // fp32 MFMA peak per CU
   constexpr double kHbmBytes = 5.0e12;                   // sustained HBM rate for split partials
   struct Cand {
