@@ -1931,7 +1931,16 @@ std::string gemm_three_stages(std::string src) {
 // storing each segment's partial sums as a split-K workgroup would. Shares
 // differ by at most one k-tile, so no CU is left without work when the tiles
 // do not divide into rounds.
-std::string gemm_stream_k(std::string src) {
+//
+// Tile order (D > 0): with equal shares, workgroups P apart (P the smallest
+// multiple of the 8 XCDs with P * share a whole number of tiles' k-tiles)
+// start at the same k position D = P * share / KTT tiles apart, and
+// round-robin dispatch puts them on one XCD. Block index c + D*j is numbered
+// c * NTILES/D + j in row-major order (column blocks fastest), so the tiles
+// that one XCD's workgroups run at the same k are a few row blocks by every
+// column block, and share their operand rows in that XCD's L2. D = 0 keeps
+// the grouped order.
+std::string gemm_stream_k(std::string src, int64_t D) {
   const std::string from = R"(  int bid = blockIdx.x;
   // Blocks are dispatched round-robin over the 8 XCDs; give each XCD a
   // contiguous run of (split, tile) pairs so neighbouring tiles of one K
@@ -1947,7 +1956,8 @@ std::string gemm_stream_k(std::string src) {
 )";
   const std::string to = R"(  // Shares in launch order, so consecutive shares (neighbouring k-ranges
   // of one tile) run on different XCDs. Gathering them on one XCD fetched
-  // 1028 against 800 MB from beyond L2 for C5's dW1 and was no faster.
+  // 1028 MB from beyond L2 for C5's dW1 (800 in launch order with the
+  // grouped tile order) and was no faster.
   const int wv = blockIdx.x;
   const long it_end = (long)(wv + 1) * ITERS_ / G_;
   for (long it = (long)wv * ITERS_ / G_; it < it_end;) {
@@ -1962,7 +1972,35 @@ std::string gemm_stream_k(std::string src) {
   FG_CHECK(p != std::string::npos && src.find(from, p + 1) == std::string::npos,
            "stream-K GEMM: generated text not found once");
   src.replace(p, from.size(), to);
+  if (D > 0) {
+    const std::string grouped = R"(  const int GM = 8;
+  const int group = bid / (GM * nbn), first_m = group * GM;
+  const int gsz = (nbm - first_m) < GM ? (nbm - first_m) : GM;
+  const int tm = first_m + (bid % (GM * nbn)) % gsz, tn = (bid % (GM * nbn)) / gsz;
+)";
+    const std::string by_xcd = R"(  const int sq = (bid % SK_D_) * (NTILES_ / SK_D_) + bid / SK_D_;  // the block's row-major slot
+  const int tm = sq / nbn, tn = sq % nbn;
+)";
+    const size_t q = src.find(grouped);
+    FG_CHECK(q != std::string::npos && src.find(grouped, q + 1) == std::string::npos,
+             "stream-K GEMM: tile order text not found once");
+    src.replace(q, grouped.size(), by_xcd);
+  }
   return src;
+}
+
+// The stream-K tile order's D (see gemm_stream_k), or 0 when the shares are
+// unequal or no such period divides the tiles.
+int64_t stream_k_tile_period(int64_t ntiles, int64_t kt, int64_t G) {
+  const int64_t iters = ntiles * kt;
+  if (iters % G != 0) return 0;
+  const int64_t share = iters / G;
+  for (int64_t P = 8; P <= G; P += 8)
+    if ((P * share) % kt == 0) {
+      const int64_t D = P * share / kt;
+      return ntiles % D == 0 ? D : 0;
+    }
+  return 0;
 }
 
 RenderedKernel render_gemm(const KernelInfo& ki, const GemmMatch& g, const std::string& name) {
@@ -1978,6 +2016,7 @@ RenderedKernel render_gemm(const KernelInfo& ki, const GemmMatch& g, const std::
   FG_CHECK(tile.nbuf == 2 || (tile.nbuf == 3 && (BK / 8) % 2 == 0), "three GEMM stages need an even number of 8-k groups");
   const bool split = S > 1 || tile.stream_k;  // partials in scratch, summed by _fin
   const int64_t KTT = (K + BK - 1) / BK;       // k-tiles per tile
+  const int64_t sk_D = tile.stream_k ? stream_k_tile_period(ntiles, KTT, tile.G) : 0;
   const std::string scratch_param = split ? ", float* __restrict__ fg_scratch" : "";
   const int waves_per_eu = static_cast<int>(std::max<int64_t>(1, gemm_tile_residency(tile) * NT / 256));
   auto sig = [&](const std::string& fn, int block, bool main) {
@@ -2034,6 +2073,7 @@ RenderedKernel render_gemm(const KernelInfo& ki, const GemmMatch& g, const std::
   s << "#define NV_ " << NV << "\n#define ND_ " << ND << "\n#define NW_ " << NW << "\n";
   if (tile.stream_k) {
     s << "#define G_ " << tile.G << "\n#define KTT_ " << KTT << "\n#define ITERS_ " << ntiles * KTT << "L\n";
+    if (sk_D > 0) s << "#define SK_D_ " << sk_D << "\n";
     s << "// Stream-K: the workgroup that runs (tile, k-tile) iteration x.\n"
          "__device__ __forceinline__ int fg_sk_owner(long x) { return (int)(((x + 1) * G_ - 1) / ITERS_); }\n";
   }
@@ -2431,7 +2471,14 @@ RenderedKernel render_gemm(const KernelInfo& ki, const GemmMatch& g, const std::
   const int grow = (int)(gid / (NP_ / 4)), gcol = (int)(gid % (NP_ / 4)) * 4;
   fg_f4 gv = *(const fg_f4*)(fg_scratch + (long)grow * NP_ + gcol);
 )";
-    if (tile.stream_k) {
+    if (tile.stream_k && sk_D > 0) {
+      // The tile's block index (the inverse of the main pass's row-major
+      // slot), then how many workgroups its k-tiles were split over.
+      s << R"(  const int nbn = (N_ + BN - 1) / BN, sq = (grow / BM) * nbn + gcol / BN;
+  const long t0 = (long)((sq % (NTILES_ / SK_D_)) * SK_D_ + sq / (NTILES_ / SK_D_)) * KTT_;
+  const int nseg = fg_sk_owner(t0 + KTT_ - 1) - fg_sk_owner(t0) + 1;
+  for (int ks = 1; ks < nseg; ks++) {)";
+    } else if (tile.stream_k) {
       // The tile's block index (the inverse of the main pass's grouped
       // order), then how many workgroups its k-tiles were split over.
       s << R"(  const int nbm = (M_ + BM - 1) / BM, nbn = (N_ + BN - 1) / BN, GM = 8;
@@ -2459,7 +2506,7 @@ RenderedKernel render_gemm(const KernelInfo& ki, const GemmMatch& g, const std::
   if (tile.nbuf == 3) rk.source = gemm_three_stages(rk.source);
   rk.block[0] = static_cast<unsigned>(NT);
   rk.grid[0] = static_cast<unsigned>(tile.stream_k ? tile.G : ntiles * S);
-  if (tile.stream_k) rk.source = gemm_stream_k(rk.source);
+  if (tile.stream_k) rk.source = gemm_stream_k(rk.source, sk_D);
   if (split) {
     LaunchSpec a, b;
     a.func = name + "_part";

@@ -56,6 +56,43 @@ def test_tile_model_gives_160_wide_tiles(fg, cpu, shape):
         assert gemm_tile(fg, p[name]) == tile, name
 
 
+def _c_expr(text, env):
+    """Evaluates one of the kernel's integer expressions (non-negative
+    operands, so C's division is Python's floor division)."""
+    return eval(text.replace("(long)", "").replace("/", "//"), {}, dict(env))
+
+
+def test_stream_k_tile_order_groups_each_xcds_tiles(fg, cpu):
+    # C5's dW1 (4096x784, K 8192): 80 tiles of 256x160, 256 k-tiles each, on
+    # 256 workgroups of 80 k-tiles. Workgroups 16 apart start at the same k
+    # position 5 tiles apart, and round-robin dispatch puts workgroups 8 apart
+    # on one XCD. The kernel's own expressions, evaluated here: the row-major
+    # slot is a bijection, the second pass inverts it, and the 16 tiles that
+    # one XCD's workgroups start at one k position cover at most 4 of the 16
+    # row blocks (the grouped order gave 16 distinct ones: no shared rows).
+    B, fi, fo = 8192, 784, 4096
+    ones = np.ones
+    p = products(fg, cpu, ones((B, fi), np.float32), ones((fo, fi), np.float32), ones((B, fo), np.float32))
+    (src,) = [it["source"] for it in fg.debug_plan([p["dw"]], fuse=True, render_hip=True)["items"]
+              if it["class"] == "gemm_mfma_f32"]
+    d = {k: int(v) for k, v in re.findall(r"#define (\w+) (\d+)L?\n", src)}
+    assert (d["NTILES_"], d["KTT_"], d["G_"], d["SK_D_"]) == (80, 256, 256, 5)
+    slot = re.search(r"const int sq = (.+?);", src).group(1)
+    inv = re.search(r"const long t0 = \(long\)(.+?) \* KTT_;", src).group(1)
+    nbn = (fi + d["BN"] - 1) // d["BN"]
+    fwd = [_c_expr(slot, {**d, "bid": b}) for b in range(d["NTILES_"])]
+    assert sorted(fwd) == list(range(d["NTILES_"]))
+    assert all(_c_expr(inv, {**d, "sq": q}) == b for b, q in enumerate(fwd))
+    share = d["NTILES_"] * d["KTT_"] // d["G_"]
+    for x in range(8):
+        starts = {}
+        for w in range(x, d["G_"], 8):
+            tile, k0 = divmod(w * share, d["KTT_"])
+            starts.setdefault(k0, []).append(fwd[tile] // nbn)
+        for rows in starts.values():
+            assert len(rows) == 16 and len(set(rows)) <= 4, rows
+
+
 @pytest.mark.gpu
 @pytest.mark.parametrize("shape", sorted(CASES))
 def test_160_wide_tiles_against_float64(fg, hip, shape):
